@@ -1,0 +1,177 @@
+"""Benchmark of the MI355X weight-only quantized matmul path (one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+A step is one call of the decode GEMV of BASELINE config 0 (W4A16, M=1, K=5120, N=17408, g128 fp16 scales,
+bf16 output) on seeded synthetic inputs already resident in HBM. The weights rotate over 8 copies (368 MB,
+more than the 256 MB Infinity Cache) so every call streams its weights from HBM. `value` = algorithmic bytes
+(N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 = 46,002,176 B per call) * K / the elapsed time of the K timed steps.
+`roofline.achieved` uses the kernel's own average duration (HIP events around each launch on the launch
+stream). The prefill GEMM (config 2) and the other configs are reported beside it in `secondary`.
+The CPU baseline is the oracle's dequantize + fp32 matmul of the same workload on the host cores.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-secondary", action="store_true", help="only the headline GEMV")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def gemv_bytes(m, n, k):
+    return n * k // 2 + n * (k // 128) * 2 + m * k * 2 + m * n * 2
+
+
+def read_traffic(name):
+    """HBM bytes per launch measured by rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE (profiles/<name>): the line
+    'hbm_bytes_per_launch: <int>' of the committed summary, else None"""
+    p = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(p):
+        return None
+    for line in open(p):
+        if line.startswith("hbm_bytes_per_launch:"):
+            return int(line.split(":")[1].strip())
+    return None
+
+
+def time_launches(fn, steps, warmup, nvar):
+    """fn(i) launches step i on the current stream. Returns (elapsed ms of the `steps` timed steps bracketed by
+    synchronize, mean per-launch ms from events recorded around each launch)."""
+    import torch
+    st = torch.cuda.current_stream()
+    for i in range(warmup):
+        fn(i % nvar)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        fn(i % nvar)
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for i in range(steps):
+        ev[i][0].record(st)
+        fn(i % nvar)
+        ev[i][1].record(st)
+    torch.cuda.synchronize()
+    per = sorted(a.elapsed_time(b) for a, b in ev)
+    mean = sum(per) / len(per)
+    return wall_ms, mean, per[len(per) // 2]
+
+
+def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None):
+    import torch
+    from qengine_amd import ops, synth
+    steps = steps or args.steps
+    warmup = warmup or args.warmup
+    ws = []
+    for c in range(args.copies):
+        q, s = synth.w4_dev(n, k, seed=100 + c)
+        ws.append(ops.repack_w4(q, s))
+        del q, s
+    x = synth.x_dev(m, k, seed=1)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    fn = lambda i: ops.gemv_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    wall_ms, ev_ms, med_ms = time_launches(fn, steps, warmup, len(ws))
+    b = gemv_bytes(m, n, k)
+    res = dict(m=m, n=n, k=k, bytes=b, ms_per_step=wall_ms / steps, kernel_ms_mean=ev_ms, kernel_ms_median=med_ms,
+               gbs_wall=b * steps / (wall_ms * 1e-3) / 1e9, gbs_kernel=b / (ev_ms * 1e-3) / 1e9)
+    del ws
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(args, m=1, n=17408, k=5120):
+    """oracle dequant (bf16_rn((u-8)*s)) + fp32 matmul, same workload shape, host cores, ~cpu_seconds of work"""
+    import numpy as np
+    import oracle
+    from qengine_amd import synth
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, 16)
+    os.environ["OMP_NUM_THREADS"] = str(cores)
+    q, s = synth.w4_host(n, k, seed=100, sdt=1)
+    x = synth.x_host(m, k, seed=1)
+    reps, t_deq, t_mm = 0, 0.0, 0.0
+    t_start = time.perf_counter()
+    while reps == 0 or time.perf_counter() - t_start < args.cpu_seconds:
+        t0 = time.perf_counter()
+        wdq = oracle.dequant_w4(q, s, n, k, 1)
+        t1 = time.perf_counter()
+        oracle.matmul_bf16(x, wdq, nthreads=cores)
+        t2 = time.perf_counter()
+        t_deq += t1 - t0
+        t_mm += t2 - t1
+        reps += 1
+    per = (t_deq + t_mm) / reps
+    return {"value": round(gemv_bytes(m, n, k) / per / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{reps} full calls of config 0 (M=1 K=5120 N=17408): oracle dequant_w4 + matmul_bf16 "
+                      f"(C, OpenMP {cores} threads); dequant {t_deq / reps * 1e3:.1f} ms + matmul "
+                      f"{t_mm / reps * 1e3:.1f} ms per call"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: every box of this build has one MI355X and the path has no "
+              f"collectives (--gpus {args.gpus} is not supported)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from qengine_amd import call
+    torch.cuda.set_device(0)
+    call("qe_gemv_workspace_init")
+
+    g = bench_gemv(args)
+    secondary = {}
+    if not args.no_secondary:
+        for (m, n) in [(2, 5120), (4, 5120), (8, 5120), (16, 5120), (2, 17408), (4, 17408), (8, 17408), (16, 17408)]:
+            r = bench_gemv(args, m=m, n=n, steps=200, warmup=20)
+            secondary[f"skinny_m{m}_n{n}"] = {"gbs_kernel": round(r["gbs_kernel"], 1),
+                                              "pct_hbm": round(100 * r["gbs_kernel"] / HBM_PEAK_GBS, 1),
+                                              "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2)}
+    cpu = None if args.no_cpu else cpu_baseline(args)
+    achieved = g["gbs_kernel"]
+    out = {
+        "metric": "W4A16 GEMV GB/s (% HBM peak) at M=1, K=5120, N=17408",
+        "value": round(g["gbs_wall"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(g["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "w4a16 (int4 g128 weights, bf16 x, fp32 accumulate, bf16 out)",
+        "data": "synthetic (seeded: uniform nibbles, fp16 scales |N(0,1)|*0.02, x bf16 N(0,1))",
+        "config": {"workload": "BASELINE config 0: W4A16 decode GEMV", "m": 1, "k": 5120, "n": 17408,
+                   "group": 128, "scales": "fp16", "out": "bf16", "weight_copies": args.copies,
+                   "bytes_per_call": g["bytes"]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic("gemv_w4_c0_m1_traffic.txt"),
+                     "kernel_us_mean": round(g["kernel_ms_mean"] * 1e3, 3),
+                     "kernel_us_median": round(g["kernel_ms_median"] * 1e3, 3)},
+        "cpu_baseline": cpu,
+        "secondary": secondary,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,114 @@
+/* qe_kernels.h - C-ABI of libqe_kernels.so, the MI355X (gfx950) weight-only quantized matmul path.
+ *
+ * Every pointer argument is a DEVICE pointer unless stated; `stream` is a hipStream_t (NULL = default
+ * stream). 16-bit floats cross the ABI as raw uint16_t bit patterns. A violated shape precondition prints
+ * "check failed ..." to stderr and aborts (the reference's convention, src/common.h:27-36); the one
+ * exception is qe_skinny_w4, which returns 0 for an unsupported shape (reference src/capi.cpp:79-83).
+ *
+ * Weight layouts are the reference's (src/kernels/gemv.cuh:7-16,33-40):
+ *   W4 q: [N/16][K/64][32 lanes][4 x u32] repacked nibbles (u = w + 8), s: [N/16][K/128][16] 16-bit scales
+ *   W8 q: [N/16][K/32][32 lanes][16 bytes] int8; s: group 128 -> [N/16][K/128][16]; per channel -> [N]
+ * Preconditions: n % 16 == 0, k % 128 == 0, x rows 4-byte aligned with an even stride.
+ */
+#ifndef QE_KERNELS_H
+#define QE_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QE_ABI_VERSION 1
+
+/* flags of the *_ex entry points */
+#define QE_SCALE_F16 1      /* scales are fp16 (default bf16) */
+#define QE_OUT_BF16 2       /* y is bf16 (round to nearest even), default fp32 */
+#define QE_GLU 4            /* GLU matrix (8 gate + 8 up rows per tile): y = bf16 silu(gate) * up, n / 2 cols */
+#define QE_W8_PER_CHANNEL 8 /* W8 with one scale per output row, s = [N] (group = K) */
+
+int qe_abi_version(void);
+
+/* ---- reference-named hooks (src/capi.cpp): bf16 scales, fp32 outputs, default stream ---- */
+
+/* Library workspaces of the current device (split-K partials + counters); call once per device before any
+ * graph capture. Replaces gemv_workspace_init, reference src/capi.cpp:131 / gemv.cuh:51. */
+void qe_gemv_workspace_init(void);
+
+/* compressed-tensors int32 [n][k/8] (nibbles LSB first, u = w + 8) + scales [n][k/128] -> W4 layout
+ * (dq: n*k/2 bytes, ds: n*k/128 16-bit). Replaces reference src/capi.cpp:13 (repack_w4, gemv.cu:1686-1694). */
+void qe_repack_w4(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds);
+
+/* y[m][n] (fp32, stride n) = x[m][k] (bf16, stride k) . W^T; m = 1..32 (GEMV for m <= 16 per launch, larger m
+ * in row blocks). Replaces reference src/capi.cpp:47 (gemv_w4, gemv.cu:1585). */
+void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m);
+
+/* as qe_gemv_w4; glu != 0: y is the bf16 activation [m][n/2] = bf16(silu(gate) * up).
+ * Replaces reference src/capi.cpp:52. */
+void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);
+
+/* skinny GEMM, bit-identical to qe_gemv_w4g for every row count; returns 0 when the shape is unsupported
+ * (m outside 1..16), 1 when it ran. Replaces reference src/capi.cpp:79 (skinny_w4, skinny.cu). */
+int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);
+
+/* qe_gemv_w4 on an explicit stream. Replaces reference src/capi.cpp:101. */
+void qe_gemv_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, void* stream);
+
+/* prefill GEMM: c[t][n] (fp32, or bf16 after qe_gemm_set_out_bf16(1)) = x[t][k] . W^T.
+ * Replaces reference src/capi.cpp:84 (gemm_w4, gemm.cu:4361). */
+void qe_gemm_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t);
+/* the tuned entry of the reference (src/capi.cpp:116); same kernel selection as qe_gemm_w4 here */
+void qe_gemm_w4_t(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t);
+/* qe_gemm_w4 on an explicit stream. Replaces reference src/capi.cpp:97. */
+void qe_gemm_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, void* stream);
+/* on != 0: later non-GLU GEMM calls write bf16 (round to nearest even) into y viewed as bf16 [t][n].
+ * Replaces reference src/capi.cpp:114 (gemm_set_out_bf16, gemm.cu:4363-4375). */
+void qe_gemm_set_out_bf16(int on);
+
+/* RTN INT8 group-128 quantization of a row-major bf16 [n][k] into the W8 layout: scale = bf16(amax/127),
+ * q = clamp(rint(v/scale), -127, 127). Replaces reference src/capi.cpp:124 (quantize_w8, gemv.cu:1085-1116). */
+void qe_quantize_w8(const uint16_t* w, int n, int k, void* dq, void* ds);
+
+/* W8 (group 128, bf16 scales) GEMV, y fp32 [m][n], m = 1..64. Replaces reference src/capi.cpp:127. */
+void qe_gemv_w8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m);
+
+/* gate/up row interleave into the GLU tile order (8 gate rows, 8 up rows per tile) of a compressed-tensors
+ * matrix, bits 4 (int32 [n][k/8]) or 8 (int32 [n][k/4]). Replaces reference src/capi.cpp:24 (qe_glu_rows8) and
+ * glu_interleave_rows (gemv.cu:1371-1375) for both widths. */
+void qe_glu_rows(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq, uint16_t* ds, int bits);
+
+/* ---- build-defined entry points (no reference counterpart; BASELINE workloads: fp16 scales, bf16 out) ---- */
+
+/* W4 -> bf16 row-major [n][k], d = bf16_rn((u - 8) * s) (the reference's dequantized weight, gemv.cu:25-36,
+ * gemm.cu:68-77, tests/test_gemv.py:36). flags: QE_SCALE_F16. */
+void qe_dequant_w4(const void* q, const void* s, int n, int k, int flags, uint16_t* out, void* stream);
+
+/* decode GEMV / skinny GEMM, m = 1..16, x rows of stride ldx, y rows of stride ldy.
+ * flags: QE_SCALE_F16 | QE_OUT_BF16 | QE_GLU. Deterministic; bit-identical across m for a given matrix. */
+void qe_gemv_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                   int flags, void* stream);
+
+/* prefill GEMM (bf16 MFMA), any t >= 1. flags: QE_SCALE_F16 | QE_OUT_BF16 | QE_GLU. */
+void qe_gemm_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                   int flags, void* stream);
+
+/* GEMV for m <= 32 (row blocks of 16), GEMM above: the reference's matmul() dispatch (gemv.cuh:187-190). */
+void qe_matmul_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                     int flags, void* stream);
+
+/* row-major int8 [n][k] + scales -> W8 layout; per_channel: s is [n] (copied), else [n][k/128] */
+void qe_tile_w8(const int8_t* w, const uint16_t* s, int n, int k, int per_channel, void* dq, void* ds, void* stream);
+
+/* W8 -> bf16 row-major [n][k], d = bf16_rn(w * s). flags: QE_SCALE_F16 | QE_W8_PER_CHANNEL. */
+void qe_dequant_w8(const void* q, const void* s, int n, int k, int flags, uint16_t* out, void* stream);
+
+/* INT8 W8A16 GEMV (m = 1..16) / GEMM (any t). flags: QE_SCALE_F16 | QE_OUT_BF16 | QE_W8_PER_CHANNEL. */
+void qe_gemv_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                   int flags, void* stream);
+void qe_gemm_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                   int flags, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

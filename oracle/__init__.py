@@ -1,0 +1,200 @@
+"""CPU oracle of the weight-only quantized matmul path: numpy wrappers over liboracle.so (qe_oracle.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, as the
+checker and the CPU baseline. The product (qengine_amd, include/) never imports, links or calls it.
+
+Parity pins (each function is checked against something other than itself in tests/test_oracle.py):
+  f32_to_bf16 / bf16_to_f32 / f16_to_f32  torch's dtype conversions (independent RNE / IEEE implementations)
+  unpack_w4         the reference's torch unpack expression (tests/test_gemv.py:13-15) restated in numpy
+  repack_w4         round trip through an independent decoder written from the PTX ISA m16n8k16 A-fragment
+                    layout + the reference's nibble pairing (gemv.cu:25-36), bijection, known answers
+  dequant_w4        closed form bf16_rn((u - 8) * s) in numpy/torch (tests/test_gemv.py:36)
+  matmul_bf16       numpy float64 matmul (|err| bound), brute force on tiny shapes
+  glu_rows / glu    the reference's interleave closed form (tests/test_q8.py:75-79 interleave_ref) + torch silu
+  quantize_w8       the reference's torch closed form (tests/test_w8.py:6-9)
+  w8_pos / tile_w8  bijection + inverse map of src/tools/qe_w8q.cu:34-45 + A-fragment decoder
+  moe_route         brute force sort with the tie rule (numpy lexsort) + softmax renormalisation
+  moe_segment       invariants (counts, contiguity, every pair once, stable order) + numpy argsort(stable)
+"""
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+_LIBPATH = os.path.join(HERE, "liboracle.so")
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", HERE, "-B", "liboracle.so"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIBPATH):
+            build()
+        _lib = ctypes.CDLL(_LIBPATH)
+        f = _lib
+        f.or_f32_to_bf16.restype = ctypes.c_uint16
+        f.or_f32_to_bf16.argtypes = [ctypes.c_float]
+        f.or_bf16_to_f32.restype = ctypes.c_float
+        f.or_bf16_to_f32.argtypes = [ctypes.c_uint16]
+        f.or_f16_to_f32.restype = ctypes.c_float
+        f.or_f16_to_f32.argtypes = [ctypes.c_uint16]
+        f.or_w8_pos.restype = ctypes.c_size_t
+        f.or_w8_pos.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        f.or_silu_mul.restype = ctypes.c_float
+        f.or_silu_mul.argtypes = [ctypes.c_float, ctypes.c_float]
+    return _lib
+
+
+def _p(a):
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _c(a, dtype):
+    a = np.ascontiguousarray(a, dtype=dtype)
+    return a
+
+
+# ---------------------------------------------------------------- 16-bit floats
+def f32_to_bf16(a):
+    """float32 array -> bf16 bit patterns (uint16), round to nearest even."""
+    a = _c(a, np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def f16_to_f32(h):
+    return np.asarray(h, dtype=np.uint16).view(np.float16).astype(np.float32)
+
+
+def scale_to_f32(s, sdt):
+    return f16_to_f32(s) if sdt else bf16_to_f32(s)
+
+
+# ---------------------------------------------------------------- W4
+def unpack_w4(q, n, k):
+    """int32 [n][k/8] -> int8 w = u - 8, [n][k]"""
+    q = _c(q, np.int32).reshape(n, k // 8)
+    w = np.empty((n, k), np.int8)
+    lib().or_unpack_w4(_p(q), n, k, _p(w))
+    return w
+
+
+def repack_w4(q, s, n, k):
+    """compressed-tensors (q int32 [n][k/8], s uint16 [n][k/128]) -> W4 layout (uint32 [n*k/8], uint16 [n*k/128])"""
+    q = _c(q, np.int32)
+    s = _c(s, np.uint16)
+    dq = np.empty(n * k // 8, np.uint32)
+    ds = np.empty(n * (k // 128), np.uint16)
+    lib().or_repack_w4(_p(q), _p(s), n, k, _p(dq), _p(ds))
+    return dq, ds
+
+
+def dequant_w4(q, s, n, k, sdt):
+    """-> bf16 bits [n][k] of bf16_rn((u - 8) * s)"""
+    q = _c(q, np.int32)
+    s = _c(s, np.uint16)
+    out = np.empty((n, k), np.uint16)
+    lib().or_dequant_w4(_p(q), _p(s), n, k, int(sdt), _p(out))
+    return out
+
+
+def glu_rows(q, s, n, k, bits=4):
+    q = _c(q, np.int32)
+    s = _c(s, np.uint16)
+    wpr = k * bits // 32
+    dq = np.empty((n, wpr), np.int32)
+    ds = np.empty((n, k // 128), np.uint16)
+    lib().or_glu_rows(_p(q), _p(s), n, k, wpr, _p(dq), _p(ds))
+    return dq, ds
+
+
+# ---------------------------------------------------------------- matmul
+def matmul_bf16(x, w, nthreads=0):
+    """x bf16 bits [m][k], w bf16 bits [n][k] -> fp32 [m][n] (fp32 accumulation)"""
+    x = _c(x, np.uint16)
+    w = _c(w, np.uint16)
+    m, k = x.shape
+    n = w.shape[0]
+    y = np.empty((m, n), np.float32)
+    lib().or_matmul_bf16(_p(x), _p(w), m, n, k, _p(y), int(nthreads))
+    return y
+
+
+def glu_epilogue(y):
+    """fp32 [m][n] product of a GLU-interleaved matrix -> bf16 bits [m][n/2]"""
+    y = _c(y, np.float32)
+    m, n = y.shape
+    act = np.empty((m, n // 2), np.uint16)
+    lib().or_glu_epilogue(_p(y), m, n, _p(act))
+    return act
+
+
+# ---------------------------------------------------------------- W8
+def quantize_w8(w, n, k):
+    """bf16 bits [n][k] -> (int8 [n][k], bf16 scales [n][k/128])"""
+    w = _c(w, np.uint16)
+    q = np.empty((n, k), np.int8)
+    s = np.empty((n, k // 128), np.uint16)
+    lib().or_quantize_w8(_p(w), n, k, _p(q), _p(s))
+    return q, s
+
+
+def w8_pos(row, c, k):
+    return lib().or_w8_pos(row, c, k)
+
+
+def tile_w8(q, s, n, k, per_channel):
+    q = _c(q, np.int8)
+    s = _c(s, np.uint16)
+    dq = np.empty(n * k, np.uint8)
+    ds = np.empty(n if per_channel else n * (k // 128), np.uint16)
+    lib().or_tile_w8(_p(q), _p(s), n, k, int(per_channel), _p(dq), _p(ds))
+    return dq, ds
+
+
+def dequant_w8(q, s, n, k, per_channel, sdt):
+    q = _c(q, np.int8)
+    s = _c(s, np.uint16)
+    out = np.empty((n, k), np.uint16)
+    lib().or_dequant_w8(_p(q), _p(s), n, k, int(per_channel), int(sdt), _p(out))
+    return out
+
+
+# ---------------------------------------------------------------- MoE
+def moe_route(logits, topk):
+    logits = _c(logits, np.float32)
+    T, E = logits.shape
+    sel = np.empty((T, topk), np.int32)
+    w = np.empty((T, topk), np.float32)
+    lib().or_moe_route(_p(logits), T, E, topk, _p(sel), _p(w))
+    return sel, w
+
+
+def moe_segment(sel, E):
+    sel = _c(sel, np.int32)
+    T, topk = sel.shape
+    cnt = np.empty(E, np.int32)
+    off = np.empty(E + 1, np.int32)
+    lst = np.empty(T * topk, np.int32)
+    inv = np.empty(T * topk, np.int32)
+    lib().or_moe_segment(_p(sel), T, E, topk, _p(cnt), _p(off), _p(lst), _p(inv))
+    return cnt, off, lst, inv
+
+
+def silu_mul(a, b):
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    return (a / (np.float32(1) + np.exp(-a)) * b).astype(np.float32)

@@ -1,0 +1,164 @@
+// extern "C" entry points of libqe_kernels.so (declared in include/qe_kernels.h).
+// Reference-named hooks keep the reference's signatures and semantics (src/capi.cpp:10-171): device
+// pointers, default stream, bf16 scales, fp32 outputs, fatal abort on a violated precondition.
+// Build-defined *_ex entry points take an explicit stream, row strides and flags (QeFlags).
+#include "qe_api.hpp"
+#include "../../include/qe_kernels.h"
+
+#include <atomic>
+
+[[noreturn]] void qe_fatal_check() {
+    fflush(stdout);
+    fflush(stderr);
+    abort();
+}
+
+[[noreturn]] void qe_fatal_hip(hipError_t err, const char* what, const char* file, int line) {
+    fprintf(stderr, "HIP error %d (%s) in %s at %s:%d\n", (int)err, hipGetErrorString(err), what, file, line);
+    qe_fatal_check();
+}
+
+namespace {
+std::atomic<int> g_out_bf16{0};
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline W4 mk_w4(const void* q, const void* s, int n, int k, bool glu, int sdt) {
+    W4 w;
+    w.q = reinterpret_cast<const uint4*>(q);
+    w.s = reinterpret_cast<const uint16_t*>(s);
+    w.n = n;
+    w.k = k;
+    w.glu = glu;
+    w.sdt = sdt;
+    return w;
+}
+inline W8 mk_w8(const void* q, const void* s, int n, int k, bool per_channel, int sdt) {
+    W8 w;
+    w.q = reinterpret_cast<const uint4*>(q);
+    w.s = reinterpret_cast<const uint16_t*>(s);
+    w.n = n;
+    w.k = k;
+    w.per_channel = per_channel;
+    w.sdt = sdt;
+    return w;
+}
+}  // namespace
+
+void gemm_set_out_bf16(bool on) { g_out_bf16.store(on ? 1 : 0); }
+bool gemm_out_bf16() { return g_out_bf16.load() != 0; }
+
+extern "C" {
+
+int qe_abi_version(void) { return QE_ABI_VERSION; }
+
+// ---------------------------------------------------------------- reference-named hooks
+void qe_gemv_workspace_init(void) { gemv_workspace_init(); }
+
+void qe_repack_w4(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds) {
+    repack_w4(q, s, n, k, reinterpret_cast<uint4*>(dq), reinterpret_cast<uint16_t*>(ds), 0);
+}
+
+void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m) {
+    gemv_workspace_init();
+    matmul_w4(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, m, false, 0);
+}
+
+void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu) {
+    gemv_workspace_init();
+    CHECK(m >= 1 && m <= kMaxGemvW4Tokens, "qe_gemv_w4g m %d", m);
+    matmul_w4(mk_w4(q, s, n, k, glu != 0, kScaleBF16), x, k, y, glu ? n / 2 : n, m, false, 0);
+}
+
+int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu) {
+    if (m < 1 || m > kMaxGemvRows || n % 16 != 0 || k % 128 != 0) return 0;
+    gemv_workspace_init();
+    gemv_w4(mk_w4(q, s, n, k, glu != 0, kScaleBF16), x, k, y, glu ? n / 2 : n, m, false, 0);
+    return 1;
+}
+
+void qe_gemv_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, void* st) {
+    gemv_workspace_init();
+    matmul_w4(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, m, false, as_stream(st));
+}
+
+void qe_gemm_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t) {
+    gemm_w4(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, t, gemm_out_bf16(), 0);
+}
+
+void qe_gemm_w4_t(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t) {
+    gemm_w4(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, t, gemm_out_bf16(), 0);
+}
+
+void qe_gemm_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, void* st) {
+    gemm_w4(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, t, gemm_out_bf16(), as_stream(st));
+}
+
+void qe_gemm_set_out_bf16(int on) { gemm_set_out_bf16(on != 0); }
+
+void qe_quantize_w8(const uint16_t* w, int n, int k, void* dq, void* ds) {
+    quantize_w8(w, n, k, reinterpret_cast<uint4*>(dq), reinterpret_cast<uint16_t*>(ds), 0);
+}
+
+void qe_gemv_w8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m) {
+    gemv_workspace_init();
+    const W8 w = mk_w8(q, s, n, k, false, kScaleBF16);
+    for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
+        const int mm = m - r0 < kMaxGemvRows ? m - r0 : kMaxGemvRows;
+        gemv_w8(w, x + (size_t)r0 * k, k, y + (size_t)r0 * n, n, mm, false, 0);
+    }
+}
+
+void qe_glu_rows(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq, uint16_t* ds, int bits) {
+    glu_interleave_rows(q, s, n, k, dq, ds, 0, bits);
+}
+
+// ---------------------------------------------------------------- build-defined entry points
+void qe_dequant_w4(const void* q, const void* s, int n, int k, int flags, uint16_t* out, void* st) {
+    dequant_w4(mk_w4(q, s, n, k, false, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), out, as_stream(st));
+}
+
+void qe_gemv_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                   int flags, void* st) {
+    gemv_workspace_init();
+    gemv_w4(mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y,
+            ldy, m, (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+void qe_gemm_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                   int flags, void* st) {
+    gemm_w4(mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y,
+            ldy, t, (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+void qe_matmul_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                     int flags, void* st) {
+    gemv_workspace_init();
+    matmul_w4(mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y,
+              ldy, m, (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+void qe_tile_w8(const int8_t* w, const uint16_t* s, int n, int k, int per_channel, void* dq, void* ds, void* st) {
+    tile_w8(w, s, n, k, reinterpret_cast<uint4*>(dq), reinterpret_cast<uint16_t*>(ds), per_channel != 0,
+            as_stream(st));
+}
+
+void qe_dequant_w8(const void* q, const void* s, int n, int k, int flags, uint16_t* out, void* st) {
+    const bool pc = (flags & QE_W8_PER_CHANNEL) != 0;
+    dequant_w8(mk_w8(q, s, n, k, pc, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), out, as_stream(st));
+}
+
+void qe_gemv_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                   int flags, void* st) {
+    gemv_workspace_init();
+    const bool pc = (flags & QE_W8_PER_CHANNEL) != 0;
+    gemv_w8(mk_w8(q, s, n, k, pc, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y, ldy, m,
+            (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+void qe_gemm_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                   int flags, void* st) {
+    const bool pc = (flags & QE_W8_PER_CHANNEL) != 0;
+    gemm_w8(mk_w8(q, s, n, k, pc, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y, ldy, t,
+            (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+}  // extern "C"

@@ -1,0 +1,56 @@
+// C++ kernel API of qengine_amd: the MI355X counterpart of the reference's kernel header
+// (src/kernels/gemv.cuh:17-200). Same weight layouts, same argument meaning, hipStream_t instead of
+// cudaStream_t. All pointers are device pointers; the caller owns weights, activations and outputs, the
+// library owns its workspaces (qe_gemv_workspace_init, once per device before any graph capture).
+#pragma once
+#include "qe_common.hpp"
+
+// W4 layout (symmetric INT4, group 128 along K, stored nibble u = w + 8), reference gemv.cuh:12-16:
+//   q: [N/16][K/64][32 lanes][4 x u32]   s: [N/16][K/128][16] 16-bit (bf16 or fp16, `sdt`)
+// glu: each 16-row tile holds 8 gate rows then the 8 matching up rows; the output is
+// act[t][i] = bf16(silu(gate_i) * up_i) with n / 2 columns (gemv.cuh:20-22).
+struct W4 {
+    const uint4* q = nullptr;
+    const uint16_t* s = nullptr;
+    int n = 0, k = 0;
+    bool glu = false;
+    int sdt = kScaleBF16;
+};
+// W8 layout (symmetric INT8), reference gemv.cuh:33-40: q [N/16][K/32][32 lanes][16 bytes].
+// group 128 (reference): s [N/16][K/128][16] bf16. per-channel (this build): s [N] fp16 (group = K).
+struct W8 {
+    const uint4* q = nullptr;
+    const uint16_t* s = nullptr;
+    int n = 0, k = 0;
+    bool per_channel = false;
+    int sdt = kScaleBF16;
+};
+
+// ---- layouts (load time) ----
+void repack_w4(const int32_t* src_q, const uint16_t* src_s, int n, int k, uint4* dst_q, uint16_t* dst_s,
+               hipStream_t st);
+void glu_interleave_rows(const int32_t* src_q, const uint16_t* src_s, int n, int k, int32_t* dst_q,
+                         uint16_t* dst_s, hipStream_t st, int bits = 4);
+void dequant_w4(const W4& w, uint16_t* out, hipStream_t st);  // bf16 [n][k] = bf16_rn((u - 8) * s)
+void quantize_w8(const uint16_t* src, int n, int k, uint4* dst_q, uint16_t* dst_s, hipStream_t st);
+void tile_w8(const int8_t* src, const uint16_t* ssrc, int n, int k, uint4* dst_q, uint16_t* dst_s,
+             bool per_channel, hipStream_t st);
+void dequant_w8(const W8& w, uint16_t* out, hipStream_t st);  // bf16 [n][k] = bf16_rn(w * s)
+
+// ---- decode GEMV / skinny GEMM (m = 1..16), VALU, deterministic split-K ----
+void gemv_workspace_init();
+// y[m][n] = sum_k x[m][k] * W[n][k]; x bf16 rows of stride ldx; y fp32 (or bf16 with out_bf16, or the GLU
+// bf16 activation) rows of stride ldy
+void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
+void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
+
+// ---- prefill GEMM (bf16 MFMA on dequantized tiles staged in LDS) ----
+void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
+void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
+void gemm_set_out_bf16(bool on);
+bool gemm_out_bf16();
+
+// GEMV for m <= 32 (split into row blocks of 16), GEMM above (reference gemv.cuh:187-190)
+void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
+
+int qe_num_cus();

@@ -1,0 +1,161 @@
+"""Typed torch wrappers over the C-ABI (the reference's W4 / W8 structs and entry points, gemv.cuh:17-200).
+
+Tensors are device tensors; 16-bit scales are torch.float16 (QE_SCALE_F16) or torch.bfloat16. Every wrapper
+checks shapes on the host before calling into the library, which checks them again (fatal abort).
+"""
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from .qe import call
+
+SCALE_F16 = 1
+OUT_BF16 = 2
+GLU = 4
+W8_PER_CHANNEL = 8
+
+
+def _stream():
+    # a pointer-sized argument: an int would be passed as a 32-bit c_int
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _scale_flag(s):
+    if s.dtype == torch.float16:
+        return SCALE_F16
+    if s.dtype == torch.bfloat16:
+        return 0
+    raise TypeError(f"scales must be float16 or bfloat16, got {s.dtype}")
+
+
+@dataclass
+class W4:
+    """INT4 g128 matrix in the W4 fragment layout (q: uint8 [n*k/2], s: [n*k/128] 16-bit)."""
+    q: torch.Tensor
+    s: torch.Tensor
+    n: int
+    k: int
+    glu: bool = False
+
+    @property
+    def flags(self):
+        return _scale_flag(self.s) | (GLU if self.glu else 0)
+
+
+@dataclass
+class W8:
+    """INT8 matrix in the W8 layout (q: uint8 [n*k]); s: [n] (per channel) or [n*k/128] (group 128)."""
+    q: torch.Tensor
+    s: torch.Tensor
+    n: int
+    k: int
+    per_channel: bool = True
+
+    @property
+    def flags(self):
+        return _scale_flag(self.s) | (W8_PER_CHANNEL if self.per_channel else 0)
+
+
+def repack_w4(q, s, glu=False):
+    """compressed-tensors int32 [n][k/8] + scales [n][k/128] -> W4 (on the default stream, as the reference)."""
+    n, k = q.shape[0], q.shape[1] * 8
+    assert q.dtype == torch.int32 and q.is_contiguous() and s.shape == (n, k // 128) and s.is_contiguous()
+    assert n % 16 == 0 and k % 128 == 0
+    dq = torch.empty(n * k // 2, dtype=torch.uint8, device=q.device)
+    ds = torch.empty(n * (k // 128), dtype=s.dtype, device=q.device)
+    call("qe_repack_w4", q, s, n, k, dq, ds)
+    return W4(dq, ds, n, k, glu)
+
+
+def glu_rows(q, s, bits=4):
+    """[gate 0..I)[up 0..I) rows -> GLU tile order (8 gate, 8 up per 16-row tile)."""
+    n = q.shape[0]
+    k = q.shape[1] * 32 // bits
+    dq = torch.empty_like(q)
+    ds = torch.empty_like(s)
+    call("qe_glu_rows", q, s, n, k, dq, ds, bits)
+    return dq, ds
+
+
+def dequant_w4(w: W4):
+    out = torch.empty(w.n, w.k, dtype=torch.bfloat16, device=w.q.device)
+    call("qe_dequant_w4", w.q, w.s, w.n, w.k, _scale_flag(w.s), out, _stream())
+    return out
+
+
+def _out(m, n, out_bf16, glu, device):
+    if glu:
+        return torch.empty(m, n // 2, dtype=torch.bfloat16, device=device)
+    return torch.empty(m, n, dtype=torch.bfloat16 if out_bf16 else torch.float32, device=device)
+
+
+def gemv_w4(w: W4, x, out_bf16=False, y=None):
+    """decode GEMV / skinny GEMM, m = x.shape[0] in 1..16"""
+    m = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(m, w.n, out_bf16, w.glu, x.device) if y is None else y
+    call("qe_gemv_w4_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), m,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y
+
+
+def gemm_w4(w: W4, x, out_bf16=False, y=None):
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, w.glu, x.device) if y is None else y
+    call("qe_gemm_w4_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y
+
+
+def matmul_w4(w: W4, x, out_bf16=False, y=None):
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, w.glu, x.device) if y is None else y
+    call("qe_matmul_w4_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y
+
+
+def tile_w8(q, s, per_channel=True):
+    """row-major int8 [n][k] + scales ([n] per channel, else [n][k/128]) -> W8 layout"""
+    n, k = q.shape
+    assert q.dtype == torch.int8 and q.is_contiguous() and n % 16 == 0 and k % 128 == 0
+    dq = torch.empty(n * k, dtype=torch.uint8, device=q.device)
+    ds = torch.empty(n if per_channel else n * (k // 128), dtype=s.dtype, device=q.device)
+    call("qe_tile_w8", q, s, n, k, int(per_channel), dq, ds, _stream())
+    return W8(dq, ds, n, k, per_channel)
+
+
+def quantize_w8(w):
+    """RTN INT8 group 128 of a bf16 [n][k] matrix (reference qe_quantize_w8)"""
+    n, k = w.shape
+    dq = torch.empty(n * k, dtype=torch.uint8, device=w.device)
+    ds = torch.empty(n * (k // 128), dtype=torch.bfloat16, device=w.device)
+    call("qe_quantize_w8", w, n, k, dq, ds)
+    return W8(dq, ds, n, k, False)
+
+
+def dequant_w8(w: W8):
+    out = torch.empty(w.n, w.k, dtype=torch.bfloat16, device=w.q.device)
+    call("qe_dequant_w8", w.q, w.s, w.n, w.k, w.flags, out, _stream())
+    return out
+
+
+def gemv_w8(w: W8, x, out_bf16=False, y=None):
+    m = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(m, w.n, out_bf16, False, x.device) if y is None else y
+    call("qe_gemv_w8_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), m,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y
+
+
+def gemm_w8(w: W8, x, out_bf16=False, y=None):
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, False, x.device) if y is None else y
+    call("qe_gemm_w8_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y

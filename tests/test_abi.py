@@ -1,0 +1,55 @@
+"""The C-ABI library loads without a GPU, exports every entry point include/qe_kernels.h declares, and a
+violated precondition aborts with the reference's "check failed" message before any GPU call. CPU only."""
+import ctypes
+import os
+import re
+import subprocess
+import sys
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qe_kernels.h")
+LIB = os.path.join(ROOT, "qengine_amd", "libqe_kernels.so")
+
+
+def declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(qe_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    for must in ["qe_repack_w4", "qe_gemv_w4", "qe_gemv_w4g", "qe_skinny_w4", "qe_gemm_w4", "qe_gemm_w4_t",
+                 "qe_gemm_w4_s", "qe_gemv_w4_s", "qe_gemm_set_out_bf16", "qe_quantize_w8", "qe_gemv_w8",
+                 "qe_gemv_workspace_init"]:
+        assert must in names
+
+
+def test_library_exports_every_declared_symbol():
+    assert os.path.exists(LIB), "build first: python -m qengine_amd.build"
+    lib = ctypes.CDLL(LIB)
+    missing = [n for n in declared() if not hasattr(lib, n)]
+    assert not missing, missing
+    lib.qe_abi_version.restype = ctypes.c_int
+    assert lib.qe_abi_version() == 1
+
+
+@pytest.mark.parametrize("call,msg", [
+    ("lib.qe_repack_w4(None, None, 15, 128, None, None)", "repack_w4 15 128"),
+    ("lib.qe_tile_w8(None, None, 16, 100, 1, None, None, None)", "tile_w8 16 100"),
+    ("lib.qe_dequant_w4(None, None, 16, 64, 0, None, None)", "dequant_w4 16 64"),
+])
+def test_precondition_aborts_with_check_message(call, msg):
+    code = f"import ctypes; lib = ctypes.CDLL({LIB!r}); {call}"
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+    assert r.returncode != 0
+    assert "check failed" in r.stderr and msg in r.stderr, r.stderr
+
+
+def test_skinny_declines_unsupported_rows():
+    lib = ctypes.CDLL(LIB)
+    lib.qe_skinny_w4.restype = ctypes.c_int
+    assert lib.qe_skinny_w4(None, None, 16, 128, None, None, 17, 0) == 0
+    assert lib.qe_skinny_w4(None, None, 16, 128, None, None, 0, 0) == 0

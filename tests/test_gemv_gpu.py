@@ -1,0 +1,206 @@
+"""Decode GEMV / skinny GEMM (m = 1..16) through the C-ABI vs the CPU oracle.
+
+Gates:
+  * BASELINE: max|y - ref| <= 2e-2 * rms(ref), ref = the fp32 dequantize-then-matmul reference: weights
+    (u - 8) * s (INT4) or w * s (INT8), exact in fp32, product in float64.
+  * the kernel's own arithmetic: fp32 outputs within 1e-4 * rms(ref) of that reference.
+  * the reference's own test gate (tests/test_gemv.py:36,84): max|y - ref_bf16w| / max|ref_bf16w| < 1e-2 with
+    ref_bf16w built on the bf16-rounded dequantized weights (the oracle's dequant_w4).
+  * bit-identity: every row count gives the same bits per row (the reference's skinny == GEMV contract,
+    tests/test_skinny.py:1-2), and repeated calls are identical (deterministic split-K).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qengine_amd import call, ops, synth
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def err_ratio(y, ref):
+    ref = np.asarray(ref, np.float64)
+    return float(np.abs(np.asarray(y, np.float64) - ref).max() / np.sqrt(np.mean(ref ** 2)))
+
+
+def ref_gate(y, ref):
+    """reference tests/test_gemv.py:84 gate"""
+    return float(np.abs(np.asarray(y, np.float64) - ref).max() / np.abs(ref).max())
+
+
+def exact_w4(q, s, n, k, sdt):
+    """(u - 8) * s as float32 (exact)"""
+    return oracle.unpack_w4(q, n, k).astype(np.float32) * np.repeat(oracle.scale_to_f32(s, sdt), 128, axis=1)
+
+
+def exact_w8(q, s, n, k, per_channel):
+    sf = oracle.f16_to_f32(s)
+    sf = sf.reshape(n, 1) if per_channel else np.repeat(sf.reshape(n, k // 128), 128, axis=1)
+    return q.astype(np.float32) * sf
+
+
+def matmul_f64(xh, w):
+    return oracle.bf16_to_f32(xh).astype(np.float64) @ w.astype(np.float64).T
+
+
+def out_f32(y):
+    return oracle.bf16_to_f32(synth.bits(y)) if y.dtype == torch.bfloat16 else y.cpu().numpy()
+
+
+def glu_act(y):
+    """product [m][n] of a GLU-interleaved matrix -> act [m][n/2] = silu(gate) * up (float64)"""
+    y = np.asarray(y, np.float64)
+    m, n = y.shape
+    yt = y.reshape(m, n // 16, 2, 8)
+    gate, up = yt[:, :, 0, :], yt[:, :, 1, :]
+    return (gate / (1 + np.exp(-gate)) * up).reshape(m, n // 2)
+
+
+def assert_glu_close(y_bf16, act_ref, rel_rms):
+    """GLU outputs are heavy-tailed (a product of two sums): besides a tolerance relative to rms(act), each
+    bf16 output carries its own rounding (<= 2^-9 relative, doubled): |y - act| <= rel_rms * rms + 2^-8 |act|"""
+    y = np.asarray(y_bf16, np.float64)
+    bound = rel_rms * np.sqrt(np.mean(act_ref ** 2)) + 2.0 ** -8 * np.abs(act_ref)
+    assert np.all(np.abs(y - act_ref) <= bound), float((np.abs(y - act_ref) / bound).max())
+
+
+def setup_w4(n, k, sdt, seed, glu=False):
+    q, s = synth.w4_host(n, k, seed=seed, sdt=sdt)
+    if glu:
+        q, s = oracle.glu_rows(q, s, n, k)
+    w = ops.repack_w4(synth.to_dev(q), synth.to_dev(s, torch.float16 if sdt else torch.bfloat16), glu=glu)
+    return w, q, s
+
+
+@pytest.mark.parametrize("n,k", [(64, 256), (256, 1280), (1024, 5120)])
+@pytest.mark.parametrize("sdt", [0, 1])
+def test_gemv_w4_parity(dev, n, k, sdt):
+    w, q, s = setup_w4(n, k, sdt, seed=n + k + sdt)
+    xh = synth.x_host(16, k, seed=k)
+    x = synth.to_dev(xh)
+    ref = matmul_f64(xh, exact_w4(q, s, n, k, sdt))
+    ref_bw = oracle.matmul_bf16(xh, oracle.dequant_w4(q, s, n, k, sdt))
+    for m in (1, 2, 3, 4, 5, 8, 9, 16):
+        for out_bf16 in (False, True):
+            y = out_f32(ops.gemv_w4(w, x[:m], out_bf16=out_bf16))
+            e = err_ratio(y, ref[:m])
+            assert e <= (TOL if out_bf16 else 1e-4), (m, out_bf16, e)
+            assert ref_gate(y, ref_bw[:m]) < 1e-2
+
+
+@pytest.mark.parametrize("n,k", [(256, 1280), (5120, 5120)])
+def test_gemv_w4_batch_equals_alone(dev, n, k):
+    w, _, _ = setup_w4(n, k, 1, seed=7)
+    x = synth.to_dev(synth.x_host(16, k, seed=8))
+    full = ops.gemv_w4(w, x)
+    torch.cuda.synchronize()
+    fb = full.cpu().numpy().view(np.uint32)
+    for m in range(1, 17):
+        y = ops.gemv_w4(w, x[:m])
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32), fb[:m]), m
+    for r in (0, 5, 15):
+        y = ops.gemv_w4(w, x[r:r + 1])
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy().view(np.uint32)[0], fb[r]), r
+    again = ops.gemv_w4(w, x)
+    torch.cuda.synchronize()
+    assert np.array_equal(again.cpu().numpy().view(np.uint32), fb)
+
+
+@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048)])
+def test_gemv_w4_glu(dev, n, k):
+    w, q, s = setup_w4(n, k, 1, seed=31, glu=True)
+    xh = synth.x_host(16, k, seed=32)
+    x = synth.to_dev(xh)
+    act = glu_act(matmul_f64(xh, exact_w4(q, s, n, k, 1)))
+    full = ops.gemv_w4(w, x)
+    torch.cuda.synchronize()
+    yv = out_f32(full)
+    assert_glu_close(yv, act, 1e-4)
+    # the reference's bf16-rounded weights: their rounding shows up in act
+    act_bw = glu_act(oracle.matmul_bf16(xh, oracle.dequant_w4(q, s, n, k, 1)))
+    assert_glu_close(yv, act_bw, 2 * TOL)
+    fb = synth.bits(full)
+    for m in (1, 3, 8):
+        y = ops.gemv_w4(w, x[:m])
+        torch.cuda.synchronize()
+        assert np.array_equal(synth.bits(y), fb[:m])
+
+
+def test_reference_named_hooks(dev):
+    """qe_gemv_w4 / qe_gemv_w4g / qe_skinny_w4 (bf16 scales, fp32 out, stride k / n) == the _ex entry"""
+    n, k = 512, 2048
+    w, q, s = setup_w4(n, k, 0, seed=41)
+    x = synth.to_dev(synth.x_host(16, k, seed=42))
+    ref = ops.gemv_w4(w, x)
+    for m in (1, 7, 16):
+        y = torch.full((m, n), float("nan"), device=dev)
+        call("qe_gemv_w4", w.q, w.s, n, k, x, y, m)
+        y2 = torch.full((m, n), float("nan"), device=dev)
+        r = call("qe_skinny_w4", w.q, w.s, n, k, x, y2, m, 0)
+        y3 = torch.full((m, n), float("nan"), device=dev)
+        call("qe_gemv_w4g", w.q, w.s, n, k, x, y3, m, 0)
+        torch.cuda.synchronize()
+        assert r == 1
+        for yy in (y, y2, y3):
+            assert torch.equal(yy.view(torch.int32), ref[:m].view(torch.int32))
+    # 17..32 rows: the GEMV in row blocks of 16
+    xh32 = synth.x_host(32, k, seed=43)
+    y = torch.empty(32, n, device=dev)
+    call("qe_gemv_w4", w.q, w.s, n, k, synth.to_dev(xh32), y, 32)
+    torch.cuda.synchronize()
+    assert err_ratio(y.cpu().numpy(), matmul_f64(xh32, exact_w4(q, s, n, k, 0))) <= 1e-4
+
+
+@pytest.mark.parametrize("n,k", [(5120, 5120), (17408, 5120)])
+@pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
+def test_gemv_w4_baseline_shapes(dev, n, k, m):
+    """BASELINE configs 0 (m = 1, n = 17408) and 1 (m in {2,4,8,16}, n in {5120, 17408}), full size, bf16 out"""
+    if m == 1 and n == 5120:
+        pytest.skip("not a BASELINE shape")
+    w, q, s = setup_w4(n, k, 1, seed=1000 + n)
+    xh = synth.x_host(m, k, seed=2000 + m)
+    y = out_f32(ops.gemv_w4(w, synth.to_dev(xh), out_bf16=True))
+    e = err_ratio(y, matmul_f64(xh, exact_w4(q, s, n, k, 1)))
+    assert e <= TOL, e
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+@pytest.mark.parametrize("n,k", [(64, 256), (8192, 2048)])
+def test_gemv_w8_parity(dev, per_channel, n, k):
+    q, s = synth.w8_host(n, k, seed=51, per_channel=per_channel)
+    if not per_channel:
+        s = s.reshape(n, k // 128)
+    w = ops.tile_w8(synth.to_dev(q), synth.to_dev(s, torch.float16), per_channel)
+    xh = synth.x_host(16, k, seed=52)
+    x = synth.to_dev(xh)
+    ref = matmul_f64(xh, exact_w8(q, s, n, k, per_channel))
+    full = ops.gemv_w8(w, x)
+    torch.cuda.synchronize()
+    assert err_ratio(full.cpu().numpy(), ref) <= 1e-4
+    for m in (1, 4):
+        y = ops.gemv_w8(w, x[:m], out_bf16=True)
+        assert err_ratio(out_f32(y), ref[:m]) <= TOL
+        y32 = ops.gemv_w8(w, x[:m])
+        torch.cuda.synchronize()
+        assert np.array_equal(y32.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32)[:m])
+
+
+def test_gemv_w8_reference_hook(dev):
+    """qe_quantize_w8 + qe_gemv_w8 vs the reference's torch check (tests/test_w8.py), m = 1, 4, 8"""
+    n, k = 256, 5120
+    rng = np.random.default_rng(60)
+    wb = synth.np_bf16(rng.standard_normal((n, k)) * 0.02)
+    wd = ops.quantize_w8(synth.to_dev(wb))
+    qr, sr = oracle.quantize_w8(wb, n, k)
+    wref = qr.astype(np.float64) * np.repeat(oracle.bf16_to_f32(sr), 128, axis=1)
+    for m in (1, 4, 8):
+        xh = synth.x_host(m, k, seed=61 + m)
+        y = torch.empty(m, n, device=dev)
+        call("qe_gemv_w8", wd.q, wd.s, n, k, synth.to_dev(xh), y, m)
+        torch.cuda.synchronize()
+        ref = oracle.bf16_to_f32(xh).astype(np.float64) @ wref.T
+        assert ref_gate(y.cpu().numpy(), ref) < 1e-2

@@ -1,0 +1,250 @@
+"""Pins of the CPU oracle (oracle/qe_oracle.c) against checks that do not restate its own formulas:
+library dtype conversions, the PTX ISA mma.m16n8k16 A-fragment table, hand-computed known answers, numpy
+float64 matmul, brute-force ranking, invariants. CPU only."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qengine_amd import synth
+
+
+# ------------------------------------------------------------------ 16-bit floats vs torch
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(0)
+    a = np.concatenate([rng.standard_normal(20000).astype(np.float32) * 10.0 ** rng.integers(-30, 30, 20000),
+                        np.array([0.0, -0.0, 1.0, 1.00390625, 1.01171875, 3.0e38, -3.4e38, 1e-40, np.inf, -np.inf],
+                                 np.float32)]).astype(np.float32)
+    ref = torch.from_numpy(a).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.f32_to_bf16(a), ref)
+    lib = oracle.lib()
+    for v in a[:500]:
+        assert lib.or_f32_to_bf16(float(v)) == torch.tensor([v]).bfloat16().view(torch.int16).numpy().view(np.uint16)[0]
+
+
+def test_f16_decode_matches_numpy_all_patterns():
+    lib = oracle.lib()
+    pats = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    ref = pats.view(np.float16).astype(np.float32)
+    got = np.array([lib.or_f16_to_f32(int(p)) for p in pats[::7]], np.float32)
+    r = ref[::7]
+    ok = (got == r) | (np.isnan(got) & np.isnan(r))
+    assert ok.all()
+
+
+# ------------------------------------------------------------------ W4 format
+def _ptx_a_fragment(e, lane):
+    """(row, col) of element e (0..7) of the m16n8k16 .bf16 A fragment held by `lane` (PTX ISA, 'Matrix
+    Fragments for mma.m16n8k16 with floating point type': a0,a1 row g; a2,a3 row g+8; a4,a5 row g col+8; a6,a7
+    row g+8 col+8; col = 2 * (lane % 4) + (e & 1))"""
+    g, t = lane // 4, lane % 4
+    row = g + (8 if e in (2, 3, 6, 7) else 0)
+    col = 2 * t + (e & 1) + (8 if e >= 4 else 0)
+    return row, col
+
+
+def _decode_w4_fragments(dq, n, k):
+    """Independent decoder of the W4 layout: word (r, c, lane, kstep) is the A fragment of k-step `kstep`;
+    register j of dequant_w4 (reference gemv.cu:25-36) holds nibble j (low half) and nibble j + 4 (high half),
+    i.e. fragment element e = 2 j + hi comes from nibble slot j + 4 hi."""
+    u = np.empty((n, k), np.int16)
+    words = dq.reshape(n // 16, k // 64, 32, 4)
+    for e in range(8):
+        slot = (e >> 1) + 4 * (e & 1)
+        nib = ((words >> np.uint32(4 * slot)) & np.uint32(15)).astype(np.int16)  # [r][c][lane][kstep]
+        for lane in range(32):
+            row, col = _ptx_a_fragment(e, lane)
+            for ks in range(4):
+                u[row::16, col + 16 * ks::64][: n // 16] = nib[:, :, lane, ks]
+    return u
+
+
+@pytest.mark.parametrize("n,k", [(16, 128), (32, 256), (48, 384)])
+def test_repack_w4_round_trip_through_ptx_decoder(n, k):
+    q, s = synth.w4_host(n, k, seed=n + k)
+    dq, ds = oracle.repack_w4(q, s, n, k)
+    u = _decode_w4_fragments(dq, n, k)
+    assert np.array_equal(u - 8, oracle.unpack_w4(q, n, k))
+    # scales: [n/16][G][16], row-in-tile fastest
+    G = k // 128
+    assert np.array_equal(ds.reshape(n // 16, G, 16).transpose(0, 2, 1).reshape(n, G), s)
+
+
+def test_repack_w4_known_answer():
+    """u(row, k) = (row + k) % 16 on one 16 x 128 tile: the first word (lane 0, k-step 0) holds, LSB first,
+    (0,0)=0 (8,0)=8 (0,8)=8 (8,8)=0 (0,1)=1 (8,1)=9 (0,9)=9 (8,9)=1 -> 0x19910880 (slot order of the reference
+    comment gemv.cu:532-537, computed by hand)."""
+    n, k = 16, 128
+    u = (np.arange(n)[:, None] + np.arange(k)[None, :]) % 16
+    q = np.zeros((n, k // 8), np.uint32)
+    for j in range(8):
+        q |= u[:, j::8].astype(np.uint32) << np.uint32(4 * j)
+    s = np.ones((n, 1), np.uint16)
+    dq, _ = oracle.repack_w4(q.view(np.int32), s, n, k)
+    assert dq[0] == 0x19910880
+    # lane 5 (g = 1, t = 1), k-step 2: row 1, k0 = 32 + 2 = 34: (1,34)=3 (9,34)=11 (1,42)=11 (9,42)=3 (1,35)=4
+    # (9,35)=12 (1,43)=12 (9,43)=4 -> 0x4CC43BB3
+    assert dq[5 * 4 + 2] == 0x4CC43BB3
+
+
+def test_repack_w4_is_a_bijection():
+    n, k = 32, 256
+    # every source nibble position gets a distinct 12-bit id split over three matrices; decode must invert
+    ids = np.arange(n * k).reshape(n, k)
+    for part in range(3):
+        u = (ids >> (4 * part)) & 15
+        q = np.zeros((n, k // 8), np.uint32)
+        for j in range(8):
+            q |= u[:, j::8].astype(np.uint32) << np.uint32(4 * j)
+        dq, _ = oracle.repack_w4(q.view(np.int32), np.zeros((n, 2), np.uint16), n, k)
+        assert np.array_equal(_decode_w4_fragments(dq, n, k), u)
+
+
+def test_unpack_matches_reference_expression():
+    """reference tests/test_gemv.py:13-15: ((wp[..., None] >> arange(0, 32, 4)) & 15) - 8"""
+    n, k = 32, 256
+    q, _ = synth.w4_host(n, k, seed=3)
+    wp = torch.from_numpy(q)
+    ref = (((wp.unsqueeze(-1) >> torch.arange(0, 32, 4, dtype=torch.int32)) & 15).reshape(n, k) - 8).numpy()
+    assert np.array_equal(oracle.unpack_w4(q, n, k), ref.astype(np.int8))
+
+
+@pytest.mark.parametrize("sdt", [0, 1])
+def test_dequant_w4_closed_form(sdt):
+    """bf16_rn((u - 8) * s) through torch: (unpack * s.repeat_interleave(128)).bfloat16() (test_gemv.py:36)"""
+    n, k = 48, 384
+    q, s = synth.w4_host(n, k, seed=5, sdt=sdt)
+    w = torch.from_numpy(oracle.unpack_w4(q, n, k).astype(np.float32))
+    sf = torch.from_numpy(oracle.scale_to_f32(s, sdt)).repeat_interleave(128, dim=1)
+    ref = (w * sf).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.dequant_w4(q, s, n, k, sdt), ref)
+
+
+def test_glu_rows_matches_interleave_closed_form():
+    """reference tests/test_q8.py:75-79: stack([gate.reshape(-1, 8, k), up.reshape(-1, 8, k)], 1)"""
+    n, k = 64, 256
+    q, s = synth.w4_host(n, k, seed=7)
+    dq, ds = oracle.glu_rows(q, s, n, k)
+    qt = torch.from_numpy(q)
+    ref = torch.stack([qt[: n // 2].reshape(-1, 8, k // 8), qt[n // 2:].reshape(-1, 8, k // 8)], 1).reshape(n, -1)
+    assert np.array_equal(dq, ref.numpy())
+    st = torch.from_numpy(s.view(np.int16))
+    refs = torch.stack([st[: n // 2].reshape(-1, 8, 2), st[n // 2:].reshape(-1, 8, 2)], 1).reshape(n, -1)
+    assert np.array_equal(ds.view(np.int16), refs.numpy())
+
+
+def test_glu_epilogue_matches_torch_silu():
+    rng = np.random.default_rng(1)
+    y = rng.standard_normal((3, 64)).astype(np.float32) * 4
+    act = oracle.bf16_to_f32(oracle.glu_epilogue(y))
+    yt = torch.from_numpy(y).double().reshape(3, 4, 2, 8)
+    ref = (torch.nn.functional.silu(yt[:, :, 0]) * yt[:, :, 1]).reshape(3, 32).numpy()
+    assert np.allclose(act, ref, rtol=2 ** -8, atol=1e-6)
+
+
+# ------------------------------------------------------------------ matmul
+def test_matmul_bf16_vs_numpy_f64():
+    rng = np.random.default_rng(2)
+    m, n, k = 5, 48, 640
+    x = synth.np_bf16(rng.standard_normal((m, k)))
+    w = synth.np_bf16(rng.standard_normal((n, k)) * 0.05)
+    y = oracle.matmul_bf16(x, w)
+    xf, wf = oracle.bf16_to_f32(x).astype(np.float64), oracle.bf16_to_f32(w).astype(np.float64)
+    ref = xf @ wf.T
+    bound = k * 2 ** -23 * (np.abs(xf) @ np.abs(wf).T)
+    assert np.all(np.abs(y - ref) <= bound)
+
+
+def test_matmul_bf16_brute_force_tiny():
+    x = synth.np_bf16(np.array([[1.0, 2.0, -3.0, 0.5]], np.float32))
+    w = synth.np_bf16(np.array([[1.0, 1.0, 1.0, 1.0], [0.25, -1.0, 2.0, 4.0]], np.float32))
+    assert np.array_equal(oracle.matmul_bf16(x, w), np.array([[0.5, -5.75]], np.float32))
+
+
+# ------------------------------------------------------------------ W8
+def test_quantize_w8_matches_reference_torch_expression():
+    """reference tests/test_w8.py:6-9"""
+    n, k = 32, 256
+    rng = np.random.default_rng(4)
+    wb = synth.np_bf16(rng.standard_normal((n, k)) * 0.02)
+    wb[3, :128] = 0  # an all-zero group (scale 0)
+    q, s = oracle.quantize_w8(wb, n, k)
+    g = torch.from_numpy(oracle.bf16_to_f32(wb)).view(n, k // 128, 128)
+    sc = (g.abs().amax(-1) / 127).bfloat16()
+    scf = sc.float()
+    qref = torch.clamp(torch.round(g / torch.where(scf > 0, scf, 1).unsqueeze(-1)), -127, 127)
+    assert np.array_equal(q, qref.reshape(n, k).numpy().astype(np.int8))
+    assert np.array_equal(s, sc.view(torch.int16).numpy().view(np.uint16))
+
+
+def _decode_w8_fragments(dq, n, k):
+    """16-byte record of lane `ln` in slab (rt, sl): bytes 8 hs + e are elements a_e of the k-step hs fragment
+    (reference gemv.cu:700-703 builds a0a1 / a2a3 from bytes 0-1 / 2-3 of each half), PTX A-fragment table."""
+    out = np.empty((n, k), np.int8)
+    rec = dq.view(np.int8).reshape(n // 16, k // 32, 32, 16)
+    for lane in range(32):
+        for hs in range(2):
+            for e in range(8):
+                row, col = _ptx_a_fragment(e, lane)
+                out[row::16, 16 * hs + col::32][: n // 16] = rec[:, :, lane, 8 * hs + e]
+    return out
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_tile_w8_round_trip_through_ptx_decoder(per_channel):
+    n, k = 32, 256
+    q, s = synth.w8_host(n, k, seed=9, per_channel=per_channel)
+    if not per_channel:
+        s = s.reshape(n, k // 128)
+    dq, ds = oracle.tile_w8(q, s, n, k, per_channel)
+    assert np.array_equal(_decode_w8_fragments(dq, n, k), q)
+    if per_channel:
+        assert np.array_equal(ds, s)
+    else:
+        assert np.array_equal(ds.reshape(n // 16, 2, 16).transpose(0, 2, 1).reshape(n, 2), s)
+    pos = {oracle.w8_pos(r, c, k) for r in range(n) for c in range(k)}
+    assert len(pos) == n * k and max(pos) == n * k - 1
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_dequant_w8_closed_form(per_channel):
+    n, k = 32, 256
+    q, s = synth.w8_host(n, k, seed=10, per_channel=per_channel)
+    sf = oracle.f16_to_f32(s)
+    sf = sf[:, None] if per_channel else np.repeat(sf.reshape(n, k // 128), 128, axis=1)
+    ref = torch.from_numpy(q.astype(np.float32) * sf).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.dequant_w8(q, s, n, k, per_channel, 1), ref)
+
+
+# ------------------------------------------------------------------ MoE
+def test_moe_route_brute_force_with_ties():
+    T, E, topk = 7, 64, 10
+    lg = synth.logits_host(T, E, seed=11)
+    lg[2, 5] = lg[2, 9] = lg[2, 40] = 3.0  # ties: lower index first
+    lg[4, :] = 0.0                         # all equal: experts 0..9
+    sel, w = oracle.moe_route(lg, topk)
+    for t in range(T):
+        order = np.lexsort((np.arange(E), -lg[t]))[:topk]
+        assert np.array_equal(sel[t], order)
+        ex = np.exp(lg[t, order].astype(np.float64) - lg[t, order[0]])
+        assert np.allclose(w[t], ex / ex.sum(), rtol=1e-6)
+        # equivalently the softmax over all E renormalised over the selection
+        p = np.exp(lg[t].astype(np.float64) - lg[t].max())
+        p /= p.sum()
+        assert np.allclose(w[t], p[order] / p[order].sum(), rtol=1e-6)
+    assert np.array_equal(sel[4], np.arange(10))
+    assert list(sel[2][:3]) == [5, 9, 40]
+
+
+def test_moe_segment_invariants():
+    T, E, topk = 33, 40, 6
+    sel, _ = oracle.moe_route(synth.logits_host(T, E, seed=12), topk)
+    cnt, off, lst, inv = oracle.moe_segment(sel, E)
+    flat = sel.ravel()
+    assert cnt.sum() == T * topk and np.array_equal(cnt, np.bincount(flat, minlength=E))
+    assert off[0] == 0 and np.array_equal(np.diff(off), cnt)
+    assert np.array_equal(np.sort(lst), np.arange(T * topk))          # every pair exactly once
+    assert np.array_equal(lst, np.argsort(flat, kind="stable"))       # expert-ordered, stable inside an expert
+    assert np.array_equal(inv[lst], np.arange(T * topk))              # inverse map
+    for e in range(E):
+        assert np.all(flat[lst[off[e]:off[e + 1]]] == e)
