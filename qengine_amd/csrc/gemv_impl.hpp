@@ -1,0 +1,288 @@
+// Decode GEMV and skinny GEMM (m = 1..16 rows) on the W4 / W8 fragment layouts, for gfx950.
+//
+// Design (memory-bound: the packed weights are streamed once from HBM; the VALU work per byte is the other
+// limit, so the inner loop is counted in instructions):
+//   * one block per 16-row tile; wave w of the block owns K slice w (NG 128-k groups). A wave-load is
+//     64 lanes x 16 B = 1 KB, contiguous in the layout (W4: one group of the tile, W8: half a group). All weight
+//     loads of the slice are issued first (non-temporal), then the activations are staged.
+//   * activation staging: lane L of a wave loads dword `slot` (L % 8) of lane class c = L / 8 of each group
+//     and stores it at LDS position L, so a class's 8 dwords are contiguous (two ds_read_b128 per lane and
+//     group, broadcast across the 8 lanes of a row pair) and the class sum is a 3-step DPP reduction.
+//   * nibbles become bf16 by OR-ing them into the mantissa of 128.0 (0x4300 -> 128 + u exactly, v_and_or_b32),
+//     v_dot2_f32_bf16 accumulates (128 + u) * x in fp32; per group the bias is removed with the staged class
+//     sum and the group scale applied: acc += s * (a - 136 X). INT8 bytes (XOR 0x80 -> u = w + 128) go through
+//     v_cvt_f32_ubyte + v_cvt_pk_bf16 (exact), bias 128.
+//   * reduction: lanes of one row within a half-wave by DPP quad swaps, then half-waves and slices through LDS
+//     in a fixed order. No global atomics, no workspace; results are deterministic and independent of m
+//     ("batch == alone", the reference's skinny / GEMV contract, skinny.cu:1-14): the slicing depends on (n, k)
+//     only.
+#pragma once
+#include "qe_api.hpp"
+
+namespace qe_gemv {
+
+typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
+
+enum Fmt : int { kFmtW4 = 0, kFmtW8G = 1, kFmtW8C = 2 };
+enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
+constexpr int kMaxWaves = 8;      // K slices per block (even slicing)
+constexpr int kGenericNG = 16;    // max groups per slice of the generic (uneven slices) variant
+constexpr int kMaxWavesGeneric = 16;  // K slices per block of the generic variant: K <= 16 * 16 * 128 = 32768
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_v, a), __builtin_bit_cast(bf16x2_v, b), c,
+                                           false);
+}
+__device__ __forceinline__ u32x4_v ld_stream(const uint4* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p));
+}
+// (a & m) | c in one VALU op (the compiler splits it into two when m and c are literals)
+__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
+    return r;
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
+                                                                     false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8
+
+// x dword (within a 128-k group, 0..63) of slot `sl` of lane class `c` (c = 4 h + t)
+template <int FMT>
+__device__ __forceinline__ int x_dword(int c, int sl) {
+    const int h = c >> 2, t = c & 3;
+    if constexpr (FMT == kFmtW4) return 32 * h + 8 * (sl >> 1) + 4 * (sl & 1) + t;  // pair at 64h + 16j + 2t (+8b)
+    else return 16 * (2 * (sl >> 2) + h) + 4 * (sl & 3) + t;  // W8: load e = sl/4, dword d = sl%4
+}
+
+template <int SDT>
+__device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
+    if constexpr (SDT >= 0) return scale_to_f32<SDT>(v);
+    else return sdt == kScaleF16 ? scale_to_f32<kScaleF16>(v) : scale_to_f32<kScaleBF16>(v);
+}
+
+// NG > 0: every slice has exactly NG groups (G = NG * S). NG == 0: slices of G / S groups (<= kGenericNG).
+// SDT < 0: scale dtype chosen at run time (`sdt`). PF: the activation dwords of every group are loaded up front,
+// interleaved with the weight loads of the same group (w_i, x_i, s_i, ...), so the activation latency hides
+// behind the weight latency; else they are loaded when the group is reached (large m).
+// Dynamic LDS: per wave xl [MT][64] u32 + xsum [MT][8] (one group at a time) + the slice's 16-bit scales
+// [NGM][16] (W8C: [16]), then red [S][2][MT][16].
+template <int MT, int FMT, int SDT, int NG, bool PF>
+__global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
+__attribute__((amdgpu_waves_per_eu(MT == 1 ? 6 : MT == 2 ? 5 : 1))) gemv_kernel(
+    const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K, const uint16_t* __restrict__ x,
+    int ldx, void* __restrict__ y, int ldy, int m, int out, int sdt) {
+    constexpr int NGM = NG > 0 ? NG : kGenericNG;
+    constexpr int LPG = FMT == kFmtW4 ? 1 : 2;  // wave-loads per group
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+
+    const int S = blockDim.x >> 6;
+    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    constexpr int WSZ = MT * 72 + NGM * 8;  // dwords of LDS per wave
+    uint32_t* xl = lds + (size_t)w * WSZ;                   // [MT][64]
+    float* xsum = reinterpret_cast<float*>(xl + MT * 64);   // [MT][8]
+    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + MT * 72);  // [NGM][16] scales of the slice
+    float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][2][MT][16]
+    const int tile = blockIdx.x;
+    const int G = K >> 7;
+    const int gb = NG > 0 ? w * NG : w * G / S;
+    const int ng = NG > 0 ? NG : (w + 1) * G / S - gb;
+    const int g = (L >> 2) & 7, t = L & 3, h = L >> 5;
+
+    // activation dword of this lane in the class-major staging: class c = L / 8, slot L % 8
+    const int c_st = L >> 3, sl_st = L & 7;
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64 + x_dword<FMT>(c_st, sl_st);
+    auto ldx_group = [&](int tok, int i) { return tok < m ? xw[(size_t)tok * (ldx >> 1) + i * 64] : 0u; };
+
+    // 1. loads, per group in the order they are consumed (vmcnt retires in order)
+    const uint4* qp = FMT == kFmtW4 ? q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + L
+                                    : q + ((size_t)tile * (K >> 5) + 4 * gb) * 32 + L;
+    // the slice's scales: 16 per group (W8C: 16 per tile) as one dword per lane, staged in LDS
+    {
+        const int ndw = FMT == kFmtW8C ? 8 : ng * 8;
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(FMT == kFmtW8C ? s + 16 * tile
+                                                                            : s + ((size_t)tile * G + gb) * 16);
+        if (L < ndw) reinterpret_cast<uint32_t*>(sl16)[L] = sp[L];
+    }
+    u32x4_v wv[NGM][LPG];
+    uint32_t xr[PF ? MT : 1][PF ? NGM : 1];
+#pragma unroll
+    for (int i = 0; i < NGM; i++) {
+        if (NG == 0 && i >= ng) break;
+#pragma unroll
+        for (int e = 0; e < LPG; e++) wv[i][e] = ld_stream(qp + (size_t)(i * LPG + e) * 64);
+        if constexpr (PF) {
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) xr[tok][i] = ldx_group(tok, i);
+        }
+    }
+
+    // 2. per group: stage x (class-major, class sums times the bias), then the dot products
+    constexpr float bias = FMT == kFmtW4 ? 136.f : 128.f;
+    const int cls = 4 * h + t;
+    const uint32_t kMask = 0x000F000Fu;
+    const uint32_t kMagic = 0x43004300u;  // bf16 (128, 128)
+    float acc_lo[MT], acc_hi[MT];
+#pragma unroll
+    for (int tok = 0; tok < MT; tok++) acc_lo[tok] = acc_hi[tok] = 0.f;
+#pragma unroll
+    for (int i = 0; i < NGM; i++) {
+        if (NG == 0 && i >= ng) break;
+        // the wave's own LDS region; LDS operations of one wave complete in order
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int tok = 0; tok < MT; tok++) {
+            const uint32_t v = PF ? xr[PF ? tok : 0][PF ? i : 0] : ldx_group(tok, i);
+            xl[tok * 64 + L] = v;
+            float sm = dot2_bf16(v, 0x3F803F80u, 0.f);  // x_lo + x_hi (bf16 (1, 1))
+            sm = dpp_add<kDppXor1>(sm);
+            sm = dpp_add<kDppXor2>(sm);
+            sm = dpp_add<kDppHalfMirror>(sm);
+            if (sl_st == 0) xsum[tok * 8 + c_st] = bias * sm;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+        const int so = FMT == kFmtW8C ? 0 : i * 16;
+        const float s_lo = scale_rt<SDT>(sl16[so + g], sdt);
+        const float s_hi = scale_rt<SDT>(sl16[so + g + 8], sdt);
+        // the dot2 chains start at -bias * X, so they end at sum (u - 8) x (or sum w x for INT8)
+        float a_lo[MT], a_hi[MT];
+#pragma unroll
+        for (int tok = 0; tok < MT; tok++) a_lo[tok] = a_hi[tok] = -xsum[tok * 8 + cls];
+        if constexpr (FMT == kFmtW4) {
+            uint32_t p[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t wd = wv[i][0][j];
+                p[j][0] = and_or(wd, kMask, kMagic);        // row g,     k0, k0 + 1
+                p[j][1] = and_or(wd >> 4, kMask, kMagic);   // row g + 8, k0, k0 + 1
+                p[j][2] = and_or(wd >> 8, kMask, kMagic);   // row g,     k0 + 8, k0 + 9
+                p[j][3] = and_or(wd >> 12, kMask, kMagic);  // row g + 8, k0 + 8, k0 + 9
+            }
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) {
+                const u32x4_v x0 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8]);
+                const u32x4_v x1 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8 + 4]);
+                const uint32_t xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    a_lo[tok] = dot2_bf16(p[j][0], xv[2 * j], a_lo[tok]);
+                    a_lo[tok] = dot2_bf16(p[j][2], xv[2 * j + 1], a_lo[tok]);
+                    a_hi[tok] = dot2_bf16(p[j][1], xv[2 * j], a_hi[tok]);
+                    a_hi[tok] = dot2_bf16(p[j][3], xv[2 * j + 1], a_hi[tok]);
+                }
+            }
+        } else {
+            uint32_t plo[2][4], phi[2][4];
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+#pragma unroll
+                for (int d = 0; d < 4; d++) {
+                    const uint32_t u = wv[i][e][d] ^ 0x80808080u;  // (g, k) (g, k+1) (g+8, k) (g+8, k+1)
+                    plo[e][d] = pack_bf16x2((float)(u & 0xffu), (float)((u >> 8) & 0xffu));
+                    phi[e][d] = pack_bf16x2((float)((u >> 16) & 0xffu), (float)(u >> 24));
+                }
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) {
+                const u32x4_v x0 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8]);
+                const u32x4_v x1 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8 + 4]);
+                const uint32_t xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int e = 0; e < 2; e++)
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {
+                        a_lo[tok] = dot2_bf16(plo[e][d], xv[4 * e + d], a_lo[tok]);
+                        a_hi[tok] = dot2_bf16(phi[e][d], xv[4 * e + d], a_hi[tok]);
+                    }
+            }
+        }
+#pragma unroll
+        for (int tok = 0; tok < MT; tok++) {
+            acc_lo[tok] = fmaf(s_lo, a_lo[tok], acc_lo[tok]);
+            acc_hi[tok] = fmaf(s_hi, a_hi[tok], acc_hi[tok]);
+        }
+    }
+
+    // 3. rows g / g + 8: lanes t (DPP quad swaps), then half-waves and slices through LDS, fixed order
+#pragma unroll
+    for (int tok = 0; tok < MT; tok++) {
+        float a = dpp_add<kDppXor1>(acc_lo[tok]);
+        float b = dpp_add<kDppXor1>(acc_hi[tok]);
+        a = dpp_add<kDppXor2>(a);
+        b = dpp_add<kDppXor2>(b);
+        if (t == 0) {
+            red[((w * 2 + h) * MT + tok) * 16 + g] = a;
+            red[((w * 2 + h) * MT + tok) * 16 + g + 8] = b;
+        }
+    }
+    __syncthreads();
+    auto rsum = [&](int tok, int rr) {
+        float v = 0.f;
+        for (int ws = 0; ws < S; ws++)
+            v += red[((ws * 2) * MT + tok) * 16 + rr] + red[((ws * 2 + 1) * MT + tok) * 16 + rr];
+        return v;
+    };
+    const int row0 = 16 * tile;
+    if (out == kOutGLU) {
+        for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
+            const int tok = idx >> 3, gg = idx & 7;
+            reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 / 2 + gg] =
+                f32_to_bf16(silu_f32(rsum(tok, gg)) * rsum(tok, gg + 8));
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
+            const int tok = idx >> 4, rr = idx & 15;
+            const float v = rsum(tok, rr);
+            if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 + rr] = f32_to_bf16(v);
+            else reinterpret_cast<float*>(y)[(size_t)tok * ldy + row0 + rr] = v;
+        }
+    }
+}
+
+// K slicing of a matrix: (groups per slice NG, slices S); NG = 0 means uneven slices (generic kernel).
+// Depends on (n, k) only, so every row count of a matrix reduces in the same order.
+struct Slicing {
+    int ng, S;
+};
+Slicing gemv_slicing(int n, int k);
+
+template <int FMT, int SDT>
+void launch_gemv(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                 int out, int sdt, hipStream_t st) {
+    const Slicing sc = gemv_slicing(n, k);
+    const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
+    const int ngm = sc.ng > 0 ? sc.ng : kGenericNG;
+    const bool pf = mt * ngm <= 16;  // activation prefetch registers
+    const size_t lds = (size_t)sc.S * (mt * 72 + ngm * 8) * 4 + (size_t)sc.S * 2 * mt * 16 * 4;
+    const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);
+#define QE_GEMV_K(MT_, NG_, PF_) \
+    gemv_kernel<MT_, FMT, SDT, NG_, PF_><<<grid, block, lds, st>>>(q, s, n, k, x, ldx, y, ldy, m, out, sdt)
+#define QE_GEMV_NG(MT_, PF_)                         \
+    do {                                             \
+        if (sc.ng == 8) QE_GEMV_K(MT_, 8, PF_);      \
+        else if (sc.ng == 4) QE_GEMV_K(MT_, 4, PF_); \
+        else if (sc.ng == 2) QE_GEMV_K(MT_, 2, PF_); \
+        else QE_GEMV_K(MT_, 0, PF_);                 \
+    } while (0)
+    if (mt == 1) QE_GEMV_NG(1, true);
+    else if (mt == 2) QE_GEMV_NG(2, true);
+    else if (mt == 4) {
+        if (pf) QE_GEMV_NG(4, true);
+        else QE_GEMV_NG(4, false);
+    } else if (mt == 8) {
+        QE_GEMV_NG(8, false);
+    } else {
+        QE_GEMV_NG(16, false);
+    }
+#undef QE_GEMV_NG
+#undef QE_GEMV_K
+    HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace qe_gemv

@@ -1,0 +1,17 @@
+// INT4 decode GEMV / skinny GEMM instantiations (kernel: gemv_impl.hpp).
+#include "gemv_impl.hpp"
+
+using namespace qe_gemv;
+
+static void gemv_check(int n, int k, const void* x, int ldx, int ldy, int m, bool glu) {
+    CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && m >= 1 && m <= kMaxGemvRows, "gemv %d %d %d", n, k, m);
+    CHECK(ldx >= k && ldx % 2 == 0 && ((uintptr_t)x & 3) == 0, "gemv ldx %d (even, >= k, x 4-byte aligned)", ldx);
+    CHECK(ldy >= (glu ? n / 2 : n), "gemv ldy %d", ldy);
+}
+
+void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
+    gemv_check(w.n, w.k, x, ldx, ldy, m, w.glu);
+    const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    if (w.sdt == kScaleF16) launch_gemv<kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    else launch_gemv<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+}
