@@ -97,6 +97,27 @@ def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None):
     return res
 
 
+def bench_gemm(m, n, k, steps=10, warmup=3, copies=2):
+    """prefill GEMM: TFLOP/s from the kernel's mean duration (events around each launch)"""
+    import torch
+    from qengine_amd import ops, synth
+    ws = []
+    for c in range(copies):
+        q, s = synth.w4_dev(n, k, seed=300 + c)
+        ws.append(ops.repack_w4(q, s))
+        del q, s
+    x = synth.x_dev(m, k, seed=2)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    fn = lambda i: ops.gemm_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    wall_ms, ev_ms, med_ms = time_launches(fn, steps, warmup, len(ws))
+    flop = 2.0 * m * n * k
+    del ws, x, y
+    torch.cuda.empty_cache()
+    return {"m": m, "n": n, "k": k, "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 1),
+            "pct_bf16_peak": round(100 * flop / (ev_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 1),
+            "ms_kernel": round(ev_ms, 4)}
+
+
 def cpu_baseline(args, m=1, n=17408, k=5120):
     """oracle dequant (bf16_rn((u-8)*s)) + fp32 matmul, same workload shape, host cores, ~cpu_seconds of work"""
     import numpy as np
@@ -144,6 +165,8 @@ def main():
             secondary[f"skinny_m{m}_n{n}"] = {"gbs_kernel": round(r["gbs_kernel"], 1),
                                               "pct_hbm": round(100 * r["gbs_kernel"] / HBM_PEAK_GBS, 1),
                                               "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2)}
+        secondary["prefill_k5120_n17408"] = bench_gemm(8192, 17408, 5120)
+        secondary["prefill_k17408_n5120"] = bench_gemm(8192, 5120, 17408)
     cpu = None if args.no_cpu else cpu_baseline(args)
     achieved = g["gbs_kernel"]
     out = {

@@ -1,0 +1,125 @@
+"""Prefill GEMM (bf16 MFMA on LDS-staged dequantized tiles) through the C-ABI vs the CPU oracle.
+
+Gate (BASELINE): max|y - ref| <= 2e-2 * rms(ref), ref = the oracle's dequantize-then-matmul (weights dequantized
+to bf16 as the reference does, bf16_rn((u - 8) * s), product in float64). That bf16 weight is exactly the operand
+this kernel multiplies, so fp32 outputs are also held to 1e-4 * rms (fp32 sums only), far inside the reference's own
+gate (tests/test_gemm.py:26-27, max|err| / max|ref| < 1e-2). Full BASELINE shapes are checked on sampled rows."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qengine_amd import call, ops, synth
+from test_gemv_gpu import TOL, assert_bf16_close, assert_glu_close, err_ratio, glu_act, matmul_f64, oracle_ref, oracle_ref_w8, out_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def setup(n, k, sdt, seed, glu=False):
+    q, s = synth.w4_host(n, k, seed=seed, sdt=sdt)
+    if glu:
+        q, s = oracle.glu_rows(q, s, n, k)
+    w = ops.repack_w4(synth.to_dev(q), synth.to_dev(s, torch.float16 if sdt else torch.bfloat16), glu=glu)
+    return w, q, s
+
+
+@pytest.mark.parametrize("n,k,t", [(128, 128, 1), (256, 512, 37), (512, 1024, 300), (384, 2048, 129),
+                                   (1024, 5120, 256)])
+@pytest.mark.parametrize("sdt", [0, 1])
+def test_gemm_w4_parity(dev, n, k, t, sdt):
+    w, q, s = setup(n, k, sdt, seed=n + k + t)
+    xh = synth.x_host(t, k, seed=t)
+    ref = oracle_ref(xh, q, s, n, k, sdt)
+    x = synth.to_dev(xh)
+    y32 = out_f32(ops.gemm_w4(w, x))
+    assert err_ratio(y32, ref) <= 1e-4
+    y16 = out_f32(ops.gemm_w4(w, x, out_bf16=True))
+    assert_bf16_close(y16, ref)
+
+
+def test_gemm_w4_glu(dev):
+    n, k, t = 512, 1024, 77
+    w, q, s = setup(n, k, 1, seed=5, glu=True)
+    xh = synth.x_host(t, k, seed=6)
+    act = glu_act(oracle.bf16_to_f32(xh).astype(np.float64)
+                  @ oracle.bf16_to_f32(oracle.dequant_w4(q, s, n, k, 1)).astype(np.float64).T)
+    y = out_f32(ops.gemm_w4(w, synth.to_dev(xh)))
+    assert_glu_close(y, act, 1e-4)
+
+
+def test_gemm_matches_gemv_rows(dev):
+    """matmul dispatch: m <= 32 runs the GEMV, above the GEMM; both meet the gate on the same rows"""
+    n, k = 1024, 2048
+    w, q, s = setup(n, k, 1, seed=9)
+    xh = synth.x_host(64, k, seed=10)
+    x = synth.to_dev(xh)
+    ref = oracle_ref(xh, q, s, n, k, 1)
+    yg = out_f32(ops.matmul_w4(w, x))        # GEMM (64 rows)
+    yv = out_f32(ops.matmul_w4(w, x[:32]))   # GEMV (32 rows in two launches)
+    assert err_ratio(yg, ref) <= 1e-4 and err_ratio(yv, ref[:32]) <= TOL
+
+
+def test_reference_named_gemm_hooks(dev):
+    """qe_gemm_w4 / _t / _s (bf16 scales, fp32 out) and qe_gemm_set_out_bf16 (bf16 RN of the same sums)"""
+    n, k, t = 256, 1024, 100
+    w, q, s = setup(n, k, 0, seed=11)
+    x = synth.to_dev(synth.x_host(t, k, seed=12))
+    ref = ops.gemm_w4(w, x)
+    for name in ("qe_gemm_w4", "qe_gemm_w4_t"):
+        y = torch.full((t, n), float("nan"), device=dev)
+        call(name, w.q, w.s, n, k, x, y, t)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+    call("qe_gemm_set_out_bf16", 1)
+    try:
+        yb = torch.full((t, n), float("nan"), device=dev, dtype=torch.bfloat16)
+        call("qe_gemm_w4", w.q, w.s, n, k, x, yb, t)
+        torch.cuda.synchronize()
+    finally:
+        call("qe_gemm_set_out_bf16", 0)
+    assert torch.equal(yb.view(torch.int16), ref.bfloat16().view(torch.int16))  # RN of the fp32 result, bit for bit
+
+
+@pytest.mark.parametrize("n,k", [(17408, 5120), (5120, 17408)])
+def test_gemm_w4_baseline_shapes_sampled(dev, n, k):
+    """BASELINE config 2 (M = 8192) at full size; 48 sampled token rows checked against the oracle"""
+    t = 8192
+    w, q, s = setup(n, k, 1, seed=n)
+    x = synth.x_dev(t, k, seed=3)
+    y = ops.gemm_w4(w, x, out_bf16=True)
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(4).choice(t, 48, replace=False)
+    rows.sort()
+    xh = synth.bits(x[torch.from_numpy(rows).to(dev)].contiguous())
+    ref = oracle_ref(xh, q, s, n, k, 1)
+    yr = out_f32(y[torch.from_numpy(rows).to(dev)].contiguous())
+    assert_bf16_close(yr, ref)
+
+
+@pytest.mark.parametrize("per_channel", [True, False])
+@pytest.mark.parametrize("n,k,t", [(256, 512, 33), (1024, 2048, 300)])
+def test_gemm_w8_parity(dev, per_channel, n, k, t):
+    q, s = synth.w8_host(n, k, seed=n + t, per_channel=per_channel)
+    if not per_channel:
+        s = s.reshape(n, k // 128)
+    w = ops.tile_w8(synth.to_dev(q), synth.to_dev(s, torch.float16), per_channel)
+    xh = synth.x_host(t, k, seed=t + 1)
+    ref = oracle_ref_w8(xh, q, s, n, k, per_channel)
+    y = out_f32(ops.gemm_w8(w, synth.to_dev(xh)))
+    assert err_ratio(y, ref) <= 1e-4
+    yb = out_f32(ops.gemm_w8(w, synth.to_dev(xh), out_bf16=True))
+    assert_bf16_close(yb, ref)
+
+
+def test_gemm_w8_baseline_shape_sampled(dev):
+    """BASELINE config 3 at M = 4096 (K = 2048, N = 8192, per-channel fp16 scales), sampled rows"""
+    n, k, t = 8192, 2048, 4096
+    q, s = synth.w8_host(n, k, seed=77, per_channel=True)
+    w = ops.tile_w8(synth.to_dev(q), synth.to_dev(s, torch.float16), True)
+    x = synth.x_dev(t, k, seed=78)
+    y = ops.gemm_w8(w, x, out_bf16=True)
+    torch.cuda.synchronize()
+    rows = np.sort(np.random.default_rng(5).choice(t, 48, replace=False))
+    sel = torch.from_numpy(rows).to(dev)
+    ref = oracle_ref_w8(synth.bits(x[sel].contiguous()), q, s, n, k, True)
+    assert_bf16_close(out_f32(y[sel].contiguous()), ref)
