@@ -118,6 +118,77 @@ def bench_gemm(m, n, k, steps=10, warmup=3, copies=2):
             "ms_kernel": round(ev_ms, 4)}
 
 
+def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=16):
+    """INT8 W8A16 per-channel: GEMV (m = 1) in GB/s, GEMM (m = 4096) in TFLOP/s"""
+    import torch
+    from qengine_amd import ops
+    g = torch.Generator(device="cuda")
+    g.manual_seed(400)
+    ws = []
+    for c in range(copies if m <= 16 else 2):
+        q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
+        s = (torch.randn(n, device="cuda", generator=g).abs() * 0.005).half()
+        ws.append(ops.tile_w8(q, s, per_channel=True))
+        del q
+    from qengine_amd import synth
+    x = synth.x_dev(m, k, seed=5)
+    y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
+    if m <= 16:
+        fn = lambda i: ops.gemv_w8(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    else:
+        fn = lambda i: ops.gemm_w8(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    _, ev_ms, _ = time_launches(fn, steps if m <= 16 else 10, warmup, len(ws))
+    del ws
+    torch.cuda.empty_cache()
+    if m <= 16:
+        b = n * k + 2 * n + 2 * m * k + 2 * m * n
+        return {"m": m, "gbs": round(b / (ev_ms * 1e-3) / 1e9, 1), "pct_hbm": round(100 * b / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
+                "us_kernel": round(ev_ms * 1e3, 2), "bytes": b}
+    flop = 2.0 * m * n * k
+    return {"m": m, "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 1),
+            "pct_bf16_peak": round(100 * flop / (ev_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 1), "ms_kernel": round(ev_ms, 4)}
+
+
+def bench_moe(Ts=(1, 16, 4096), E=512, topk=10, H=2048, I=512, nrout=8):
+    """MoE layer: route + segment + gate_up + down + combine per call, 8 rotating routings so the
+    hit experts change every call (the 830 MB of records exceed the Infinity Cache)"""
+    import torch
+    from qengine_amd import ops, synth
+    g = torch.Generator(device="cuda")
+    g.manual_seed(500)
+    gq = torch.randint(-2**31, 2**31 - 1, (E, 2 * I, H // 8), dtype=torch.int32, device="cuda", generator=g)
+    gs = (torch.randn(E, 2 * I, H // 128, device="cuda", generator=g).abs() * 0.02).half()
+    dq = torch.randint(-2**31, 2**31 - 1, (E, H, I // 8), dtype=torch.int32, device="cuda", generator=g)
+    ds = (torch.randn(E, H, I // 128, device="cuda", generator=g).abs() * 0.02).half()
+    moe = ops.MoE.pack(gq, gs, dq, ds, topk)
+    del gq, gs, dq, ds
+    torch.cuda.empty_cache()
+    res = {}
+    per_expert = 256 * H // 2 + 256 * (H // 128) * 2 + H * 64 + H * 2  # one group record
+    per_expert *= I // 128
+    for T in Ts:
+        lgs = [torch.randn(T, E, device="cuda", generator=g) for _ in range(nrout)]
+        x = synth.x_dev(T, H, seed=6)
+        y = torch.empty(T, H, dtype=torch.bfloat16, device="cuda")
+        hits = []
+        for lg in lgs:
+            sel, _ = ops.moe_route(lg, topk)
+            hits.append(int(torch.unique(sel).numel()))
+        fn = lambda i: moe(lgs[i], x, out_bf16=True, out=y)  # noqa: E731
+        steps = 100 if T <= 16 else 20
+        _, ev_ms, _ = time_launches(fn, steps, 5, nrout)
+        b = sum(hits) / len(hits) * per_expert + 4 * T * H
+        flop = 6.0 * T * topk * H * I
+        t_roof = max(b / (HBM_PEAK_GBS * 1e9), flop / (BF16_PEAK_TFLOPS * 1e12))
+        res[f"T{T}"] = {"us_layer": round(ev_ms * 1e3, 2), "experts_hit": round(sum(hits) / len(hits), 1),
+                        "gbs": round(b / (ev_ms * 1e-3) / 1e9, 1), "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 2),
+                        "roofline_frac": round(t_roof / (ev_ms * 1e-3), 3)}
+        del lgs, x, y
+    del moe
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(args, m=1, n=17408, k=5120):
     """oracle dequant (bf16_rn((u-8)*s)) + fp32 matmul, same workload shape, host cores, ~cpu_seconds of work"""
     import numpy as np
@@ -167,6 +238,9 @@ def main():
                                               "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2)}
         secondary["prefill_k5120_n17408"] = bench_gemm(8192, 17408, 5120)
         secondary["prefill_k17408_n5120"] = bench_gemm(8192, 5120, 17408)
+        secondary["w8_gemv_m1_k2048_n8192"] = bench_w8(1)
+        secondary["w8_gemm_m4096_k2048_n8192"] = bench_w8(4096)
+        secondary["moe_e512_top10_h2048_i512"] = bench_moe()
     cpu = None if args.no_cpu else cpu_baseline(args)
     achieved = g["gbs_kernel"]
     out = {

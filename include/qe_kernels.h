@@ -13,6 +13,7 @@
 #ifndef QE_KERNELS_H
 #define QE_KERNELS_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -107,6 +108,37 @@ void qe_gemv_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x
                    int flags, void* stream);
 void qe_gemm_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                    int flags, void* stream);
+
+/* ---- MoE grouped INT4 expert layer (one GPU, every expert local). No reference C-ABI exists for it: it replaces
+ * Worker::moe (reference src/flash/flash.cu:4842-5020) and its kernels k_topk_rows / k_jobs_pf / k_moe_* with the
+ * expert weights in the Flash-Next group-record format (src/flash/flash.h:203-218, fp16 scales): record (e, g) =
+ * [gq: 256 GLU rows x H W4][gs][dq: H rows x 128 W4][ds], NGRP = I / 128 records per expert, expert-major. ---- */
+
+/* top-k routing: sel int32 [T][topk], w fp32 [T][topk] = exp(l_i - l_max) / sum_sel exp(l_j - l_max); ties: lower
+ * expert index first (reference k_topk_rows, flash_kernels.cuh:4351-4399). E <= 1024, topk <= 32. */
+void qe_moe_route(const float* logits, int T, int E, int topk, int32_t* sel, float* w, void* stream);
+
+/* sort & segment (token, k) pairs by expert (reference k_jobs_pf, flash_kernels.cuh:6007-6100): off [E+1]; per slot
+ * (expert-major, ascending pair t*topk+k inside an expert): slot_pair, slot_tok, slot_w; inv [T*topk] = slot of a
+ * pair; jobs int32 [2 * n] = (expert, first row) of `chunk`-row jobs, njobs [1]. Deterministic. topk <= 16. */
+void qe_moe_segment(const int32_t* sel, const float* w, int T, int E, int topk, int chunk, int32_t* off,
+                    int32_t* slot_pair, int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs, int32_t* njobs,
+                    void* stream);
+
+/* device workspace of qe_moe_w4 for these sizes, and the bytes of one expert's records */
+size_t qe_moe_workspace_bytes(int T, int E, int topk, int H, int I);
+size_t qe_moe_record_bytes(int H, int I);
+
+/* one MoE layer: out [T][H] (fp32, or bf16 with QE_OUT_BF16) = sum_k w_k * down_e(silu(gate_e x) * up_e x) for the
+ * top-k experts e of each token; logits fp32 [T][E], x bf16 [T][H]. H % 512 == 0, I % 128 == 0. */
+void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
+               void* out, int flags, void* workspace, size_t ws_bytes, void* stream);
+
+/* load time: compressed-tensors experts -> group records (reference loader, src/flash/flash.cu:1555-1611).
+ * gate_up int32 [E][2I][H/8] (gate rows then up rows) + fp16 [E][2I][H/128]; down int32 [E][H][I/8] + fp16
+ * [E][H][I/128]; records: E * qe_moe_record_bytes(H, I) bytes. Synchronizes the stream. */
+void qe_moe_pack_w4(const int32_t* gu_q, const uint16_t* gu_s, const int32_t* dn_q, const uint16_t* dn_s, int E, int H,
+                    int I, void* records, void* stream);
 
 #ifdef __cplusplus
 }

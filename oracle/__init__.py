@@ -198,3 +198,53 @@ def silu_mul(a, b):
     a = np.asarray(a, np.float32)
     b = np.asarray(b, np.float32)
     return (a / (np.float32(1) + np.exp(-a)) * b).astype(np.float32)
+
+
+def moe_pack(gu_q, gu_s, dn_q, dn_s, E, H, I):
+    """compressed-tensors experts -> the group records (uint8 bytes), restated from the reference loader
+    (flash.cu:1555-1611): per (e, g) gather gate/up rows of group g, GLU-interleave, repack; gather down columns,
+    repack. Record layout [gq][gs][dq][ds] (flash.h:203-218)."""
+    ngrp = I // 128
+    out = []
+    for e in range(E):
+        for g in range(ngrp):
+            rows = np.concatenate([np.arange(g * 128, g * 128 + 128), I + np.arange(g * 128, g * 128 + 128)])
+            q = gu_q[e][rows]
+            s = gu_s[e][rows]
+            qg, sg = glu_rows(q, s, 256, H)
+            gq, gs = repack_w4(qg, sg, 256, H)
+            dq_src = np.ascontiguousarray(dn_q[e][:, g * 16:(g + 1) * 16])
+            ds_src = np.ascontiguousarray(dn_s[e][:, g:g + 1])
+            dq, ds = repack_w4(dq_src, ds_src, H, 128)
+            out += [gq.view(np.uint8), gs.view(np.uint8), dq.view(np.uint8), ds.view(np.uint8)]
+    return np.concatenate(out)
+
+
+def moe_ref(logits, x, gu_q, gu_s, dn_q, dn_s, topk, H, I, tokens=None, exact=False):
+    """one MoE layer in float64: out[t] = sum_k w_k * down_e(silu(gate_e x) * up_e x) with (sel, w) from moe_route,
+    on the bf16-dequantized experts (exact: the unrounded (u - 8) * s); tokens: subset of rows (default all).
+    Returns (out [len(tokens)][H], sel, w)."""
+    sel, w = moe_route(logits, topk)
+    T = logits.shape[0]
+    tokens = np.arange(T) if tokens is None else np.asarray(tokens)
+    xf = bf16_to_f32(x).astype(np.float64)
+    cache = {}
+
+    def deq(q, s, n, k):
+        if exact:
+            return unpack_w4(q, n, k).astype(np.float64) * np.repeat(f16_to_f32(s), 128, axis=1)
+        return bf16_to_f32(dequant_w4(q, s, n, k, 1)).astype(np.float64)
+
+    def expert(e):
+        if e not in cache:
+            cache[e] = (deq(gu_q[e], gu_s[e], 2 * I, H), deq(dn_q[e], dn_s[e], H, I))
+        return cache[e]
+
+    out = np.zeros((len(tokens), H))
+    for r, t in enumerate(tokens):
+        for k in range(topk):
+            wgu, wdn = expert(int(sel[t, k]))
+            gu = wgu @ xf[t]
+            act = gu[:I] / (1 + np.exp(-gu[:I])) * gu[I:]
+            out[r] += float(w[t, k]) * (wdn @ act)
+    return out, sel, w

@@ -8,54 +8,16 @@
 //   LDS: two stages of X [128][64] and W [128][64] bf16, rows of 128 B with the 16-byte chunks XOR-swizzled by
 //        (row % 8) so the MFMA fragment reads (32 rows x 16 B per half-wave) spread over the banks
 //   pipeline: the global loads of step k + 1 are issued before the MFMAs of step k; one barrier per step.
-#include "qe_api.hpp"
+#include "mfma_tile.hpp"
 
 namespace {
 
-typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
+using namespace qe_tile;
 constexpr int BM = 128, BN = 128, BK = 64, NTH = 256;
 constexpr int kStageBytes = (BM + BN) * BK * 2;  // 32 KB
 
 enum Fmt : int { kFmtW4 = 0, kFmtW8G = 1, kFmtW8C = 2 };
 enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
-
-// byte offset of the 16-byte chunk `c` (0..7) of row `r` in a [rows][64] bf16 tile
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
-
-template <int SDT>
-__device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
-    if constexpr (SDT >= 0) return scale_to_f32<SDT>(v);
-    else return sdt == kScaleF16 ? scale_to_f32<kScaleF16>(v) : scale_to_f32<kScaleBF16>(v);
-}
-
-// dequantize the 8 nibbles of one W4 word (rows g / g + 8, k0 + {0, 1, 8, 9}) and store them as 4 bf16 pairs
-__device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k0) {
-    const uint32_t ev = wd & 0x0F0F0F0Fu;         // bytes: slots 0, 2, 4, 6 (row g: k0, k0+8, k0+1, k0+9)
-    const uint32_t od = (wd >> 4) & 0x0F0F0F0Fu;  // slots 1, 3, 5, 7 (row g + 8)
-    const float b_lo = -8.f * s_lo, b_hi = -8.f * s_hi;
-    // (u - 8) * s = fma(u, s, -8 s): exact in fp32, then one rounding to bf16
-    const uint32_t g0 = pack_bf16x2(fmaf((float)(ev & 0xff), s_lo, b_lo), fmaf((float)((ev >> 16) & 0xff), s_lo, b_lo));
-    const uint32_t g8 = pack_bf16x2(fmaf((float)((ev >> 8) & 0xff), s_lo, b_lo), fmaf((float)(ev >> 24), s_lo, b_lo));
-    const uint32_t h0 = pack_bf16x2(fmaf((float)(od & 0xff), s_hi, b_hi), fmaf((float)((od >> 16) & 0xff), s_hi, b_hi));
-    const uint32_t h8 = pack_bf16x2(fmaf((float)((od >> 8) & 0xff), s_hi, b_hi), fmaf((float)(od >> 24), s_hi, b_hi));
-    // k0 = 16 j + 2 t: pair (k0, k0+1) lives in chunk k0 / 8, byte (k0 % 8) * 2
-    const int c0 = k0 >> 3, o0 = (k0 & 7) * 2;
-    *reinterpret_cast<uint32_t*>(wt + swz(row, c0) + o0) = g0;
-    *reinterpret_cast<uint32_t*>(wt + swz(row, c0 + 1) + o0) = g8;
-    *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c0) + o0) = h0;
-    *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c0 + 1) + o0) = h8;
-}
-
-// one INT8 dword: bytes (g, k) (g, k+1) (g+8, k) (g+8, k+1)
-__device__ __forceinline__ void dq_w8_dword(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k) {
-    const uint32_t u = wd ^ 0x80808080u;  // w + 128
-    const float b_lo = -128.f * s_lo, b_hi = -128.f * s_hi;
-    const uint32_t g = pack_bf16x2(fmaf((float)(u & 0xff), s_lo, b_lo), fmaf((float)((u >> 8) & 0xff), s_lo, b_lo));
-    const uint32_t h = pack_bf16x2(fmaf((float)((u >> 16) & 0xff), s_hi, b_hi), fmaf((float)(u >> 24), s_hi, b_hi));
-    const int c = k >> 3, o = (k & 7) * 2;
-    *reinterpret_cast<uint32_t*>(wt + swz(row, c) + o) = g;
-    *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c) + o) = h;
-}
 
 template <int FMT, int SDT>
 __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,

@@ -65,51 +65,45 @@ __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
     else return sdt == kScaleF16 ? scale_to_f32<kScaleF16>(v) : scale_to_f32<kScaleBF16>(v);
 }
 
-// NG > 0: every slice has exactly NG groups (G = NG * S). NG == 0: slices of G / S groups (<= kGenericNG).
+// One block computes the 16 rows of one weight tile for up to MT activation rows; wave w owns K slice w (NG
+// groups, NG == 0: ng groups, <= kGenericNG). The caller supplies, per wave, the first weight record of the slice
+// (qp: uint4 of lane 0 of the slice's first group; W4: groups 64 uint4 apart, W8: 128), the slice's 16-bit scales
+// (sp: [ng][16] rows of the tile, W8C: [16]) and, per activation row, the dword pointer of the slice's first group
+// (xw[tok], 64 dwords per group). On return (after a barrier) red[S][2][MT][16] holds the partial sums; rsum()
+// below adds them in a fixed order.
 // SDT < 0: scale dtype chosen at run time (`sdt`). PF: the activation dwords of every group are loaded up front,
-// interleaved with the weight loads of the same group (w_i, x_i, s_i, ...), so the activation latency hides
-// behind the weight latency; else they are loaded when the group is reached (large m).
-// Dynamic LDS: per wave xl [MT][64] u32 + xsum [MT][8] (one group at a time) + the slice's 16-bit scales
-// [NGM][16] (W8C: [16]), then red [S][2][MT][16].
+// interleaved with the weight loads of the same group (w_i, x_i, ...), so the activation latency hides behind the
+// weight latency; else they are loaded when the group is reached (large m).
+// LDS (`lds`): per wave xl [MT][64] u32 + xsum [MT][8] + the slice's scales [NGM][16] half, then red.
 template <int MT, int FMT, int SDT, int NG, bool PF>
-__global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
-__attribute__((amdgpu_waves_per_eu(MT == 1 ? 6 : MT == 2 ? 5 : 1))) gemv_kernel(
-    const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K, const uint16_t* __restrict__ x,
-    int ldx, void* __restrict__ y, int ldy, int m, int out, int sdt) {
+__device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restrict__ qp, const uint16_t* __restrict__ sp,
+                                            const uint32_t* const* xw, int m, int ng, int sdt) {
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
     constexpr int LPG = FMT == kFmtW4 ? 1 : 2;  // wave-loads per group
-    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-
     const int S = blockDim.x >> 6;
     const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
     constexpr int WSZ = MT * 72 + NGM * 8;  // dwords of LDS per wave
-    uint32_t* xl = lds + (size_t)w * WSZ;                   // [MT][64]
-    float* xsum = reinterpret_cast<float*>(xl + MT * 64);   // [MT][8]
+    uint32_t* xl = lds + (size_t)w * WSZ;                        // [MT][64]
+    float* xsum = reinterpret_cast<float*>(xl + MT * 64);        // [MT][8]
     uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + MT * 72);  // [NGM][16] scales of the slice
     float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][2][MT][16]
-    const int tile = blockIdx.x;
-    const int G = K >> 7;
-    const int gb = NG > 0 ? w * NG : w * G / S;
-    const int ng = NG > 0 ? NG : (w + 1) * G / S - gb;
     const int g = (L >> 2) & 7, t = L & 3, h = L >> 5;
+    if (NG > 0) ng = NG;
 
     // activation dword of this lane in the class-major staging: class c = L / 8, slot L % 8
     const int c_st = L >> 3, sl_st = L & 7;
-    const uint32_t* xw = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64 + x_dword<FMT>(c_st, sl_st);
-    auto ldx_group = [&](int tok, int i) { return tok < m ? xw[(size_t)tok * (ldx >> 1) + i * 64] : 0u; };
+    const int xoff = x_dword<FMT>(c_st, sl_st);
+    auto ldx_group = [&](int tok, int i) { return tok < m ? xw[tok][i * 64 + xoff] : 0u; };
 
-    // 1. loads, per group in the order they are consumed (vmcnt retires in order)
-    const uint4* qp = FMT == kFmtW4 ? q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + L
-                                    : q + ((size_t)tile * (K >> 5) + 4 * gb) * 32 + L;
-    // the slice's scales: 16 per group (W8C: 16 per tile) as one dword per lane, staged in LDS
+    // 1. loads, per group in the order they are consumed (vmcnt retires in order); the scales first, one dword
+    //    per lane, staged in LDS
     {
         const int ndw = FMT == kFmtW8C ? 8 : ng * 8;
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(FMT == kFmtW8C ? s + 16 * tile
-                                                                            : s + ((size_t)tile * G + gb) * 16);
-        if (L < ndw) reinterpret_cast<uint32_t*>(sl16)[L] = sp[L];
+        if (L < ndw) reinterpret_cast<uint32_t*>(sl16)[L] = reinterpret_cast<const uint32_t*>(sp)[L];
     }
     u32x4_v wv[NGM][LPG];
     uint32_t xr[PF ? MT : 1][PF ? NGM : 1];
+    qp += L;
 #pragma unroll
     for (int i = 0; i < NGM; i++) {
         if (NG == 0 && i >= ng) break;
@@ -209,7 +203,7 @@ __attribute__((amdgpu_waves_per_eu(MT == 1 ? 6 : MT == 2 ? 5 : 1))) gemv_kernel(
         }
     }
 
-    // 3. rows g / g + 8: lanes t (DPP quad swaps), then half-waves and slices through LDS, fixed order
+    // 3. rows g / g + 8: lanes t (DPP quad swaps), then half-waves and slices through LDS (rsum)
 #pragma unroll
     for (int tok = 0; tok < MT; tok++) {
         float a = dpp_add<kDppXor1>(acc_lo[tok]);
@@ -222,23 +216,52 @@ __attribute__((amdgpu_waves_per_eu(MT == 1 ? 6 : MT == 2 ? 5 : 1))) gemv_kernel(
         }
     }
     __syncthreads();
-    auto rsum = [&](int tok, int rr) {
-        float v = 0.f;
-        for (int ws = 0; ws < S; ws++)
-            v += red[((ws * 2) * MT + tok) * 16 + rr] + red[((ws * 2 + 1) * MT + tok) * 16 + rr];
-        return v;
-    };
+    return red;
+}
+
+// sum of row rr (0..15) for activation row tok over the S slices and both half-waves, in a fixed order
+template <int MT>
+__device__ __forceinline__ float rsum(const float* red, int S, int tok, int rr) {
+    float v = 0.f;
+    for (int ws = 0; ws < S; ws++) v += red[((ws * 2) * MT + tok) * 16 + rr] + red[((ws * 2 + 1) * MT + tok) * 16 + rr];
+    return v;
+}
+
+template <int MT, int NG>
+constexpr size_t gemv_lds_bytes(int S) {
+    return (size_t)S * (MT * 72 + (NG > 0 ? NG : kGenericNG) * 8) * 4 + (size_t)S * 2 * MT * 16 * 4;
+}
+
+// Plain decode GEMV: one block per 16-row tile of a tile-major matrix, K slices of NG groups.
+template <int MT, int FMT, int SDT, int NG, bool PF>
+__global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
+__attribute__((amdgpu_waves_per_eu(MT == 1 ? 6 : MT == 2 ? 5 : 1))) gemv_kernel(
+    const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K, const uint16_t* __restrict__ x,
+    int ldx, void* __restrict__ y, int ldy, int m, int out, int sdt) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6;
+    const int tile = blockIdx.x, G = K >> 7;
+    const int gb = NG > 0 ? w * NG : w * G / S;
+    const int ng = NG > 0 ? NG : (w + 1) * G / S - gb;
+    const uint4* qp = FMT == kFmtW4 ? q + ((size_t)tile * (K >> 6) + 2 * gb) * 32
+                                    : q + ((size_t)tile * (K >> 5) + 4 * gb) * 32;
+    const uint16_t* sp = FMT == kFmtW8C ? s + 16 * tile : s + ((size_t)tile * G + gb) * 16;
+    const uint32_t* xw[MT];
+#pragma unroll
+    for (int tok = 0; tok < MT; tok++)
+        xw[tok] = reinterpret_cast<const uint32_t*>(x) + (size_t)(tok < m ? tok : 0) * (ldx >> 1) + (size_t)gb * 64;
+    const float* red = gemv_tile<MT, FMT, SDT, NG, PF>(lds, qp, sp, xw, m, ng, sdt);
     const int row0 = 16 * tile;
     if (out == kOutGLU) {
         for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
             const int tok = idx >> 3, gg = idx & 7;
             reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 / 2 + gg] =
-                f32_to_bf16(silu_f32(rsum(tok, gg)) * rsum(tok, gg + 8));
+                f32_to_bf16(silu_f32(rsum<MT>(red, S, tok, gg)) * rsum<MT>(red, S, tok, gg + 8));
         }
     } else {
         for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
             const int tok = idx >> 4, rr = idx & 15;
-            const float v = rsum(tok, rr);
+            const float v = rsum<MT>(red, S, tok, rr);
             if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 + rr] = f32_to_bf16(v);
             else reinterpret_cast<float*>(y)[(size_t)tok * ldy + row0 + rr] = v;
         }
@@ -259,7 +282,7 @@ void launch_gemv(const uint4* q, const uint16_t* s, int n, int k, const uint16_t
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
     const int ngm = sc.ng > 0 ? sc.ng : kGenericNG;
     const bool pf = mt * ngm <= 16;  // activation prefetch registers
-    const size_t lds = (size_t)sc.S * (mt * 72 + ngm * 8) * 4 + (size_t)sc.S * 2 * mt * 16 * 4;
+    const size_t lds = (size_t)sc.S * (mt * 72 + ngm * 8) * 4 + (size_t)sc.S * 2 * mt * 16 * 4;  // gemv_lds_bytes
     const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);
 #define QE_GEMV_K(MT_, NG_, PF_) \
     gemv_kernel<MT_, FMT, SDT, NG_, PF_><<<grid, block, lds, st>>>(q, s, n, k, x, ldx, y, ldy, m, out, sdt)

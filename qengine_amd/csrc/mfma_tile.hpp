@@ -1,0 +1,53 @@
+// Shared pieces of the MFMA matmul kernels (prefill GEMM, MoE grouped GEMMs): the swizzled [rows][64] bf16 LDS
+// tile and the in-register dequantization of W4 / W8 records to the reference's bf16 operand.
+#pragma once
+#include "qe_api.hpp"
+
+namespace qe_tile {
+
+typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
+
+// byte offset of the 16-byte chunk `c` (0..7) of row `r` in a [rows][64] bf16 tile: 128-byte rows, chunks XOR-swizzled
+// by (row % 8) so that MFMA fragment reads (32 rows x 16 B per half-wave) spread over the LDS banks
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+
+template <int SDT>
+__device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
+    if constexpr (SDT >= 0) return scale_to_f32<SDT>(v);
+    else return sdt == kScaleF16 ? scale_to_f32<kScaleF16>(v) : scale_to_f32<kScaleBF16>(v);
+}
+
+// dequantize the 8 nibbles of one W4 word (rows g / g + 8, k0 + {0, 1, 8, 9}) to bf16_rn((u - 8) * s) and store them
+// as 4 bf16 pairs at (row, k0) (row, k0 + 8) (row + 8, k0) (row + 8, k0 + 8) of the tile
+__device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k0) {
+    const uint32_t ev = wd & 0x0F0F0F0Fu;         // bytes: slots 0, 2, 4, 6 (row g: k0, k0+8, k0+1, k0+9)
+    const uint32_t od = (wd >> 4) & 0x0F0F0F0Fu;  // slots 1, 3, 5, 7 (row g + 8)
+    const float b_lo = -8.f * s_lo, b_hi = -8.f * s_hi;
+    // (u - 8) * s = fma(u, s, -8 s): exact in fp32, then one rounding to bf16
+    const uint32_t g0 = pack_bf16x2(fmaf((float)(ev & 0xff), s_lo, b_lo), fmaf((float)((ev >> 16) & 0xff), s_lo, b_lo));
+    const uint32_t g8 = pack_bf16x2(fmaf((float)((ev >> 8) & 0xff), s_lo, b_lo), fmaf((float)(ev >> 24), s_lo, b_lo));
+    const uint32_t h0 = pack_bf16x2(fmaf((float)(od & 0xff), s_hi, b_hi), fmaf((float)((od >> 16) & 0xff), s_hi, b_hi));
+    const uint32_t h8 = pack_bf16x2(fmaf((float)((od >> 8) & 0xff), s_hi, b_hi), fmaf((float)(od >> 24), s_hi, b_hi));
+    // k0 = 16 j + 2 t: pair (k0, k0+1) lives in chunk k0 / 8, byte (k0 % 8) * 2
+    const int c0 = k0 >> 3, o0 = (k0 & 7) * 2;
+    *reinterpret_cast<uint32_t*>(wt + swz(row, c0) + o0) = g0;
+    *reinterpret_cast<uint32_t*>(wt + swz(row, c0 + 1) + o0) = g8;
+    *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c0) + o0) = h0;
+    *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c0 + 1) + o0) = h8;
+}
+
+// one INT8 dword of the W8 layout: bytes (g, k) (g, k+1) (g+8, k) (g+8, k+1) -> bf16_rn(w * s)
+__device__ __forceinline__ void dq_w8_dword(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k) {
+    const uint32_t u = wd ^ 0x80808080u;  // w + 128
+    const float b_lo = -128.f * s_lo, b_hi = -128.f * s_hi;
+    const uint32_t g = pack_bf16x2(fmaf((float)(u & 0xff), s_lo, b_lo), fmaf((float)((u >> 8) & 0xff), s_lo, b_lo));
+    const uint32_t h = pack_bf16x2(fmaf((float)((u >> 16) & 0xff), s_hi, b_hi), fmaf((float)(u >> 24), s_hi, b_hi));
+    const int c = k >> 3, o = (k & 7) * 2;
+    *reinterpret_cast<uint32_t*>(wt + swz(row, c) + o) = g;
+    *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c) + o) = h;
+}
+
+// 32x32 MFMA C fragment: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 for r = 0..15
+__device__ __forceinline__ int c_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
+
+}  // namespace qe_tile

@@ -1,0 +1,555 @@
+// MoE grouped INT4 expert layer on one GPU: router -> sort & segment tokens by expert -> grouped gate_up (GLU,
+// routing weight) -> grouped down -> fixed-order combine.
+//
+// Expert weights use the reference's Flash-Next group-record format (flash.h:203-218): every expert's intermediate
+// dimension I is split into NGRP = I / 128 groups; record (e, g) is
+//   gq [256 rows x H] W4 (gate rows 128 g .. +128 and the matching up rows, GLU-interleaved per 16-row tile)
+//   gs fp16 W4 scales, dq [H rows x 128] W4 (down columns 128 g .. +128), ds fp16 W4 scales,
+// and records are stored expert-major (record index e * NGRP + g). On one GPU every group is local.
+//
+// Routing (reference k_topk_rows, flash_kernels.cuh:4351-4399): top-k logits per token, ties to the lower expert
+// index, weights exp(l_i - l_max) / sum_sel exp(l_j - l_max). Segmentation (reference k_jobs_pf, :6007-6100) is a
+// counting sort whose order inside an expert is ascending (token, k) (the reference's atomics leave it open):
+// tokens are processed in chunks of 64 with per-expert 64-bit token masks, so every slot is a pure function of
+// the routing. The per-(token, k) down outputs go to bf16 slots summed in k order (reference k_moe_sum,
+// :6436-6482), so the layer is deterministic.
+//
+// Decode (T <= 32): the grouped GEMVs reuse the decode GEMV tile (gemv_impl.hpp) with gathered activation rows,
+// jobs = (expert, chunk of <= 2 rows). Prefill: grouped MFMA GEMMs over (expert, 64-row tile) jobs.
+#include "gemv_impl.hpp"
+#include "mfma_tile.hpp"
+#include "../../include/qe_kernels.h"
+
+#include <vector>
+
+namespace {
+
+using namespace qe_gemv;
+
+struct MoeShape {
+    int E, topk, H, I, ngrp;
+    size_t gg_q, gg_s, gd_q, gd_s, rec;  // bytes of the record parts and of a record
+};
+
+MoeShape moe_shape(int E, int topk, int H, int I) {
+    MoeShape s;
+    s.E = E;
+    s.topk = topk;
+    s.H = H;
+    s.I = I;
+    s.ngrp = I / 128;
+    s.gg_q = (size_t)256 * H / 2;
+    s.gg_s = (size_t)256 * (H / 128) * 2;
+    s.gd_q = (size_t)H * 128 / 2;
+    s.gd_s = (size_t)H * 2;
+    s.rec = s.gg_q + s.gg_s + s.gd_q + s.gd_s;
+    return s;
+}
+
+__device__ __forceinline__ const char* rec_ptr(const char* recs, const MoeShape& sh, int e, int g) {
+    return recs + ((size_t)e * sh.ngrp + g) * sh.rec;
+}
+
+// ------------------------------------------------------------------ router: one block (256 threads) per token
+constexpr int kRouteThreads = 256;
+constexpr int kMaxExperts = 1024;
+
+__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int E, int topk,
+                                                                  int32_t* __restrict__ sel, float* __restrict__ w) {
+    __shared__ float bv[kRouteThreads / 64];
+    __shared__ int bi[kRouteThreads / 64];
+    __shared__ float sv[32];
+    __shared__ int si[32];
+    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    constexpr int PER = kMaxExperts / kRouteThreads;
+    float v[PER];
+    const float* l = logits + (size_t)t * E;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int e = tid + i * kRouteThreads;
+        v[i] = e < E ? l[e] : -INFINITY;
+    }
+    unsigned taken = 0;
+    for (int k = 0; k < topk; k++) {
+        // this thread's best untaken expert (value desc, index asc: its own experts come in ascending order)
+        float bvv = -INFINITY;
+        int bii = 0x7fffffff;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const int e = tid + i * kRouteThreads;
+            if (e < E && !(taken >> i & 1u) && (v[i] > bvv || bii == 0x7fffffff)) {
+                bvv = v[i];
+                bii = e;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float v2 = __shfl_xor(bvv, o);
+            const int i2 = __shfl_xor(bii, o);
+            if (v2 > bvv || (v2 == bvv && i2 < bii)) {
+                bvv = v2;
+                bii = i2;
+            }
+        }
+        if (lane == 0) {
+            bv[wave] = bvv;
+            bi[wave] = bii;
+        }
+        __syncthreads();
+        float V = bv[0];
+        int I = bi[0];
+#pragma unroll
+        for (int q = 1; q < kRouteThreads / 64; q++)
+            if (bv[q] > V || (bv[q] == V && bi[q] < I)) {
+                V = bv[q];
+                I = bi[q];
+            }
+        if (I % kRouteThreads == tid) taken |= 1u << (I / kRouteThreads);
+        if (tid == 0) {
+            sv[k] = V;
+            si[k] = I;
+        }
+        __syncthreads();
+    }
+    if (tid < topk) {
+        float tot = 0.f;
+        for (int k = 0; k < topk; k++) tot += expf(sv[k] - sv[0]);
+        sel[(size_t)t * topk + tid] = si[tid];
+        w[(size_t)t * topk + tid] = expf(sv[tid] - sv[0]) / tot;
+    }
+}
+
+// ------------------------------------------------------------------ sort & segment: one block
+constexpr int kSegThreads = 1024;
+constexpr int kSegChunk = 64;  // tokens per chunk (64-bit masks)
+
+// out: off [E+1]; per slot: pair (t * topk + k), token, weight; inv [pair] = slot; jobs (expert, first row) of
+// `chunk` rows each, njobs
+__global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t* __restrict__ sel,
+                                                                  const float* __restrict__ w, int T, int E, int topk,
+                                                                  int chunk, int32_t* __restrict__ off,
+                                                                  int32_t* __restrict__ slot_pair,
+                                                                  int32_t* __restrict__ slot_tok,
+                                                                  float* __restrict__ slot_w, int32_t* __restrict__ inv,
+                                                                  int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
+    __shared__ int cnt[kMaxExperts], pre[kMaxExperts + 1], jpre[kMaxExperts + 1], fill[kMaxExperts];
+    __shared__ unsigned long long mark[kMaxExperts];
+    const int tid = threadIdx.x;
+    const int P = T * topk;
+    for (int e = tid; e < E; e += kSegThreads) {
+        cnt[e] = 0;
+        fill[e] = 0;
+    }
+    __syncthreads();
+    for (int i = tid; i < P; i += kSegThreads) atomicAdd(&cnt[sel[i]], 1);
+    __syncthreads();
+    if (tid == 0) {  // exclusive scans over E <= 1024 entries (one thread: ~E additions)
+        int a = 0, b = 0;
+        for (int e = 0; e < E; e++) {
+            pre[e] = a;
+            jpre[e] = b;
+            a += cnt[e];
+            b += (cnt[e] + chunk - 1) / chunk;
+        }
+        pre[E] = a;
+        jpre[E] = b;
+        *njobs = b;
+    }
+    __syncthreads();
+    for (int e = tid; e <= E; e += kSegThreads) off[e] = pre[e];
+    for (int e = tid; e < E; e += kSegThreads) {
+        const int nj = (cnt[e] + chunk - 1) / chunk;
+        for (int j = 0; j < nj; j++) {
+            jobs[2 * (jpre[e] + j)] = e;
+            jobs[2 * (jpre[e] + j) + 1] = j * chunk;
+        }
+    }
+    for (int t0 = 0; t0 < T; t0 += kSegChunk) {
+        for (int e = tid; e < E; e += kSegThreads) mark[e] = 0ull;
+        __syncthreads();
+        const int tl = tid / topk;  // token of this thread within the chunk (topk <= 16)
+        const int p = t0 * topk + tid;
+        const bool act = tl < kSegChunk && t0 + tl < T;
+        int e = 0;
+        if (act) {
+            e = sel[p];
+            atomicOr(&mark[e], 1ull << tl);
+        }
+        __syncthreads();
+        if (act) {
+            const int slot = pre[e] + fill[e] + __popcll(mark[e] & ((1ull << tl) - 1ull));
+            slot_pair[slot] = p;
+            slot_tok[slot] = t0 + tl;
+            slot_w[slot] = w[p];
+            inv[p] = slot;
+        }
+        __syncthreads();
+        for (int e2 = tid; e2 < E; e2 += kSegThreads) fill[e2] += __popcll(mark[e2]);
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------------ decode grouped GEMVs (gemv_tile)
+constexpr int kDecRows = 2;  // rows per decode job
+
+// gate_up: block (job, record g * 16 + 16-row tile); S = G / NG waves over K = H
+template <int MT, int NG>
+__global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
+    const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ x, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ slot_tok, const float* __restrict__ slot_w, const int32_t* __restrict__ jobs,
+    const int32_t* __restrict__ njobs, uint16_t* __restrict__ act) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const int job = blockIdx.x;
+    if (job >= *njobs) return;
+    const int e = jobs[2 * job], r0 = jobs[2 * job + 1];
+    const int slot0 = off[e] + r0, m = min(MT, off[e + 1] - slot0);
+    const int g = blockIdx.y >> 4, tile = blockIdx.y & 15;
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6;
+    const int G = sh.H >> 7, gb = w * NG;
+    const char* rp = rec_ptr(recs, sh, e, g);
+    const uint4* qp = reinterpret_cast<const uint4*>(rp) + ((size_t)tile * (sh.H >> 6) + 2 * gb) * 32;
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q) + ((size_t)tile * G + gb) * 16;
+    const uint32_t* xw[MT];
+#pragma unroll
+    for (int r = 0; r < MT; r++)
+        xw[r] = reinterpret_cast<const uint32_t*>(x + (size_t)slot_tok[slot0 + (r < m ? r : 0)] * sh.H) + gb * 64;
+    const float* red = gemv_tile<MT, kFmtW4, kScaleF16, NG, true>(lds, qp, sp, xw, m, NG, kScaleF16);
+    for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
+        const int r = idx >> 3, gg = idx & 7;
+        const float v = silu_f32(rsum<MT>(red, S, r, gg)) * rsum<MT>(red, S, r, gg + 8) * slot_w[slot0 + r];
+        act[(size_t)(slot0 + r) * sh.I + g * 128 + tile * 8 + gg] = f32_to_bf16(v);
+    }
+}
+
+// down: block (job, 16-row tile of H); wave g = record g (K = 128 each)
+template <int MT>
+__global__ void __launch_bounds__(64 * kMaxWavesGeneric) moe_dec_down_kernel(
+    const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ act, const int32_t* __restrict__ off,
+    const int32_t* __restrict__ jobs, const int32_t* __restrict__ njobs, uint16_t* __restrict__ slot_out) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const int job = blockIdx.x;
+    if (job >= *njobs) return;
+    const int e = jobs[2 * job], r0 = jobs[2 * job + 1];
+    const int slot0 = off[e] + r0, m = min(MT, off[e + 1] - slot0);
+    const int tile = blockIdx.y;
+    const int S = blockDim.x >> 6, g = threadIdx.x >> 6;
+    const char* rp = rec_ptr(recs, sh, e, g);
+    const uint4* qp = reinterpret_cast<const uint4*>(rp + sh.gg_q + sh.gg_s) + (size_t)tile * 2 * 32;
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q) + (size_t)tile * 16;
+    const uint32_t* xw[MT];
+#pragma unroll
+    for (int r = 0; r < MT; r++)
+        xw[r] = reinterpret_cast<const uint32_t*>(act + (size_t)(slot0 + (r < m ? r : 0)) * sh.I) + g * 64;
+    const float* red = gemv_tile<MT, kFmtW4, kScaleF16, 1, true>(lds, qp, sp, xw, m, 1, kScaleF16);
+    for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
+        const int r = idx >> 4, rr = idx & 15;
+        slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_bf16(rsum<MT>(red, S, r, rr));
+    }
+}
+
+// ------------------------------------------------------------------ prefill grouped GEMMs (MFMA)
+constexpr int PBM = 64, PBN = 128, PBK = 64, PNTH = 256;
+constexpr int kPStage = (PBM + PBN) * PBK * 2;  // 24 KB
+
+// MODE 0: gate_up, block (job, record g * 2 + half): rows 128 half .. +128 of gq, K = H, A = x[token(slot)]
+// MODE 1: down, block (job, 128-row tile of H): K = I over the NGRP records, A = act[slot]
+template <int MODE>
+__global__ void __launch_bounds__(PNTH) moe_pf_kernel(const char* __restrict__ recs, MoeShape sh,
+                                                      const uint16_t* __restrict__ a_src,
+                                                      const int32_t* __restrict__ off,
+                                                      const int32_t* __restrict__ slot_tok,
+                                                      const float* __restrict__ slot_w,
+                                                      const int32_t* __restrict__ jobs,
+                                                      const int32_t* __restrict__ njobs, uint16_t* __restrict__ out) {
+    using namespace qe_tile;
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    char* plds = reinterpret_cast<char*>(lds);
+    const int job = blockIdx.x;
+    if (job >= *njobs) return;
+    const int e = jobs[2 * job], r0 = jobs[2 * job + 1];
+    const int slot0 = off[e] + r0, rows = min(PBM, off[e + 1] - slot0);
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int K = MODE == 0 ? sh.H : sh.I, KT = K / PBK, lda = K;
+
+    // A rows: 64 x 64 bf16 per step, 2 x 16 B per thread
+    const uint16_t* arow[2];
+    int ach[2], arr[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int idx = tid + i * PNTH;
+        arr[i] = idx >> 3;
+        ach[i] = idx & 7;
+        const int sl = slot0 + (arr[i] < rows ? arr[i] : 0);
+        arow[i] = a_src + (size_t)(MODE == 0 ? slot_tok[sl] : sl) * lda;
+    }
+    // W: 8 tiles of 16 rows, one 16 B record per thread
+    const int tr = tid >> 5, wl = tid & 31, wg = wl >> 2, wt4 = wl & 3, wrow = tr * 16 + wg;
+    const int G = sh.H >> 7;
+    u32x4_v ar[2], wr;
+    uint16_t sr_lo, sr_hi;
+    auto load = [&](int kt) {
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            ar[i] = arr[i] < rows ? *reinterpret_cast<const u32x4_v*>(arow[i] + kt * PBK + ach[i] * 8)
+                                  : u32x4_v{0u, 0u, 0u, 0u};
+        const uint4* qp;
+        const uint16_t* sp;
+        if constexpr (MODE == 0) {
+            const char* rp = rec_ptr(recs, sh, e, blockIdx.y >> 1);
+            const int tile = (blockIdx.y & 1) * 8 + tr;
+            qp = reinterpret_cast<const uint4*>(rp) + ((size_t)tile * (sh.H >> 6) + kt) * 32 + wl;
+            sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q) + ((size_t)tile * G + (kt >> 1)) * 16;
+        } else {
+            const char* rp = rec_ptr(recs, sh, e, kt >> 1);
+            const int tile = blockIdx.y * 8 + tr;
+            qp = reinterpret_cast<const uint4*>(rp + sh.gg_q + sh.gg_s) + ((size_t)tile * 2 + (kt & 1)) * 32 + wl;
+            sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q) + (size_t)tile * 16;
+        }
+        wr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(qp));
+        sr_lo = sp[wg];
+        sr_hi = sp[wg + 8];
+    };
+    auto store = [&](char* at, char* wt) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) *reinterpret_cast<u32x4_v*>(at + swz(arr[i], ach[i])) = ar[i];
+        const float s_lo = scale_to_f32<kScaleF16>(sr_lo), s_hi = scale_to_f32<kScaleF16>(sr_hi);
+#pragma unroll
+        for (int j = 0; j < 4; j++) dq_w4_word(wr[j], s_lo, s_hi, wt, wrow, 16 * j + 2 * wt4);
+    };
+
+    // waves 2 x 2: rows wm * 32 .. +32, weight rows wn * 64 .. +64 (two 32 x 32 tiles)
+    const int wm = wave >> 1, wn = wave & 1;
+    f32x16_v acc[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[b][r] = 0.f;
+    load(0);
+    for (int kt = 0; kt < KT; kt++) {
+        char* at = plds + (kt & 1) * kPStage;
+        char* wt = at + PBM * PBK * 2;
+        store(at, wt);
+        __syncthreads();
+        if (kt + 1 < KT) load(kt + 1);
+#pragma unroll
+        for (int ks = 0; ks < PBK / 16; ks++) {
+            const int fr = lane & 31, fc = 2 * ks + (lane >> 5);
+            const bf16x8_v af = *reinterpret_cast<const bf16x8_v*>(at + swz(wm * 32 + fr, fc));
+#pragma unroll
+            for (int b = 0; b < 2; b++) {
+                const bf16x8_v bf = *reinterpret_cast<const bf16x8_v*>(wt + swz(wn * 64 + b * 32 + fr, fc));
+                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[b], 0, 0, 0);
+            }
+        }
+    }
+    const int cj = lane & 31;
+#pragma unroll
+    for (int b = 0; b < 2; b++) {
+        const int nl = wn * 64 + b * 32 + cj;  // weight row within the block's 128
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int row = wm * 32 + c_row(lane, r);
+            const float v = acc[b][r];
+            if constexpr (MODE == 0) {
+                const float up = __builtin_bit_cast(
+                    float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128 /* row_ror:8 */, 0xF, 0xF,
+                                                       false));
+                if ((cj & 15) < 8 && row < rows) {
+                    const int col = (blockIdx.y >> 1) * 128 + (blockIdx.y & 1) * 64 + (nl >> 4) * 8 + (cj & 7);
+                    out[(size_t)(slot0 + row) * sh.I + col] = f32_to_bf16(silu_f32(v) * up * slot_w[slot0 + row]);
+                }
+            } else if (row < rows) {
+                out[(size_t)(slot0 + row) * sh.H + blockIdx.y * PBN + nl] = f32_to_bf16(v);
+            }
+        }
+    }
+}
+
+// ------------------------------------------------------------------ combine: out[t] = sum_k slot_out[inv[t, k]]
+__global__ void moe_combine_kernel(const uint16_t* __restrict__ slot_out, const int32_t* __restrict__ inv, int topk,
+                                   int H, void* __restrict__ out, int out_bf16) {
+    const int t = blockIdx.x;
+    for (int c = threadIdx.x * 2; c < H; c += blockDim.x * 2) {
+        float a0 = 0.f, a1 = 0.f;
+        for (int k = 0; k < topk; k++) {
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(slot_out + (size_t)inv[t * topk + k] * H + c);
+            a0 += bf16_to_f32((uint16_t)v);
+            a1 += bf16_to_f32((uint16_t)(v >> 16));
+        }
+        if (out_bf16) {
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + (size_t)t * H + c) = pack_bf16x2(a0, a1);
+        } else {
+            float* o = reinterpret_cast<float*>(out) + (size_t)t * H + c;
+            o[0] = a0;
+            o[1] = a1;
+        }
+    }
+}
+
+// ------------------------------------------------------------------ workspace layout
+struct MoeWs {
+    int32_t *sel, *off, *slot_pair, *slot_tok, *inv, *jobs, *njobs;
+    float *w, *slot_w;
+    uint16_t *act, *slot_out;
+    size_t bytes;
+};
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+int max_jobs(int T, int E, int topk, int chunk) { return (T * topk + chunk - 1) / chunk + (E < T * topk ? E : T * topk); }
+
+MoeWs moe_ws(void* base, int T, int E, int topk, int H, int I) {
+    MoeWs ws;
+    char* p = reinterpret_cast<char*>(base);
+    size_t o = 0;
+    auto take = [&](size_t b) {
+        char* r = p ? p + o : nullptr;
+        o += align256(b);
+        return r;
+    };
+    const size_t P = (size_t)T * topk;
+    const int mj = max_jobs(T, E, topk, T <= 32 ? kDecRows : PBM);
+    ws.sel = reinterpret_cast<int32_t*>(take(P * 4));
+    ws.w = reinterpret_cast<float*>(take(P * 4));
+    ws.off = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
+    ws.slot_pair = reinterpret_cast<int32_t*>(take(P * 4));
+    ws.slot_tok = reinterpret_cast<int32_t*>(take(P * 4));
+    ws.slot_w = reinterpret_cast<float*>(take(P * 4));
+    ws.inv = reinterpret_cast<int32_t*>(take(P * 4));
+    ws.jobs = reinterpret_cast<int32_t*>(take((size_t)mj * 8));
+    ws.njobs = reinterpret_cast<int32_t*>(take(4));
+    ws.act = reinterpret_cast<uint16_t*>(take(P * I * 2));
+    ws.slot_out = reinterpret_cast<uint16_t*>(take(P * H * 2));
+    ws.bytes = o;
+    return ws;
+}
+
+void moe_check(int T, int E, int topk, int H, int I) {
+    CHECK(T >= 1 && E >= 1 && E <= kMaxExperts && topk >= 1 && topk <= 16 && topk <= E, "moe T %d E %d topk %d", T, E,
+          topk);
+    CHECK(H % 512 == 0 && H / 128 <= 4 * kMaxWaves && I % 128 == 0 && I / 128 <= kMaxWavesGeneric, "moe H %d I %d", H,
+          I);
+}
+
+}  // namespace
+
+extern "C" {
+
+void qe_moe_route(const float* logits, int T, int E, int topk, int32_t* sel, float* w, void* stream) {
+    CHECK(T >= 1 && E >= 1 && E <= kMaxExperts && topk >= 1 && topk <= 32 && topk <= E, "moe_route T %d E %d topk %d",
+          T, E, topk);
+    moe_route_kernel<<<T, kRouteThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(logits, E, topk, sel, w);
+    HIP_CHECK(hipGetLastError());
+}
+
+void qe_moe_segment(const int32_t* sel, const float* w, int T, int E, int topk, int chunk, int32_t* off,
+                    int32_t* slot_pair, int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs, int32_t* njobs,
+                    void* stream) {
+    CHECK(T >= 1 && E >= 1 && E <= kMaxExperts && topk >= 1 && topk <= 16 && chunk >= 1, "moe_segment T %d E %d", T, E);
+    moe_segment_kernel<<<1, kSegThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        sel, w, T, E, topk, chunk, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs);
+    HIP_CHECK(hipGetLastError());
+}
+
+size_t qe_moe_workspace_bytes(int T, int E, int topk, int H, int I) {
+    moe_check(T, E, topk, H, I);
+    return moe_ws(nullptr, T, E, topk, H, I).bytes;
+}
+
+size_t qe_moe_record_bytes(int H, int I) { return moe_shape(1, 1, H, I).rec * (size_t)(I / 128); }
+
+void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
+               void* out, int flags, void* workspace, size_t ws_bytes, void* stream) {
+    moe_check(T, E, topk, H, I);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const MoeShape sh = moe_shape(E, topk, H, I);
+    const MoeWs ws = moe_ws(workspace, T, E, topk, H, I);
+    CHECK(workspace && ws_bytes >= ws.bytes, "moe workspace %zu < %zu bytes", ws_bytes, ws.bytes);
+    const char* recs = reinterpret_cast<const char*>(records);
+    const bool decode = T <= 32;
+    const int chunk = decode ? kDecRows : PBM;
+    const int mj = max_jobs(T, E, topk, chunk);
+
+    moe_route_kernel<<<T, kRouteThreads, 0, st>>>(logits, E, topk, ws.sel, ws.w);
+    HIP_CHECK(hipGetLastError());
+    moe_segment_kernel<<<1, kSegThreads, 0, st>>>(ws.sel, ws.w, T, E, topk, chunk, ws.off, ws.slot_pair, ws.slot_tok,
+                                                  ws.slot_w, ws.inv, ws.jobs, ws.njobs);
+    HIP_CHECK(hipGetLastError());
+    if (decode) {
+        const int G = H / 128;
+        const int ng = (G % 4 == 0 && G / 4 <= kMaxWaves) ? 4 : 8;
+        CHECK(G % ng == 0 && G / ng <= kMaxWaves, "moe decode H %d", H);
+        const size_t lds_gu = gemv_lds_bytes<kDecRows, 8>(G / ng);
+        if (ng == 4)
+            moe_dec_gate_up_kernel<kDecRows, 4><<<dim3(mj, sh.ngrp * 16), 64 * (G / 4), lds_gu, st>>>(
+                recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
+        else
+            moe_dec_gate_up_kernel<kDecRows, 8><<<dim3(mj, sh.ngrp * 16), 64 * (G / 8), lds_gu, st>>>(
+                recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
+        HIP_CHECK(hipGetLastError());
+        moe_dec_down_kernel<kDecRows><<<dim3(mj, H / 16), 64 * sh.ngrp, gemv_lds_bytes<kDecRows, 1>(sh.ngrp), st>>>(
+            recs, sh, ws.act, ws.off, ws.jobs, ws.njobs, ws.slot_out);
+        HIP_CHECK(hipGetLastError());
+    } else {
+        moe_pf_kernel<0><<<dim3(mj, sh.ngrp * 2), PNTH, 2 * kPStage, st>>>(recs, sh, x, ws.off, ws.slot_tok, ws.slot_w,
+                                                                         ws.jobs, ws.njobs, ws.act);
+        HIP_CHECK(hipGetLastError());
+        moe_pf_kernel<1><<<dim3(mj, H / PBN), PNTH, 2 * kPStage, st>>>(recs, sh, ws.act, ws.off, ws.slot_tok,
+                                                                     ws.slot_w, ws.jobs, ws.njobs, ws.slot_out);
+        HIP_CHECK(hipGetLastError());
+    }
+    moe_combine_kernel<<<T, 256, 0, st>>>(ws.slot_out, ws.inv, topk, H, out, (flags & QE_OUT_BF16) ? 1 : 0);
+    HIP_CHECK(hipGetLastError());
+}
+
+// compressed-tensors experts -> group records. gate_up: int32 [E][2I][H/8] (rows gate 0..I then up 0..I), fp16
+// scales [E][2I][H/128]; down: int32 [E][H][I/8], fp16 scales [E][H][I/128]. The reference's loader does the same
+// per group (flash.cu:1555-1611): gather the group's gate/up rows, GLU-interleave, repack; gather the group's down
+// columns, repack.
+void qe_moe_pack_w4(const int32_t* gu_q, const uint16_t* gu_s, const int32_t* dn_q, const uint16_t* dn_s, int E, int H,
+                    int I, void* records, void* stream) {
+    moe_check(1, E, 1, H, I);
+    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+    const MoeShape sh = moe_shape(E, 1, H, I);
+    int32_t *tq, *tq2;
+    uint16_t *ts, *ts2;
+    HIP_CHECK(hipMalloc(&tq, (size_t)256 * H / 2));
+    HIP_CHECK(hipMalloc(&tq2, (size_t)256 * H / 2));
+    HIP_CHECK(hipMalloc(&ts, (size_t)256 * (H / 128) * 2));
+    HIP_CHECK(hipMalloc(&ts2, (size_t)256 * (H / 128) * 2));
+    int32_t* dq;
+    uint16_t* dsc;
+    HIP_CHECK(hipMalloc(&dq, (size_t)H * 64));
+    HIP_CHECK(hipMalloc(&dsc, (size_t)H * 2));
+    char* recs = reinterpret_cast<char*>(records);
+    const size_t gwpr = H / 8, gspr = H / 128, dwpr = I / 8, dspr = I / 128;
+    for (int e = 0; e < E; e++)
+        for (int g = 0; g < sh.ngrp; g++) {
+            char* rp = recs + ((size_t)e * sh.ngrp + g) * sh.rec;
+            const int32_t* gq = gu_q + (size_t)e * 2 * I * gwpr;
+            const uint16_t* gs = gu_s + (size_t)e * 2 * I * gspr;
+            HIP_CHECK(hipMemcpyAsync(tq, gq + (size_t)g * 128 * gwpr, 128 * gwpr * 4, hipMemcpyDeviceToDevice, st));
+            HIP_CHECK(hipMemcpyAsync(tq + 128 * gwpr, gq + ((size_t)I + g * 128) * gwpr, 128 * gwpr * 4,
+                                     hipMemcpyDeviceToDevice, st));
+            HIP_CHECK(hipMemcpyAsync(ts, gs + (size_t)g * 128 * gspr, 128 * gspr * 2, hipMemcpyDeviceToDevice, st));
+            HIP_CHECK(hipMemcpyAsync(ts + 128 * gspr, gs + ((size_t)I + g * 128) * gspr, 128 * gspr * 2,
+                                     hipMemcpyDeviceToDevice, st));
+            glu_interleave_rows(tq, ts, 256, H, tq2, ts2, st, 4);
+            repack_w4(tq2, ts2, 256, H, reinterpret_cast<uint4*>(rp), reinterpret_cast<uint16_t*>(rp + sh.gg_q), st);
+            const int32_t* eq = dn_q + (size_t)e * H * dwpr;
+            const uint16_t* es = dn_s + (size_t)e * H * dspr;
+            HIP_CHECK(hipMemcpy2DAsync(dq, 64, eq + g * 16, dwpr * 4, 64, H, hipMemcpyDeviceToDevice, st));
+            HIP_CHECK(hipMemcpy2DAsync(dsc, 2, es + g, dspr * 2, 2, H, hipMemcpyDeviceToDevice, st));
+            repack_w4(dq, dsc, H, 128, reinterpret_cast<uint4*>(rp + sh.gg_q + sh.gg_s),
+                      reinterpret_cast<uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q), st);
+        }
+    HIP_CHECK(hipStreamSynchronize(st));
+    HIP_CHECK(hipFree(tq));
+    HIP_CHECK(hipFree(tq2));
+    HIP_CHECK(hipFree(ts));
+    HIP_CHECK(hipFree(ts2));
+    HIP_CHECK(hipFree(dq));
+    HIP_CHECK(hipFree(dsc));
+}
+
+}  // extern "C"

@@ -159,3 +159,64 @@ def gemm_w8(w: W8, x, out_bf16=False, y=None):
     call("qe_gemm_w8_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
          w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
     return y
+
+
+class MoE:
+    """One MoE layer of E INT4 experts in the group-record format (see include/qe_kernels.h)."""
+
+    def __init__(self, records, E, topk, H, I):
+        self.records, self.E, self.topk, self.H, self.I = records, E, topk, H, I
+        self._ws = None
+
+    @staticmethod
+    def pack(gu_q, gu_s, dn_q, dn_s, topk):
+        """gate_up int32 [E][2I][H/8] + fp16 [E][2I][H/128]; down int32 [E][H][I/8] + fp16 [E][H][I/128]"""
+        E, I2, h8 = gu_q.shape
+        H, I = h8 * 8, I2 // 2
+        from .qe import lib
+        lib().qe_moe_record_bytes.restype = ctypes.c_size_t
+        rb = lib().qe_moe_record_bytes(H, I)
+        recs = torch.empty(E * rb, dtype=torch.uint8, device=gu_q.device)
+        call("qe_moe_pack_w4", gu_q, gu_s, dn_q, dn_s, E, H, I, recs, _stream())
+        return MoE(recs, E, topk, H, I)
+
+    def workspace(self, T):
+        from .qe import lib
+        lib().qe_moe_workspace_bytes.restype = ctypes.c_size_t
+        nb = lib().qe_moe_workspace_bytes(T, self.E, self.topk, self.H, self.I)
+        if self._ws is None or self._ws.numel() < nb:
+            self._ws = torch.empty(nb, dtype=torch.uint8, device=self.records.device)
+        return self._ws, nb
+
+    def __call__(self, logits, x, out_bf16=False, out=None):
+        T = x.shape[0]
+        assert logits.dtype == torch.float32 and logits.shape == (T, self.E) and x.shape == (T, self.H)
+        ws, nb = self.workspace(T)
+        if out is None:
+            out = torch.empty(T, self.H, dtype=torch.bfloat16 if out_bf16 else torch.float32, device=x.device)
+        call("qe_moe_w4", logits, x, self.records, T, self.E, self.topk, self.H, self.I, out,
+             OUT_BF16 if out_bf16 else 0, ws, ctypes.c_size_t(nb), _stream())
+        return out
+
+
+def moe_route(logits, topk):
+    T, E = logits.shape
+    sel = torch.empty(T, topk, dtype=torch.int32, device=logits.device)
+    w = torch.empty(T, topk, dtype=torch.float32, device=logits.device)
+    call("qe_moe_route", logits, T, E, topk, sel, w, _stream())
+    return sel, w
+
+
+def moe_segment(sel, w, E, chunk):
+    T, topk = sel.shape
+    dev = sel.device
+    P = T * topk
+    off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    slot_pair = torch.empty(P, dtype=torch.int32, device=dev)
+    slot_tok = torch.empty(P, dtype=torch.int32, device=dev)
+    slot_w = torch.empty(P, dtype=torch.float32, device=dev)
+    inv = torch.empty(P, dtype=torch.int32, device=dev)
+    jobs = torch.empty(2 * ((P + chunk - 1) // chunk + min(E, P)), dtype=torch.int32, device=dev)
+    njobs = torch.empty(1, dtype=torch.int32, device=dev)
+    call("qe_moe_segment", sel, w, T, E, topk, chunk, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs, _stream())
+    return dict(off=off, slot_pair=slot_pair, slot_tok=slot_tok, slot_w=slot_w, inv=inv, jobs=jobs, njobs=njobs)

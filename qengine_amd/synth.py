@@ -70,3 +70,14 @@ def x_dev(m, k, seed, device="cuda"):
     g = torch.Generator(device=device)
     g.manual_seed(seed)
     return torch.randn(m, k, device=device, generator=g).bfloat16()
+
+
+def moe_host(E, H, I, seed):
+    """experts in compressed-tensors form: gate_up int32 [E][2I][H/8] + fp16 scales [E][2I][H/128], down int32
+    [E][H][I/8] + fp16 [E][H][I/128] (BASELINE: uniform nibbles, scales |N(0,1)| * 0.02)"""
+    rng = np.random.default_rng(seed)
+    gq = rng.integers(0, 2**32, size=(E, 2 * I, H // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    gs = (np.abs(rng.standard_normal((E, 2 * I, H // 128))) * 0.02).astype(np.float16).view(np.uint16)
+    dq = rng.integers(0, 2**32, size=(E, H, I // 8), dtype=np.uint64).astype(np.uint32).view(np.int32)
+    ds = (np.abs(rng.standard_normal((E, H, I // 128))) * 0.02).astype(np.float16).view(np.uint16)
+    return gq, gs, dq, ds

@@ -1,0 +1,88 @@
+"""MoE grouped INT4 expert layer through the C-ABI vs the CPU oracle: routing and segmentation bit-exact, packed
+records bit-exact, the layer within 2e-2 * rms(ref) plus the output's own rounding.
+
+The layer keeps two bf16 intermediates, as the reference keeps fp16 ones (the GLU activation, flash_kernels.cuh:6185,
+and the per-(token, k) down slots, :6421-6427). The decode path (T <= 32) runs the decode GEMV, which multiplies the
+unrounded weights (u - 8) * s, so it is compared with the oracle on unrounded weights; the prefill path (MFMA on
+bf16_rn((u - 8) * s) tiles) with the oracle on the bf16-dequantized weights. Through the GLU the weight rounding
+alone moves act by more than the gate leaves, so each path is held to the reference of its own numerics."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qengine_amd import ops, synth
+from test_gemv_gpu import assert_bf16_close, out_f32
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("T,E,topk", [(1, 512, 10), (16, 512, 10), (300, 64, 6), (4096, 512, 10)])
+def test_route_and_segment_bit_exact(dev, T, E, topk):
+    lg = synth.logits_host(T, E, seed=T + E)
+    lg[0, 3] = lg[0, 7] = lg[0].max() + 1.0  # a tie at the top: lower index first
+    sel_ref, w_ref = oracle.moe_route(lg, topk)
+    sel, w = ops.moe_route(torch.from_numpy(lg).to(dev), topk)
+    torch.cuda.synchronize()
+    assert np.array_equal(sel.cpu().numpy(), sel_ref)
+    assert np.allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
+    assert sel_ref[0, 0] == 3 and sel_ref[0, 1] == 7
+    cnt, off, lst, inv = oracle.moe_segment(sel_ref, E)
+    for chunk in (2, 64):
+        seg = ops.moe_segment(sel, w, E, chunk)
+        torch.cuda.synchronize()
+        assert np.array_equal(seg["off"].cpu().numpy(), off)
+        assert np.array_equal(seg["slot_pair"].cpu().numpy(), lst)
+        assert np.array_equal(seg["inv"].cpu().numpy(), inv)
+        assert np.array_equal(seg["slot_tok"].cpu().numpy(), lst // topk)
+        assert np.array_equal(seg["slot_w"].cpu().numpy(), w.cpu().numpy().ravel()[lst])
+        nj = int(seg["njobs"].item())
+        jobs = seg["jobs"].cpu().numpy()[:2 * nj].reshape(nj, 2)
+        ref_jobs = [(e, j) for e in range(E) for j in range(0, cnt[e], chunk)]
+        assert [tuple(r) for r in jobs] == ref_jobs
+
+
+def test_pack_records_bit_exact(dev):
+    E, H, I = 3, 512, 256
+    gq, gs, dq, ds = synth.moe_host(E, H, I, seed=1)
+    ref = oracle.moe_pack(gq, gs, dq, ds, E, H, I)
+    moe = ops.MoE.pack(synth.to_dev(gq), synth.to_dev(gs, torch.float16), synth.to_dev(dq),
+                       synth.to_dev(ds, torch.float16), topk=2)
+    torch.cuda.synchronize()
+    assert np.array_equal(moe.records.cpu().numpy(), ref)
+
+
+def _layer(dev, T, E, topk, H, I, seed, tokens=None, out_bf16=True):
+    gq, gs, dq, ds = synth.moe_host(E, H, I, seed=seed)
+    moe = ops.MoE.pack(synth.to_dev(gq), synth.to_dev(gs, torch.float16), synth.to_dev(dq),
+                       synth.to_dev(ds, torch.float16), topk=topk)
+    lg = synth.logits_host(T, E, seed=seed + 1)
+    xh = synth.x_host(T, H, seed=seed + 2)
+    y = moe(torch.from_numpy(lg).to(dev), synth.to_dev(xh), out_bf16=out_bf16)
+    torch.cuda.synchronize()
+    ref, _, _ = oracle.moe_ref(lg, xh, gq, gs, dq, ds, topk, H, I, tokens=tokens, exact=T <= 32)
+    yv = out_f32(y)
+    return (yv if tokens is None else yv[tokens]), ref, moe, lg, xh
+
+
+@pytest.mark.parametrize("T", [1, 5, 16, 32, 33, 100])
+def test_moe_layer_small(dev, T):
+    """decode path (T <= 32) and prefill path (T > 32) on a small layer"""
+    y, ref, *_ = _layer(dev, T, E=16, topk=4, H=512, I=256, seed=T)
+    assert_bf16_close(y, ref)
+
+
+def test_moe_layer_fp32_out_deterministic(dev):
+    y1, ref, moe, lg, xh = _layer(dev, 40, E=16, topk=4, H=512, I=256, seed=9, out_bf16=False)
+    assert_bf16_close(y1, ref)
+    y2 = moe(torch.from_numpy(lg).to(dev), synth.to_dev(xh), out_bf16=False)
+    torch.cuda.synchronize()
+    assert np.array_equal(y1.view(np.uint32), y2.cpu().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("T", [1, 16, 4096])
+def test_moe_layer_baseline(dev, T):
+    """512 experts, top-10, H = 2048, I = 512 (T = 4096: 24 sampled tokens)"""
+    tokens = None if T <= 16 else np.sort(np.random.default_rng(7).choice(T, 24, replace=False))
+    y, ref, *_ = _layer(dev, T, E=512, topk=10, H=2048, I=512, seed=100 + T, tokens=tokens)
+    assert_bf16_close(y, ref)
