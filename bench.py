@@ -6,8 +6,9 @@ A step is one call of the decode GEMV of BASELINE config 0 (W4A16, M=1, K=5120, 
 bf16 output) on seeded synthetic inputs already resident in HBM. The weights rotate over 8 copies (368 MB,
 more than the 256 MB Infinity Cache) so every call streams its weights from HBM. `value` = algorithmic bytes
 (N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 = 46,002,176 B per call) * K / the elapsed time of the K timed steps.
-`roofline.achieved` uses the kernel's own average duration (HIP events around each launch on the launch
-stream). The prefill GEMM (config 2) and the other configs are reported beside it in `secondary`.
+The K decode launches are captured in one HIP graph and replayed (as a decode loop is served), so the host's
+per-call overhead does not starve the GPU. `roofline.achieved` = bytes per call / the stream time per launch
+(HIP events on the launch stream before and after the K timed launches). The prefill GEMM (config 2) and the other configs are reported beside it in `secondary`.
 The CPU baseline is the oracle's dequantize + fp32 matmul of the same workload on the host cores.
 """
 import argparse
@@ -32,6 +33,10 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="only the headline GEMV")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--only", choices=["prefill", "w8", "moe", "skinny"], default=None,
+                    help="run one secondary workload alone (profiling); prints its result")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
+                    help="time a plain device copy of MB megabytes x 20 (scale for FETCH_SIZE / WRITE_SIZE) and exit")
     return ap.parse_args()
 
 
@@ -51,28 +56,33 @@ def read_traffic(name):
     return None
 
 
-def time_launches(fn, steps, warmup, nvar):
-    """fn(i) launches step i on the current stream. Returns (elapsed ms of the `steps` timed steps bracketed by
-    synchronize, mean per-launch ms from events recorded around each launch)."""
+def time_launches(fn, steps, warmup, nvar, graph=False):
+    """fn(i) launches step i on the current stream. Returns (wall ms of the `steps` timed steps bracketed by
+    synchronize, stream ms per step from HIP events recorded on the launch stream before and after the timed
+    steps). graph=True captures the `steps` launches into one HIP graph and replays it, so host launch overhead
+    (ctypes + torch stream lookup, comparable to a 10 us kernel) never starves the GPU: the per-step figure is
+    then the kernel's duration plus the dispatch gap between consecutive graph nodes."""
     import torch
-    st = torch.cuda.current_stream()
     for i in range(warmup):
         fn(i % nvar)
     torch.cuda.synchronize()
+    run = lambda: [fn(i % nvar) for i in range(steps)]  # noqa: E731
+    if graph:
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            run()
+        g.replay()  # upload + one untimed pass
+        run = g.replay
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        fn(i % nvar)
+    e0.record(st)
+    run()
+    e1.record(st)
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record(st)
-        fn(i % nvar)
-        ev[i][1].record(st)
-    torch.cuda.synchronize()
-    per = sorted(a.elapsed_time(b) for a, b in ev)
-    mean = sum(per) / len(per)
-    return wall_ms, mean, per[len(per) // 2]
+    return wall_ms, e0.elapsed_time(e1) / steps
 
 
 def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None):
@@ -88,9 +98,9 @@ def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None):
     x = synth.x_dev(m, k, seed=1)
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
     fn = lambda i: ops.gemv_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
-    wall_ms, ev_ms, med_ms = time_launches(fn, steps, warmup, len(ws))
+    wall_ms, ev_ms = time_launches(fn, steps, warmup, len(ws), graph=True)
     b = gemv_bytes(m, n, k)
-    res = dict(m=m, n=n, k=k, bytes=b, ms_per_step=wall_ms / steps, kernel_ms_mean=ev_ms, kernel_ms_median=med_ms,
+    res = dict(m=m, n=n, k=k, bytes=b, ms_per_step=wall_ms / steps, kernel_ms_mean=ev_ms,
                gbs_wall=b * steps / (wall_ms * 1e-3) / 1e9, gbs_kernel=b / (ev_ms * 1e-3) / 1e9)
     del ws
     torch.cuda.empty_cache()
@@ -109,7 +119,7 @@ def bench_gemm(m, n, k, steps=10, warmup=3, copies=2):
     x = synth.x_dev(m, k, seed=2)
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
     fn = lambda i: ops.gemm_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
-    wall_ms, ev_ms, med_ms = time_launches(fn, steps, warmup, len(ws))
+    _, ev_ms = time_launches(fn, steps, warmup, len(ws))
     flop = 2.0 * m * n * k
     del ws, x, y
     torch.cuda.empty_cache()
@@ -137,7 +147,7 @@ def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=16):
         fn = lambda i: ops.gemv_w8(ws[i], x, out_bf16=True, y=y)  # noqa: E731
     else:
         fn = lambda i: ops.gemm_w8(ws[i], x, out_bf16=True, y=y)  # noqa: E731
-    _, ev_ms, _ = time_launches(fn, steps if m <= 16 else 10, warmup, len(ws))
+    _, ev_ms = time_launches(fn, steps if m <= 16 else 10, warmup, len(ws), graph=m <= 16)
     del ws
     torch.cuda.empty_cache()
     if m <= 16:
@@ -176,7 +186,7 @@ def bench_moe(Ts=(1, 16, 4096), E=512, topk=10, H=2048, I=512, nrout=8):
             hits.append(int(torch.unique(sel).numel()))
         fn = lambda i: moe(lgs[i], x, out_bf16=True, out=y)  # noqa: E731
         steps = 100 if T <= 16 else 20
-        _, ev_ms, _ = time_launches(fn, steps, 5, nrout)
+        _, ev_ms = time_launches(fn, steps, 5, nrout)
         b = sum(hits) / len(hits) * per_expert + 4 * T * H
         flop = 6.0 * T * topk * H * I
         t_roof = max(b / (HBM_PEAK_GBS * 1e9), flop / (BF16_PEAK_TFLOPS * 1e12))
@@ -227,6 +237,25 @@ def main():
     from qengine_amd import call
     torch.cuda.set_device(0)
     call("qe_gemv_workspace_init")
+    if args.copy_calibration:
+        nb = args.copy_calibration << 20
+        a = torch.empty(nb, dtype=torch.uint8, device="cuda").fill_(1)
+        b = torch.empty_like(a)
+        torch.cuda.synchronize()
+        for _ in range(20):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": nb, "launches": 20}))
+        return
+    if args.only:
+        fns = {"prefill": lambda: {"k5120_n17408": bench_gemm(8192, 17408, 5120),
+                                   "k17408_n5120": bench_gemm(8192, 5120, 17408)},
+               "w8": lambda: {"m1": bench_w8(1), "m4096": bench_w8(4096)},
+               "moe": lambda: bench_moe(),
+               "skinny": lambda: {f"m{m}": bench_gemv(args, m=m, n=17408, steps=100, warmup=10)["kernel_ms_mean"]
+                                  for m in (2, 4, 8, 16)}}
+        print(json.dumps({args.only: fns[args.only]()}))
+        return
 
     g = bench_gemv(args)
     secondary = {}
@@ -262,8 +291,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("gemv_w4_c0_m1_traffic.txt"),
-                     "kernel_us_mean": round(g["kernel_ms_mean"] * 1e3, 3),
-                     "kernel_us_median": round(g["kernel_ms_median"] * 1e3, 3)},
+                     "kernel_us_mean": round(g["kernel_ms_mean"] * 1e3, 3)},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }
