@@ -15,6 +15,8 @@ Parity pins (each function is checked against something other than itself in tes
   w8_pos / tile_w8  bijection + inverse map of src/tools/qe_w8q.cu:34-45 + A-fragment decoder
   moe_route         brute force sort with the tie rule (numpy lexsort) + softmax renormalisation
   moe_segment       invariants (counts, contiguity, every pair once, stable order) + numpy argsort(stable)
+  moe_pack          records decoded back to the source rows with the independent fragment decoder
+  moe_ref           float64 composite of the pinned pieces above (the layer's checker)
 """
 import ctypes
 import os

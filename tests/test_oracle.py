@@ -248,3 +248,31 @@ def test_moe_segment_invariants():
     assert np.array_equal(inv[lst], np.arange(T * topk))              # inverse map
     for e in range(E):
         assert np.all(flat[lst[off[e]:off[e + 1]]] == e)
+
+
+def test_moe_pack_decodes_to_source_rows():
+    """group record (e, g) (reference flash.h:203-218, loader flash.cu:1555-1611) decoded with the independent
+    fragment decoder: gq rows = GLU tile order of gate rows [128g, 128g+128) and up rows I + [128g, 128g+128),
+    gs their scales; dq = down columns [128g, 128g+128) of all H rows, ds the matching scale column"""
+    E, H, I = 2, 256, 256
+    gq, gs, dq, ds = synth.moe_host(E, H, I, seed=4)
+    rec = oracle.moe_pack(gq, gs, dq, ds, E, H, I)
+    sizes = [256 * H // 2, 256 * (H // 128) * 2, H * 64, H * 2]
+    assert rec.size == E * (I // 128) * sum(sizes)
+    pos = 0
+    for e in range(E):
+        for g in range(I // 128):
+            parts = []
+            for sz in sizes:
+                parts.append(rec[pos:pos + sz])
+                pos += sz
+            u = _decode_w4_fragments(parts[0].view(np.uint32), 256, H)
+            s = parts[1].view(np.uint16).reshape(16, H // 128, 16).transpose(0, 2, 1).reshape(256, H // 128)
+            src_u = oracle.unpack_w4(gq[e], 2 * I, H) + 8
+            for dr in range(256):  # GLU tile order: per 16 rows 8 gate + 8 up
+                t, j = dr // 16, dr % 16
+                sr = 128 * g + 8 * t + j if j < 8 else I + 128 * g + 8 * t + (j - 8)
+                assert np.array_equal(u[dr], src_u[sr]) and np.array_equal(s[dr], gs[e][sr])
+            ud = _decode_w4_fragments(parts[2].view(np.uint32), H, 128)
+            assert np.array_equal(ud, oracle.unpack_w4(dq[e], H, I)[:, 128 * g:128 * g + 128] + 8)
+            assert np.array_equal(parts[3].view(np.uint16), ds[e][:, g])
