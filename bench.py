@@ -252,8 +252,10 @@ def main():
                                    "k17408_n5120": bench_gemm(8192, 5120, 17408)},
                "w8": lambda: {"m1": bench_w8(1), "m4096": bench_w8(4096)},
                "moe": lambda: bench_moe(),
-               "skinny": lambda: {f"m{m}": bench_gemv(args, m=m, n=17408, steps=100, warmup=10)["kernel_ms_mean"]
-                                  for m in (2, 4, 8, 16)}}
+               "skinny": lambda: {f"m{m}_n{n}": (lambda r: {"us": round(r["kernel_ms_mean"] * 1e3, 2),
+                                                             "gbs": round(r["gbs_kernel"], 1)})(
+                   bench_gemv(args, m=m, n=n, steps=200, warmup=20))
+                   for n in (5120, 17408) for m in (1, 2, 4, 8, 16)}}
         print(json.dumps({args.only: fns[args.only]()}))
         return
 

@@ -71,21 +71,26 @@ __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
 // (sp: [ng][16] rows of the tile, W8C: [16]) and, per activation row, the dword pointer of the slice's first group
 // (xw[tok], 64 dwords per group). On return (after a barrier) red[S][2][MT][16] holds the partial sums; rsum()
 // below adds them in a fixed order.
-// SDT < 0: scale dtype chosen at run time (`sdt`). PF: the activation dwords of every group are loaded up front,
-// interleaved with the weight loads of the same group (w_i, x_i, ...), so the activation latency hides behind the
-// weight latency; else they are loaded when the group is reached (large m).
-// LDS (`lds`): per wave xl [MT][64] u32 + xsum [MT][8] + the slice's scales [NGM][16] half, then red.
+// SDT < 0: scale dtype chosen at run time (`sdt`). PF: the activation dwords of every group are loaded up front;
+// with even slices (NG > 0) before all weights, and staged while the weights are in flight, else interleaved with
+// the weight loads of the same group (w_i, x_i, ...). !PF: loaded when the group is reached (large m).
+// LDS (`lds`): per wave xl [XG][MT][64] u32 + xsum [XG][MT][8] + the slice's scales [NGM][16] half, then red
+// (XG = NG groups when PF with even slices, else 1).
 template <int MT, int FMT, int SDT, int NG, bool PF>
 __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restrict__ qp, const uint16_t* __restrict__ sp,
                                             const uint32_t* const* xw, int m, int ng, int sdt) {
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
     constexpr int LPG = FMT == kFmtW4 ? 1 : 2;  // wave-loads per group
+    // UP: every group's activations are loaded before the weights and staged while the weights are in flight,
+    // so a group's work after its weights arrive is the unpack and the dot products only
+    constexpr bool UP = PF && NG > 0;
+    constexpr int XG = UP ? NGM : 1;  // groups of activations staged at once
     const int S = blockDim.x >> 6;
     const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
-    constexpr int WSZ = MT * 72 + NGM * 8;  // dwords of LDS per wave
-    uint32_t* xl = lds + (size_t)w * WSZ;                        // [MT][64]
-    float* xsum = reinterpret_cast<float*>(xl + MT * 64);        // [MT][8]
-    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + MT * 72);  // [NGM][16] scales of the slice
+    constexpr int WSZ = XG * MT * 72 + NGM * 8;  // dwords of LDS per wave
+    uint32_t* xl = lds + (size_t)w * WSZ;                             // [XG][MT][64]
+    float* xsum = reinterpret_cast<float*>(xl + XG * MT * 64);        // [XG][MT][8]
+    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + XG * MT * 72);  // [NGM][16] scales of the slice
     float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][2][MT][16]
     const int g = (L >> 2) & 7, t = L & 3, h = L >> 5;
     if (NG > 0) ng = NG;
@@ -104,12 +109,18 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     u32x4_v wv[NGM][LPG];
     uint32_t xr[PF ? MT : 1][PF ? NGM : 1];
     qp += L;
+    if constexpr (UP) {
+#pragma unroll
+        for (int i = 0; i < NGM; i++)
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) xr[tok][i] = ldx_group(tok, i);
+    }
 #pragma unroll
     for (int i = 0; i < NGM; i++) {
         if (NG == 0 && i >= ng) break;
 #pragma unroll
         for (int e = 0; e < LPG; e++) wv[i][e] = ld_stream(qp + (size_t)(i * LPG + e) * 64);
-        if constexpr (PF) {
+        if constexpr (PF && !UP) {
 #pragma unroll
             for (int tok = 0; tok < MT; tok++) xr[tok][i] = ldx_group(tok, i);
         }
@@ -123,24 +134,39 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     float acc_lo[MT], acc_hi[MT];
 #pragma unroll
     for (int tok = 0; tok < MT; tok++) acc_lo[tok] = acc_hi[tok] = 0.f;
-#pragma unroll
-    for (int i = 0; i < NGM; i++) {
-        if (NG == 0 && i >= ng) break;
-        // the wave's own LDS region; LDS operations of one wave complete in order
-        __builtin_amdgcn_wave_barrier();
+    // stage group i's activations at xl[i % XG] (class-major) with the class sums times the bias
+    auto stage = [&](int i) {
 #pragma unroll
         for (int tok = 0; tok < MT; tok++) {
             const uint32_t v = PF ? xr[PF ? tok : 0][PF ? i : 0] : ldx_group(tok, i);
-            xl[tok * 64 + L] = v;
+            const int xi = (UP ? i : 0) * MT + tok;
+            xl[xi * 64 + L] = v;
             float sm = dot2_bf16(v, 0x3F803F80u, 0.f);  // x_lo + x_hi (bf16 (1, 1))
             sm = dpp_add<kDppXor1>(sm);
             sm = dpp_add<kDppXor2>(sm);
             sm = dpp_add<kDppHalfMirror>(sm);
-            if (sl_st == 0) xsum[tok * 8 + c_st] = bias * sm;
+            if (sl_st == 0) xsum[xi * 8 + c_st] = bias * sm;
         }
+    };
+    if constexpr (UP) {
+#pragma unroll
+        for (int i = 0; i < NGM; i++) stage(i);
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+#pragma unroll
+    for (int i = 0; i < NGM; i++) {
+        if (NG == 0 && i >= ng) break;
+        if constexpr (!UP) {
+            // the wave's own LDS region; LDS operations of one wave complete in order
+            __builtin_amdgcn_wave_barrier();
+            stage(i);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        const int xg = (UP ? i : 0) * MT;  // first staged row of this group
 
         const int so = FMT == kFmtW8C ? 0 : i * 16;
         const float s_lo = scale_rt<SDT>(sl16[so + g], sdt);
@@ -148,7 +174,7 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
         // the dot2 chains start at -bias * X, so they end at sum (u - 8) x (or sum w x for INT8)
         float a_lo[MT], a_hi[MT];
 #pragma unroll
-        for (int tok = 0; tok < MT; tok++) a_lo[tok] = a_hi[tok] = -xsum[tok * 8 + cls];
+        for (int tok = 0; tok < MT; tok++) a_lo[tok] = a_hi[tok] = -xsum[(xg + tok) * 8 + cls];
         if constexpr (FMT == kFmtW4) {
             uint32_t p[4][4];
 #pragma unroll
@@ -161,8 +187,8 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
             }
 #pragma unroll
             for (int tok = 0; tok < MT; tok++) {
-                const u32x4_v x0 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8]);
-                const u32x4_v x1 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8 + 4]);
+                const u32x4_v x0 = *reinterpret_cast<const u32x4_v*>(&xl[(xg + tok) * 64 + cls * 8]);
+                const u32x4_v x1 = *reinterpret_cast<const u32x4_v*>(&xl[(xg + tok) * 64 + cls * 8 + 4]);
                 const uint32_t xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
                 for (int j = 0; j < 4; j++) {
@@ -184,8 +210,8 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
                 }
 #pragma unroll
             for (int tok = 0; tok < MT; tok++) {
-                const u32x4_v x0 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8]);
-                const u32x4_v x1 = *reinterpret_cast<const u32x4_v*>(&xl[tok * 64 + cls * 8 + 4]);
+                const u32x4_v x0 = *reinterpret_cast<const u32x4_v*>(&xl[(xg + tok) * 64 + cls * 8]);
+                const u32x4_v x1 = *reinterpret_cast<const u32x4_v*>(&xl[(xg + tok) * 64 + cls * 8 + 4]);
                 const uint32_t xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
 #pragma unroll
                 for (int e = 0; e < 2; e++)
@@ -227,10 +253,7 @@ __device__ __forceinline__ float rsum(const float* red, int S, int tok, int rr) 
     return v;
 }
 
-template <int MT, int NG>
-constexpr size_t gemv_lds_bytes(int S) {
-    return (size_t)S * (MT * 72 + (NG > 0 ? NG : kGenericNG) * 8) * 4 + (size_t)S * 2 * MT * 16 * 4;
-}
+
 
 // Plain decode GEMV: one block per 16-row tile of a tile-major matrix, K slices of NG groups.
 template <int MT, int FMT, int SDT, int NG, bool PF>
@@ -268,6 +291,14 @@ __attribute__((amdgpu_waves_per_eu(MT == 1 ? 6 : MT == 2 ? 5 : 1))) gemv_kernel(
     }
 }
 
+// dynamic LDS of gemv_tile for S waves (the layout described above gemv_tile)
+template <int MT, int NG, bool PF>
+constexpr size_t gemv_lds_bytes(int S) {
+    constexpr int NGM = NG > 0 ? NG : kGenericNG;
+    constexpr int XG = PF && NG > 0 ? NGM : 1;
+    return (size_t)S * (XG * MT * 72 + NGM * 8) * 4 + (size_t)S * 2 * MT * 16 * 4;
+}
+
 // K slicing of a matrix: (groups per slice NG, slices S); NG = 0 means uneven slices (generic kernel).
 // Depends on (n, k) only, so every row count of a matrix reduces in the same order.
 struct Slicing {
@@ -282,7 +313,8 @@ void launch_gemv(const uint4* q, const uint16_t* s, int n, int k, const uint16_t
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
     const int ngm = sc.ng > 0 ? sc.ng : kGenericNG;
     const bool pf = mt * ngm <= 16;  // activation prefetch registers
-    const size_t lds = (size_t)sc.S * (mt * 72 + ngm * 8) * 4 + (size_t)sc.S * 2 * mt * 16 * 4;  // gemv_lds_bytes
+    const int xg = pf && sc.ng > 0 ? sc.ng : 1;  // activation groups staged at once (gemv_tile's XG)
+    const size_t lds = (size_t)sc.S * (xg * mt * 72 + ngm * 8) * 4 + (size_t)sc.S * 2 * mt * 16 * 4;  // gemv_lds_bytes
     const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);
 #define QE_GEMV_K(MT_, NG_, PF_) \
     gemv_kernel<MT_, FMT, SDT, NG_, PF_><<<grid, block, lds, st>>>(q, s, n, k, x, ldx, y, ldy, m, out, sdt)

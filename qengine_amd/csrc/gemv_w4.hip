@@ -1,7 +1,17 @@
 // INT4 decode GEMV / skinny GEMM instantiations (kernel: gemv_impl.hpp).
 #include "gemv_impl.hpp"
 
+#include <cstdlib>
+
 using namespace qe_gemv;
+
+int skinny_min_m() {
+    static const int v = [] {
+        const char* e = getenv("QE_SKINNY_MIN_M");
+        return e && atoi(e) >= 1 ? atoi(e) : 2;
+    }();
+    return v;
+}
 
 static void gemv_check(int n, int k, const void* x, int ldx, int ldy, int m, bool glu) {
     CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && m >= 1 && m <= kMaxGemvRows, "gemv %d %d %d", n, k, m);
@@ -12,6 +22,10 @@ static void gemv_check(int n, int k, const void* x, int ldx, int ldy, int m, boo
 void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
     gemv_check(w.n, w.k, x, ldx, ldy, m, w.glu);
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    if (m >= skinny_min_m()) {
+        skinny_w4_mfma(w, x, ldx, y, ldy, m, out, st);
+        return;
+    }
     if (w.sdt == kScaleF16) launch_gemv<kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else launch_gemv<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }

@@ -479,7 +479,7 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
         const int G = H / 128;
         const int ng = (G % 4 == 0 && G / 4 <= kMaxWaves) ? 4 : 8;
         CHECK(G % ng == 0 && G / ng <= kMaxWaves, "moe decode H %d", H);
-        const size_t lds_gu = gemv_lds_bytes<kDecRows, 8>(G / ng);
+        const size_t lds_gu = ng == 4 ? gemv_lds_bytes<kDecRows, 4, true>(G / 4) : gemv_lds_bytes<kDecRows, 8, true>(G / 8);
         if (ng == 4)
             moe_dec_gate_up_kernel<kDecRows, 4><<<dim3(mj, sh.ngrp * 16), 64 * (G / 4), lds_gu, st>>>(
                 recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
@@ -487,7 +487,7 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
             moe_dec_gate_up_kernel<kDecRows, 8><<<dim3(mj, sh.ngrp * 16), 64 * (G / 8), lds_gu, st>>>(
                 recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
         HIP_CHECK(hipGetLastError());
-        moe_dec_down_kernel<kDecRows><<<dim3(mj, H / 16), 64 * sh.ngrp, gemv_lds_bytes<kDecRows, 1>(sh.ngrp), st>>>(
+        moe_dec_down_kernel<kDecRows><<<dim3(mj, H / 16), 64 * sh.ngrp, gemv_lds_bytes<kDecRows, 1, true>(sh.ngrp), st>>>(
             recs, sh, ws.act, ws.off, ws.jobs, ws.njobs, ws.slot_out);
         HIP_CHECK(hipGetLastError());
     } else {

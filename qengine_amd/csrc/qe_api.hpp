@@ -42,6 +42,10 @@ void gemv_workspace_init();
 // y[m][n] = sum_k x[m][k] * W[n][k]; x bf16 rows of stride ldx; y fp32 (or bf16 with out_bf16, or the GLU
 // bf16 activation) rows of stride ldy
 void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
+// skinny GEMM on the matrix cores (skinny.hip), m = 1..16; out: 0 fp32, 1 bf16, 2 GLU (bf16 act)
+void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st);
+// smallest row count that gemv_w4 sends to skinny_w4_mfma (QE_SKINNY_MIN_M, default 2)
+int skinny_min_m();
 void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 
 // ---- prefill GEMM (bf16 MFMA on dequantized tiles staged in LDS) ----

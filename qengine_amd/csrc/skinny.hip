@@ -1,0 +1,222 @@
+// Skinny GEMM (m = 2..16 activation rows) on the W4 layout, with the multiply-adds on the matrix cores.
+//
+// The VALU GEMV (gemv_impl.hpp) spends one v_dot2 per weight pair and activation row, so its cost grows with m.
+// Here the weights are unpacked once per tile and group and v_mfma_f32_16x16x32_bf16 multiplies them by all 16
+// (padded) activation rows at once:
+//   * MFMA operand lanes: lane l = 16 q + i supplies A row i (the tile's row i) and B column i (activation row i)
+//     for the k slots 8 q .. 8 q + 7; the output lane l holds column l % 16, rows 4 q .. 4 q + 3.
+//   * The W4 record of lane (g, t) holds rows g and g + 8 at k = 64 c + 16 j + 2 t + {0, 1, 8, 9} (j = 0..3).
+//     Lane 16 q + i of the wave loads the records (c, g = i % 8, t = q) of the group's two 64-k chunks and keeps the
+//     rows of half i / 8: k slots of lane group q are then the k of record t = q, the same for every row, which
+//     is what the B operand needs. Lanes i and i + 8 load the same two records (one 16-byte load each, merged by
+//     the cache), so each lane unpacks 32 weights of its own row: (w >> 4 h) & 0x000F000F | 0x43004300 is the
+//     bf16 pair (128 + u) of two consecutive k.
+//   * Activations are staged per group in the wave's LDS in class-major order (class c = 4 h + t holds the 8
+//     dwords of k = 64 h + 16 j + 2 t (+8)), which is exactly the B operand: one ds_read_b128 per MFMA.
+//   * The bias 136 (u = w + 8 over the 128 of the magic) is removed by one more MFMA per k step with A = -136:
+//     C = sum (128 + u) x - 136 sum x = sum (u - 8) x, all products exact in fp32. The group scale is applied
+//     once per group: acc += s * C.
+//   * K slices per block and the fixed-order LDS reduction are those of the GEMV (gemv_slicing): deterministic,
+//     and an activation row's result does not depend on the other rows (MFMA columns are independent).
+#include "gemv_impl.hpp"
+
+namespace qe_skinny {
+using namespace qe_gemv;
+
+// weight groups in flight per wave (4 keeps MT <= 4 at 6 waves per SIMD; the MT rows of activations of each group
+// in the window take registers too for larger MT)
+template <int MT, int NG>
+constexpr int skinny_d() {
+    return MT <= 4 ? 4 : 3;
+}
+
+// UPX (MT <= 4 with even slices): every group's activations are loaded before the weights and staged in LDS
+// while the weights are in flight. Else the activations of a group are loaded with its weights (x_j before w_j,
+// so waiting for x_j never waits for w_j) and staged one group ahead into a double buffer. Weight records stream
+// through a window of D groups.
+template <int MT, int NG>
+constexpr bool skinny_upx() {
+    return MT <= 4 && NG > 0;
+}
+template <int MT, int NG>
+constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][64], scales [NGM][16] half
+    constexpr int NGM = NG > 0 ? NG : kGenericNG;
+    return (skinny_upx<MT, NG>() ? NGM : 2) * MT * 64 + NGM * 8;
+}
+
+template <int MT, int SDT, int NG, int D>
+__global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
+__attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
+    const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K, const uint16_t* __restrict__ x,
+    int ldx, void* __restrict__ y, int ldy, int m, int out, int sdt) {
+    constexpr int NGM = NG > 0 ? NG : kGenericNG;
+    constexpr bool UPX = skinny_upx<MT, NG>();
+    constexpr int WSZ = skinny_wsz<MT, NG>();
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const int tile = blockIdx.x, G = K >> 7;
+    const int gb = NG > 0 ? w * NG : w * G / S;
+    const int ng = NG > 0 ? NG : (w + 1) * G / S - gb;
+    uint32_t* xl = lds + (size_t)w * WSZ;
+    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + (WSZ - NGM * 8));
+    float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][16 tok][16 rows]
+
+    const int qg = L >> 4, i = L & 15;  // operand lane group, row / column within the tile
+    const int g = i & 7, sh = 4 * (i >> 3);
+
+    // activation staging: lane L holds dword (class L / 8, slot L % 8) of each row's group
+    const uint32_t* xb = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64 + x_dword<kFmtW4>(L >> 3, L & 7);
+    const size_t xs = (size_t)(ldx >> 1);
+    auto ldxg = [&](int tok, int ii) { return tok < m ? xb[tok * xs + ii * 64] : 0u; };
+
+    // 1. loads in consumption order: the slice's scales (one dword per lane); UPX: every group's activations, then
+    //    the first D groups of weight records; else (x_j, w_j) pairs for the first D groups
+    {
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)tile * G + gb) * 16);
+        if (L < ng * 8) reinterpret_cast<uint32_t*>(sl16)[L] = sp[L];
+    }
+    constexpr int XR = UPX ? NGM : D;  // activation register slots
+    uint32_t xr[XR][MT];
+    const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + 4 * g + qg;
+    u32x4_v wv[D][2];
+    auto ldw = [&](int slot, int ii) {
+        wv[slot][0] = ld_stream(qp + (size_t)ii * 64);
+        wv[slot][1] = ld_stream(qp + (size_t)ii * 64 + 32);
+    };
+    if constexpr (UPX) {
+#pragma unroll
+        for (int ii = 0; ii < NGM; ii++)
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) xr[ii][tok] = ldxg(tok, ii);
+#pragma unroll
+        for (int ii = 0; ii < D; ii++)
+            if (ii < ng) ldw(ii, ii);
+#pragma unroll
+        for (int ii = 0; ii < NGM; ii++)
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) xl[(ii * MT + tok) * 64 + L] = xr[ii][tok];
+    } else {
+#pragma unroll
+        for (int ii = 0; ii < D; ii++) {
+            if (ii < ng) {
+#pragma unroll
+                for (int tok = 0; tok < MT; tok++) xr[ii][tok] = ldxg(tok, ii);
+                ldw(ii, ii);
+            }
+        }
+#pragma unroll
+        for (int tok = 0; tok < MT; tok++) xl[tok * 64 + L] = xr[0][tok];  // group 0 -> buffer 0
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const uint32_t kMask = 0x000F000Fu, kMagic = 0x43004300u;  // bf16 (128, 128)
+    const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
+    f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ii = 0; ii < NGM; ii++) {
+        if (NG == 0 && ii >= ng) break;
+        const int xrow = UPX ? ii * MT : (ii & 1) * MT;  // first staged row of this group
+        if constexpr (!UPX) {
+            // stage the next group's activations into the other buffer (read two groups ago, LDS operations of
+            // a wave complete in order)
+            if (ii + 1 < ng) {
+#pragma unroll
+                for (int tok = 0; tok < MT; tok++) xl[(((ii + 1) & 1) * MT + tok) * 64 + L] = xr[(ii + 1) % D][tok];
+            }
+        }
+        const u32x4_v r0 = wv[ii % D][0], r1 = wv[ii % D][1];
+        // refill the window: group ii + D goes where group ii was
+        if (ii + D < ng) {
+            if constexpr (!UPX) {
+#pragma unroll
+                for (int tok = 0; tok < MT; tok++) xr[ii % D][tok] = ldxg(tok, ii + D);
+            }
+            ldw(ii % D, ii + D);
+        }
+        f32x4_v c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++) {
+            const int j0 = 2 * (mm & 1);
+            const u32x4_v rec = mm < 2 ? r0 : r1;
+            u32x4_v b = {0u, 0u, 0u, 0u};
+            if (MT == 16 || i < MT)
+                b = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + (i < MT ? i : 0)) * 64 + (4 * (mm >> 1) + qg) * 8 + 2 * j0]);
+            const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
+            const u32x4_v a = {and_or(w0 >> sh, kMask, kMagic), and_or(w0 >> (sh + 8), kMask, kMagic),
+                               and_or(w1 >> sh, kMask, kMagic), and_or(w1 >> (sh + 8), kMask, kMagic)};
+            const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c, 0, 0, 0);
+        }
+        // rows 4 qg .. 4 qg + 3 of the group's scales
+        const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[ii * 16 + 4 * qg]);
+        acc[0] = fmaf(scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt), c[0], acc[0]);
+        acc[1] = fmaf(scale_rt<SDT>((uint16_t)(sv.x >> 16), sdt), c[1], acc[1]);
+        acc[2] = fmaf(scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt), c[2], acc[2]);
+        acc[3] = fmaf(scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt), c[3], acc[3]);
+        if constexpr (!UPX) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+    }
+
+    // 2. slices through LDS in a fixed order: red[w][tok][row], lane (qg, i) holds rows 4 qg .. + 3 of column i
+    *reinterpret_cast<f32x4_v*>(&red[(w * 16 + i) * 16 + 4 * qg]) = acc;
+    __syncthreads();
+    auto rsum = [&](int tok, int rr) {
+        float v = 0.f;
+        for (int ws = 0; ws < S; ws++) v += red[(ws * 16 + tok) * 16 + rr];
+        return v;
+    };
+    const int row0 = 16 * tile;
+    if (out == kOutGLU) {
+        for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
+            const int tok = idx >> 3, gg = idx & 7;
+            reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 / 2 + gg] =
+                f32_to_bf16(silu_f32(rsum(tok, gg)) * rsum(tok, gg + 8));
+        }
+    } else {
+        for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
+            const int tok = idx >> 4, rr = idx & 15;
+            const float v = rsum(tok, rr);
+            if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 + rr] = f32_to_bf16(v);
+            else reinterpret_cast<float*>(y)[(size_t)tok * ldy + row0 + rr] = v;
+        }
+    }
+}
+
+template <int SDT>
+void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+            int out, int sdt, hipStream_t st) {
+    const Slicing sc = gemv_slicing(n, k);
+    const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
+    const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);
+#define QE_SK_K(MT_, NG_)                                                                                         \
+    skinny_kernel<MT_, SDT, NG_, skinny_d<MT_, NG_>()><<<grid, block, (size_t)sc.S * (skinny_wsz<MT_, NG_>() + 256) * 4, st>>>( \
+        q, s, n, k, x, ldx, y, ldy, m, out, sdt)
+#define QE_SK_NG(MT_)                             \
+    do {                                          \
+        if (sc.ng == 8) QE_SK_K(MT_, 8);          \
+        else if (sc.ng == 4) QE_SK_K(MT_, 4);     \
+        else if (sc.ng == 2) QE_SK_K(MT_, 2);     \
+        else QE_SK_K(MT_, 0);                     \
+    } while (0)
+    if (mt == 1) QE_SK_NG(1);
+    else if (mt == 2) QE_SK_NG(2);
+    else if (mt == 4) QE_SK_NG(4);
+    else if (mt == 8) QE_SK_NG(8);
+    else QE_SK_NG(16);
+#undef QE_SK_NG
+#undef QE_SK_K
+    HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace qe_skinny
+
+void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
+    if (w.sdt == kScaleF16) qe_skinny::launch<kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    else qe_skinny::launch<kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+}
