@@ -3,139 +3,288 @@
 // The weights are dequantized once per block tile, in registers, to the reference's bf16 operand
 // (bf16_rn((u - 8) * s) for INT4, bf16_rn(w * s) for INT8; reference gemm.cu:68-77) and staged in LDS next to the
 // activation tile; v_mfma_f32_32x32x16_bf16 consumes both from LDS.
-//   block: 256 threads (4 waves, 2 x 2), tile BM = 128 tokens x BN = 128 weight rows, BK = 64 (one W4 chunk)
-//   wave: 64 x 64 = 2 x 2 MFMA 32x32 tiles, 4 k16 steps per BK
-//   LDS: two stages of X [128][64] and W [128][64] bf16, rows of 128 B with the 16-byte chunks XOR-swizzled by
+//   block: 512 threads = 8 waves in 2 (tokens) x 4 (weight rows); wave tile WMT x WNT MFMA tiles of 32 x 32;
+//          block tile BM = 64 WMT tokens x BN = 128 WNT rows, BK = 64 (one W4 chunk)
+//   LDS: two stages of X [BM][64] and W [BN][64] bf16, rows of 128 B with the 16-byte chunks XOR-swizzled by
 //        (row % 8) so the MFMA fragment reads (32 rows x 16 B per half-wave) spread over the banks
-//   pipeline: the global loads of step k + 1 are issued before the MFMAs of step k; one barrier per step.
+//   pipeline, per k step: the MFMAs of step k read stage k % 2 while the same waves dequantize and store step k + 1
+//        (loaded during step k - 1) into the other stage; then the global loads of step k + 2 are issued and one
+//        barrier closes the step. The VALU dequantization overlaps the matrix pipe; the global loads get a step
+//        of MFMA time to arrive.
+//   grid: one block per output tile, tiles ordered so that the 8 XCDs (blockIdx % 8) each sweep a contiguous band
+//        of tiles (their L2 keeps the shared X / W tiles).
 #include "mfma_tile.hpp"
 
 namespace {
 
 using namespace qe_tile;
-constexpr int BM = 128, BN = 128, BK = 64, NTH = 256;
-constexpr int kStageBytes = (BM + BN) * BK * 2;  // 32 KB
+constexpr int BK = 64, NTH = 512;
 
 enum Fmt : int { kFmtW4 = 0, kFmtW8G = 1, kFmtW8C = 2 };
 enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
 
-template <int FMT, int SDT>
+template <int WMT, int WNT>
+struct Cfg {
+    static constexpr int BM = 64 * WMT, BN = 128 * WNT;
+    static constexpr int kStage = (BM + BN) * BK * 2;
+    static constexpr int XLD = BM * 8 / NTH;     // 16-byte X loads per thread and step (INT8 path)
+    static constexpr int XDMA = BM / 64;         // 1 KB X DMA loads per wave and step (INT4 path)
+    // INT4 path: raw W records of one k step (BN / 16 tiles x 512 B) and the scales of one group (BN / 16 x 32 B),
+    // both double-buffered after the two stages
+    static constexpr int kRaw = BN * 32, kSc = BN * 2;
+    static constexpr int kLdsW4 = 2 * kStage + 2 * kRaw + 2 * kSc;
+};
+
+// global_load_lds_dwordx4: lane i's 16 bytes land at LDS byte m0 + 16 i. Issued from inline asm so that the
+// compiler, which cannot tell these LDS writes from the stage the MFMAs read, does not wait for them before every
+// LDS read; the kernel waits for them itself (vmcnt) before the barrier that publishes the stage.
+__device__ __forceinline__ void dma16(const void* src, const char* lds_dst) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds_dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, const char* lds_dst) {  // 4 bytes per lane
+    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds_dst);
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+}
+
+template <int FMT, int SDT, int WMT, int WNT>
 __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                    int N, int K, const uint16_t* __restrict__ x, int ldx, int T,
-                                                   void* __restrict__ c, int ldc, int out, int sdt) {
+                                                   void* __restrict__ c, int ldc, int out, int sdt, int nbn, int nbt) {
+    using C = Cfg<WMT, WNT>;
+    constexpr int BM = C::BM, BN = C::BN;
+    constexpr bool W4 = FMT == kFmtW4;
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int n0 = blockIdx.x * BN, t0 = blockIdx.y * BM;
+    // XCD-aware tile order: block b runs on XCD b % 8; XCD j takes tiles [j * per, (j + 1) * per) of the
+    // n-major tile sequence (consecutive tiles share the X tile, a band of them shares W tiles)
+    const int ntiles = nbn * nbt, per = (ntiles + 7) >> 3;
+    const int b = blockIdx.x, tile = (b & 7) * per + (b >> 3);
+    if (tile >= ntiles) return;
+    const int n0 = (tile % nbn) * BN, t0 = (tile / nbn) * BM;
     const int G = K >> 7, KT = K / BK;
 
-    // ---- X loads: 4 x 16 B per thread (row = idx / 8, chunk = idx % 8)
-    u32x4_v xr[4];
+    // ---- X, INT4 path: LDS DMA (global_load_lds_dwordx4), 1 KB = 8 rows per wave instruction. Lane i lands at
+    //      LDS slot i of the 8-row block, so it loads the chunk that the swizzle puts there. Rows past T re-read
+    //      row T - 1 (their outputs are not stored).
+    auto dma_x = [&](int kt, char* xt) {
+#pragma unroll
+        for (int i = 0; i < C::XDMA; i++) {
+            const int r0 = (wave * C::XDMA + i) * 8, row = r0 + (lane >> 3);
+            const int ch = (lane & 7) ^ swz_f(row);
+            const int tok = t0 + row < T ? t0 + row : T - 1;
+            dma16(x + (size_t)tok * ldx + kt * BK + ch * 8, xt + r0 * 128);
+        }
+    };
+    // ---- X, INT8 path: XLD x 16 B per thread through registers (row = idx / 8, chunk = idx % 8)
+    u32x4_v xr[W4 ? 1 : C::XLD];
     auto load_x = [&](int kt) {
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < C::XLD; i++) {
             const int idx = tid + i * NTH, r = idx >> 3, ch = idx & 7;
             const int tok = t0 + r;
             xr[i] = tok < T ? *reinterpret_cast<const u32x4_v*>(x + (size_t)tok * ldx + kt * BK + ch * 8)
                             : u32x4_v{0u, 0u, 0u, 0u};
         }
     };
-    auto store_x = [&](char* xt) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int idx = tid + i * NTH, r = idx >> 3, ch = idx & 7;
-            *reinterpret_cast<u32x4_v*>(xt + swz(r, ch)) = xr[i];
+    auto store_x = [&](char* xt, int i) {
+        const int idx = tid + i * NTH, r = idx >> 3, ch = idx & 7;
+        *reinterpret_cast<u32x4_v*>(xt + swz(r, ch)) = xr[i];
+    };
+
+    // ---- W, INT4 path. Raw records go to LDS by DMA: a 1 KB wave load covers two 16-row tiles; lane i holds record
+    //      (tile 2 u + (i / 8) % 2, g = i % 8, t = i / 16), so that a job's reads below hit 64 distinct banks. A job =
+    //      k step j (16 k) of the row pair (g, g + 8) of a tile: word j of the tile's 4 records (g, t = 0..3) ->
+    //      4 full 16-byte chunks of the bf16 tile (rows g and g + 8, chunks 2 j and 2 j + 1).
+    constexpr int NJOB = BN * 2;
+    const bool jactive = tid < NJOB;
+    const int jj = tid & 3, jg = (tid >> 2) & 7, jtr = tid >> 5;
+    const int ntile_last = (N >> 4) - 1;
+    auto dma_w4 = [&](int kt, char* raw) {
+        if (wave < BN / 32) {
+            const int tl = min((n0 >> 4) + 2 * wave + ((lane >> 3) & 1), ntile_last);
+            dma16(q + ((size_t)tl * (K >> 6) + kt) * 32 + 4 * (lane & 7) + (lane >> 4), raw + wave * 1024);
         }
     };
-    // ---- W loads. W4: one 16 B record per thread (tile tr = tid / 32 of 8, lane wl); W8: two (slabs)
-    constexpr int WREC = FMT == kFmtW4 ? 1 : 2;
-    const int tr = tid >> 5, wl = tid & 31, wg = wl >> 2, wt4 = wl & 3;
-    const int wrow = tr * 16 + wg;  // rows wrow, wrow + 8 of the block tile
-    const bool wvalid = n0 + tr * 16 < N;
-    u32x4_v wr[WREC];
-    uint16_t sr_lo, sr_hi;
-    auto load_w = [&](int kt) {
-        const size_t tile = (size_t)(n0 >> 4) + tr;
+    auto dma_sc = [&](int grp, char* sc) {  // [BN / 16 tiles][16] scales of group grp; lane i: dword i % 8 of tile i / 8
+        if (wave < BN / 128) {
+            const int tl = min((n0 >> 4) + 8 * wave + (lane >> 3), ntile_last);
+            dma4(s + ((size_t)tl * G + grp) * 16 + 2 * (lane & 7), sc + wave * 256);
+        }
+    };
+    // dequantize half h (0: row g, 1: row g + 8) of this thread's job from the raw records into the W tile
+    auto store_w4 = [&](char* wtile, const char* raw, const char* sc, int h) {
+        if (!jactive) return;
+        const uint32_t* rw = reinterpret_cast<const uint32_t*>(raw + (jtr >> 1) * 1024) + (8 * (jtr & 1) + jg) * 4 + jj;
+        const float scl = scale_rt<SDT>(reinterpret_cast<const uint16_t*>(sc)[jtr * 16 + jg + 8 * h], sdt);
+        const float bias = -8.f * scl;
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const uint32_t wd = rw[64 * t];
+            const uint32_t u = h ? (wd >> 4) & 0x0F0F0F0Fu : wd & 0x0F0F0F0Fu;  // bytes: k0, k0+8, k0+1, k0+9
+            lo[t] = pack_bf16x2(fmaf(cvt_ubyte<0>(u), scl, bias), fmaf(cvt_ubyte<2>(u), scl, bias));
+            hi[t] = pack_bf16x2(fmaf(cvt_ubyte<1>(u), scl, bias), fmaf(cvt_ubyte<3>(u), scl, bias));
+        }
+        const int row = jtr * 16 + jg + 8 * h;
+        *reinterpret_cast<u32x4_v*>(wtile + swz(row, 2 * jj)) = u32x4_v{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u32x4_v*>(wtile + swz(row, 2 * jj + 1)) = u32x4_v{hi[0], hi[1], hi[2], hi[3]};
+    };
+
+    // ---- W, INT8 path: two 16-byte records (slabs of 32 k) per (16-row tile, lane), WREC per thread
+    constexpr int NREC = (BN / 16) * 64;
+    constexpr int WREC = NREC >= NTH ? NREC / NTH : 1;
+    const bool wactive = tid < NREC;
+    u32x4_v wr[W4 ? 1 : WREC];
+    uint16_t sr_lo[W4 ? 1 : WREC], sr_hi[W4 ? 1 : WREC];
+    auto rec_of = [&](int e, int& tr, int& slab, int& wl) {
+        const int r = tid + e * NTH;
+        tr = r >> 6, slab = (r >> 5) & 1, wl = r & 31;
+    };
+    auto load_w8 = [&](int kt) {
 #pragma unroll
         for (int e = 0; e < WREC; e++) {
-            const uint4* p = FMT == kFmtW4 ? q + (tile * (K >> 6) + kt) * 32 + wl
-                                           : q + (tile * (K >> 5) + 2 * kt + e) * 32 + wl;
-            wr[e] = wvalid ? __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p)) : u32x4_v{0u, 0u, 0u, 0u};
-        }
-        if (FMT == kFmtW8C) {
-            sr_lo = wvalid ? s[n0 + wrow] : 0;
-            sr_hi = wvalid ? s[n0 + wrow + 8] : 0;
-        } else {
-            const uint16_t* sp = s + (tile * G + (kt >> 1)) * 16;
-            sr_lo = wvalid ? sp[wg] : 0;
-            sr_hi = wvalid ? sp[wg + 8] : 0;
+            int tr, slab, wl;
+            rec_of(e, tr, slab, wl);
+            const size_t tl = (size_t)(n0 >> 4) + tr;
+            const bool v = wactive && n0 + tr * 16 < N;
+            const uint4* p = q + (tl * (K >> 5) + 2 * kt + slab) * 32 + wl;
+            wr[e] = v ? __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p)) : u32x4_v{0u, 0u, 0u, 0u};
+            const int wg = wl >> 2;
+            if (FMT == kFmtW8C) {
+                sr_lo[e] = v ? s[n0 + tr * 16 + wg] : 0;
+                sr_hi[e] = v ? s[n0 + tr * 16 + wg + 8] : 0;
+            } else {
+                const uint16_t* sp = s + (tl * G + (kt >> 1)) * 16;
+                sr_lo[e] = v ? sp[wg] : 0;
+                sr_hi[e] = v ? sp[wg + 8] : 0;
+            }
         }
     };
-    auto store_w = [&](char* wtile) {
-        const float s_lo = scale_rt<SDT>(sr_lo, sdt), s_hi = scale_rt<SDT>(sr_hi, sdt);
-        if constexpr (FMT == kFmtW4) {
+    auto store_w8 = [&](char* wtile, int d) {  // dword d (0..3) of every record of this thread
+        if (!wactive) return;
 #pragma unroll
-            for (int j = 0; j < 4; j++) dq_w4_word(wr[0][j], s_lo, s_hi, wtile, wrow, 16 * j + 2 * wt4);
-        } else {
-#pragma unroll
-            for (int e = 0; e < 2; e++)
-#pragma unroll
-                for (int d = 0; d < 4; d++)  // slab e covers k 32 e .. 32 e + 31; dword d: k step d / 2, half d % 2
-                    dq_w8_dword(wr[e][d], s_lo, s_hi, wtile, wrow, 32 * e + 16 * (d >> 1) + 8 * (d & 1) + 2 * wt4);
+        for (int e = 0; e < WREC; e++) {
+            int tr, slab, wl;
+            rec_of(e, tr, slab, wl);
+            const int wrow = tr * 16 + (wl >> 2), wt4 = wl & 3;
+            const float s_lo = scale_rt<SDT>(sr_lo[e], sdt), s_hi = scale_rt<SDT>(sr_hi[e], sdt);
+            // slab covers k 32 slab .. + 31; dword d: k step d / 2, half d % 2
+            dq_w8_dword(wr[e][d], s_lo, s_hi, wtile, wrow, 32 * slab + 16 * (d >> 1) + 8 * (d & 1) + 2 * wt4);
         }
     };
 
-    // ---- MFMA tiles: wave (wm, wn) owns tokens wm*64 .. +64, rows wn*64 .. +64
-    const int wm = wave >> 1, wn = wave & 1;
-    f32x16_v acc[2][2];
+    // ---- MFMA tiles: wave (wm, wn) owns tokens wm * 32 WMT .. , rows wn * 32 WNT ..
+    const int wm = wave >> 2, wn = wave & 3;
+    f32x16_v acc[WMT][WNT];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < WMT; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++)
+        for (int bb = 0; bb < WNT; bb++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[a][b][r] = 0.f;
+            for (int r = 0; r < 16; r++) acc[a][bb][r] = 0.f;
 
-    load_x(0);
-    load_w(0);
-    for (int kt = 0; kt < KT; kt++) {
-        char* xt = lds + (kt & 1) * kStageBytes;
-        char* wt = xt + BM * BK * 2;
-        store_x(xt);
-        store_w(wt);
-        __syncthreads();
-        if (kt + 1 < KT) {
-            load_x(kt + 1);
-            load_w(kt + 1);
-        }
+    // one k step: MFMAs on stage kt % 2 while the next step's tiles go into the other stage
+    auto mfma_step = [&](int kt, auto&& store_part) {
+        const char* xt = lds + (kt & 1) * C::kStage;
+        const char* wt = xt + BM * BK * 2;
+        // fragments of lane l: row l % 32, k = 16 ks + 8 (l / 32) .. + 8 -> chunk 2 ks + l / 32; the reads of k16
+        // step ks + 1 are issued before the MFMAs of step ks
+        bf16x8_v af[2][WMT], bfr[2][WNT];
+        auto read_frags = [&](int ks, int buf) {
+            const int fr = lane & 31, fc = 2 * ks + (lane >> 5);
+#pragma unroll
+            for (int a = 0; a < WMT; a++)
+                af[buf][a] = *reinterpret_cast<const bf16x8_v*>(xt + swz(wm * 32 * WMT + a * 32 + fr, fc));
+#pragma unroll
+            for (int bb = 0; bb < WNT; bb++)
+                bfr[buf][bb] = *reinterpret_cast<const bf16x8_v*>(wt + swz(wn * 32 * WNT + bb * 32 + fr, fc));
+        };
+        read_frags(0, 0);
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
-            // fragment of lane l: row l % 32, k = 16 ks + 8 (l / 32) .. + 8 -> chunk 2 ks + l / 32
-            const int fr = lane & 31, fc = 2 * ks + (lane >> 5);
-            bf16x8_v af[2], bfr[2];
+            if (ks + 1 < BK / 16) read_frags(ks + 1, (ks + 1) & 1);
 #pragma unroll
-            for (int a = 0; a < 2; a++)
-                af[a] = *reinterpret_cast<const bf16x8_v*>(xt + swz(wm * 64 + a * 32 + fr, fc));
+            for (int a = 0; a < WMT; a++)
 #pragma unroll
-            for (int b = 0; b < 2; b++)
-                bfr[b] = *reinterpret_cast<const bf16x8_v*>(wt + swz(wn * 64 + b * 32 + fr, fc));
+                for (int bb = 0; bb < WNT; bb++)
+                    acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][a], bfr[ks & 1][bb], acc[a][bb], 0, 0, 0);
+            store_part(ks);
+        }
+    };
+
+    if constexpr (W4) {
+        // Every global load is an LDS DMA issued at the top of a step, so the compiler tracks none of them and
+        // inserts no waits inside the step; each step ends with vmcnt(0) (its DMAs landed), lgkmcnt(0) and the
+        // barrier that publishes them. Step kt: DMA X of step kt + 1 into the other stage and the raw W of step
+        // kt + 2 (plus the scales of its group when it starts one), then the MFMAs of step kt with the dequantization
+        // of step kt + 1 (raw records published by the previous step) into the other stage.
+        char* raw = lds + 2 * C::kStage;
+        char* scb = raw + 2 * C::kRaw;
+        dma_x(0, lds);
+        dma_w4(0, raw);
+        dma_w4(1, raw + C::kRaw);
+        dma_sc(0, scb);
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+        store_w4(lds + BM * BK * 2, raw, scb, 0);
+        store_w4(lds + BM * BK * 2, raw, scb, 1);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        for (int kt = 0; kt < KT; kt++) {
+            char* st = lds + ((kt + 1) & 1) * C::kStage;
+            if (kt + 1 < KT) dma_x(kt + 1, st);
+            if (kt + 2 < KT) {
+                dma_w4(kt + 2, raw + (kt & 1) * C::kRaw);
+                if (((kt + 2) & 1) == 0) dma_sc((kt + 2) >> 1, scb + (((kt + 2) >> 1) & 1) * C::kSc);
+            }
+            const bool more = kt + 1 < KT;
+            const char* rnext = raw + ((kt + 1) & 1) * C::kRaw;
+            const char* snext = scb + (((kt + 1) >> 1) & 1) * C::kSc;
+            mfma_step(kt, [&](int ks) {
+                if (more && ks >= 2) store_w4(st + BM * BK * 2, rnext, snext, ks - 2);
+            });
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        }
+    } else {
+        load_x(0);
+        load_w8(0);
 #pragma unroll
-            for (int a = 0; a < 2; a++)
+        for (int i = 0; i < C::XLD; i++) store_x(lds, i);
 #pragma unroll
-                for (int b = 0; b < 2; b++)
-                    acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[a], bfr[b], acc[a][b], 0, 0, 0);
+        for (int d = 0; d < 4; d++) store_w8(lds + BM * BK * 2, d);
+        if (KT > 1) {
+            load_x(1);
+            load_w8(1);
+        }
+        __syncthreads();
+        for (int kt = 0; kt < KT; kt++) {
+            char* nxt = lds + ((kt + 1) & 1) * C::kStage;
+            const bool more = kt + 1 < KT;
+            mfma_step(kt, [&](int ks) {
+                if (!more) return;
+                store_w8(nxt + BM * BK * 2, ks);
+#pragma unroll
+                for (int i = 0; i < C::XLD; i++)
+                    if ((i & 3) == ks) store_x(nxt, i);
+            });
+            if (kt + 2 < KT) {
+                load_x(kt + 2);
+                load_w8(kt + 2);
+            }
+            __syncthreads();
         }
     }
 
     // ---- epilogue: lane l holds column n = l % 32 of each 32 x 32 tile, rows 8 (r / 4) + 4 (l / 32) + r % 4
     const int cj = lane & 31, ci = 4 * (lane >> 5);
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < WMT; a++)
 #pragma unroll
-        for (int b = 0; b < 2; b++) {
-            const int n = n0 + wn * 64 + b * 32 + cj;
+        for (int bb = 0; bb < WNT; bb++) {
+            const int n = n0 + wn * 32 * WNT + bb * 32 + cj;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                const int tok = t0 + wm * 64 + a * 32 + 8 * (r >> 2) + ci + (r & 3);
-                const float v = acc[a][b][r];
+                const int tok = t0 + wm * 32 * WMT + a * 32 + 8 * (r >> 2) + ci + (r & 3);
+                const float v = acc[a][bb][r];
                 if (out == kOutGLU) {
                     // gate = row g, up = row g + 8 of the 16-row tile: lanes j and j + 8
                     const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
@@ -151,19 +300,34 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         }
 }
 
+template <int FMT, int SDT, int WMT, int WNT>
+void launch_cfg(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc,
+                int out, int sdt, hipStream_t st) {
+    using C = Cfg<WMT, WNT>;
+    const int nbn = (n + C::BN - 1) / C::BN, nbt = (t + C::BM - 1) / C::BM;
+    const int ntiles = nbn * nbt, per = (ntiles + 7) / 8;
+    gemm_kernel<FMT, SDT, WMT, WNT><<<dim3((unsigned)(8 * per)), dim3(NTH), FMT == kFmtW4 ? C::kLdsW4 : 2 * C::kStage, st>>>(
+        q, s, n, k, x, ldx, t, c, ldc, out, sdt, nbn, nbt);
+    HIP_CHECK(hipGetLastError());
+}
+
+// block tile choice: 256 tokens x 256 rows when that fills the CUs in whole rounds, else 256 x 128
 template <int FMT, int SDT>
 void launch_gemm(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc,
                  int out, int sdt, hipStream_t st) {
-    const dim3 grid((unsigned)((n + BN - 1) / BN), (unsigned)((t + BM - 1) / BM)), block(NTH);
-    gemm_kernel<FMT, SDT><<<grid, block, 2 * kStageBytes, st>>>(q, s, n, k, x, ldx, t, c, ldc, out, sdt);
-    HIP_CHECK(hipGetLastError());
+    const int cus = qe_num_cus();
+    const long tiles_big = (long)((n + 255) / 256) * ((t + 255) / 256);
+    const long rounds_big = (tiles_big + cus - 1) / cus;
+    const bool big = tiles_big >= cus && (double)tiles_big / (rounds_big * cus) >= 0.9;
+    if (big) launch_cfg<FMT, SDT, 4, 2>(q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
+    else launch_cfg<FMT, SDT, 4, 1>(q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
 }
 
 void gemm_check(int n, int k, const void* x, int ldx, int ldc, int t, bool glu) {
     CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && t >= 1, "gemm %d %d %d", n, k, t);
     CHECK(ldx >= k && ldx % 8 == 0 && ((uintptr_t)x & 15) == 0, "gemm ldx %d (multiple of 8, x 16-byte aligned)", ldx);
     CHECK(ldc >= (glu ? n / 2 : n), "gemm ldc %d", ldc);
-    CHECK((size_t)t < (size_t)65535 * BM, "gemm t %d", t);
+    CHECK((long)((n + 127) / 128) * ((t + 255) / 256) < (1L << 31) / 8, "gemm t %d n %d", t, n);
 }
 
 }  // namespace

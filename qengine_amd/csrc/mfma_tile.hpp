@@ -8,8 +8,23 @@ namespace qe_tile {
 typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
 
 // byte offset of the 16-byte chunk `c` (0..7) of row `r` in a [rows][64] bf16 tile: 128-byte rows, chunks XOR-swizzled
-// by (row % 8) so that MFMA fragment reads (32 rows x 16 B per half-wave) spread over the LDS banks
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// by f(r) = (r & 7) ^ ((r >> 3) & 7). Measured on gfx950 (SQ_LDS_BANK_CONFLICT): with this f the MFMA fragment
+// reads (32 consecutive rows x one 16-byte chunk per half-wave), the 4-byte dequantized-weight stores of two
+// 16-row tiles per wave and the 16-byte row-pair stores are all conflict-free; with f = r & 7 the fragment reads
+// take 4 extra cycles per instruction.
+__device__ __forceinline__ int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 7); }
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_f(r)) << 4); }
+
+// v_cvt_f32_ubyte{B}: byte B of v as float (the compiler would extract a 4-bit field and convert byte 0 instead)
+template <int B>
+__device__ __forceinline__ float cvt_ubyte(uint32_t v) {
+    float r;
+    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
 
 template <int SDT>
 __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
@@ -24,10 +39,10 @@ __device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, 
     const uint32_t od = (wd >> 4) & 0x0F0F0F0Fu;  // slots 1, 3, 5, 7 (row g + 8)
     const float b_lo = -8.f * s_lo, b_hi = -8.f * s_hi;
     // (u - 8) * s = fma(u, s, -8 s): exact in fp32, then one rounding to bf16
-    const uint32_t g0 = pack_bf16x2(fmaf((float)(ev & 0xff), s_lo, b_lo), fmaf((float)((ev >> 16) & 0xff), s_lo, b_lo));
-    const uint32_t g8 = pack_bf16x2(fmaf((float)((ev >> 8) & 0xff), s_lo, b_lo), fmaf((float)(ev >> 24), s_lo, b_lo));
-    const uint32_t h0 = pack_bf16x2(fmaf((float)(od & 0xff), s_hi, b_hi), fmaf((float)((od >> 16) & 0xff), s_hi, b_hi));
-    const uint32_t h8 = pack_bf16x2(fmaf((float)((od >> 8) & 0xff), s_hi, b_hi), fmaf((float)(od >> 24), s_hi, b_hi));
+    const uint32_t g0 = pack_bf16x2(fmaf(cvt_ubyte<0>(ev), s_lo, b_lo), fmaf(cvt_ubyte<2>(ev), s_lo, b_lo));
+    const uint32_t g8 = pack_bf16x2(fmaf(cvt_ubyte<1>(ev), s_lo, b_lo), fmaf(cvt_ubyte<3>(ev), s_lo, b_lo));
+    const uint32_t h0 = pack_bf16x2(fmaf(cvt_ubyte<0>(od), s_hi, b_hi), fmaf(cvt_ubyte<2>(od), s_hi, b_hi));
+    const uint32_t h8 = pack_bf16x2(fmaf(cvt_ubyte<1>(od), s_hi, b_hi), fmaf(cvt_ubyte<3>(od), s_hi, b_hi));
     // k0 = 16 j + 2 t: pair (k0, k0+1) lives in chunk k0 / 8, byte (k0 % 8) * 2
     const int c0 = k0 >> 3, o0 = (k0 & 7) * 2;
     *reinterpret_cast<uint32_t*>(wt + swz(row, c0) + o0) = g0;
@@ -40,8 +55,8 @@ __device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, 
 __device__ __forceinline__ void dq_w8_dword(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k) {
     const uint32_t u = wd ^ 0x80808080u;  // w + 128
     const float b_lo = -128.f * s_lo, b_hi = -128.f * s_hi;
-    const uint32_t g = pack_bf16x2(fmaf((float)(u & 0xff), s_lo, b_lo), fmaf((float)((u >> 8) & 0xff), s_lo, b_lo));
-    const uint32_t h = pack_bf16x2(fmaf((float)((u >> 16) & 0xff), s_hi, b_hi), fmaf((float)(u >> 24), s_hi, b_hi));
+    const uint32_t g = pack_bf16x2(fmaf(cvt_ubyte<0>(u), s_lo, b_lo), fmaf(cvt_ubyte<1>(u), s_lo, b_lo));
+    const uint32_t h = pack_bf16x2(fmaf(cvt_ubyte<2>(u), s_hi, b_hi), fmaf(cvt_ubyte<3>(u), s_hi, b_hi));
     const int c = k >> 3, o = (k & 7) * 2;
     *reinterpret_cast<uint32_t*>(wt + swz(row, c) + o) = g;
     *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c) + o) = h;
