@@ -38,13 +38,12 @@ struct Cfg {
 // global_load_lds_dwordx4: lane i's 16 bytes land at LDS byte m0 + 16 i. Issued from inline asm so that the
 // compiler, which cannot tell these LDS writes from the stage the MFMAs read, does not wait for them before every
 // LDS read; the kernel waits for them itself (vmcnt) before the barrier that publishes the stage.
-__device__ __forceinline__ void dma16(const void* src, const char* lds_dst) {
-    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds_dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+// lds_dst: LDS byte address, wave-uniform
+__device__ __forceinline__ void dma16(const void* src, unsigned lds_dst) {
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
 }
-__device__ __forceinline__ void dma4(const void* src, const char* lds_dst) {  // 4 bytes per lane
-    const unsigned m0 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds_dst);
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(m0), "v"(src) : "memory", "m0");
+__device__ __forceinline__ void dma4(const void* src, unsigned lds_dst) {  // 4 bytes per lane
+    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
 }
 
 template <int FMT, int SDT, int WMT, int WNT>
@@ -55,7 +54,9 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     constexpr int BM = C::BM, BN = C::BN;
     constexpr bool W4 = FMT == kFmtW4;
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const unsigned lds32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds);  // LDS byte address of lds[]
     // XCD-aware tile order: block b runs on XCD b % 8; XCD j takes tiles [j * per, (j + 1) * per) of the
     // n-major tile sequence (consecutive tiles share the X tile, a band of them shares W tiles)
     const int ntiles = nbn * nbt, per = (ntiles + 7) >> 3;
@@ -67,13 +68,13 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     // ---- X, INT4 path: LDS DMA (global_load_lds_dwordx4), 1 KB = 8 rows per wave instruction. Lane i lands at
     //      LDS slot i of the 8-row block, so it loads the chunk that the swizzle puts there. Rows past T re-read
     //      row T - 1 (their outputs are not stored).
-    auto dma_x = [&](int kt, char* xt) {
+    auto dma_x = [&](int kt, unsigned xt) {  // xt: LDS offset of the X tile from lds[]
 #pragma unroll
         for (int i = 0; i < C::XDMA; i++) {
             const int r0 = (wave * C::XDMA + i) * 8, row = r0 + (lane >> 3);
             const int ch = (lane & 7) ^ swz_f(row);
             const int tok = t0 + row < T ? t0 + row : T - 1;
-            dma16(x + (size_t)tok * ldx + kt * BK + ch * 8, xt + r0 * 128);
+            dma16(x + (size_t)tok * ldx + kt * BK + ch * 8, lds32 + xt + r0 * 128);
         }
     };
     // ---- X, INT8 path: XLD x 16 B per thread through registers (row = idx / 8, chunk = idx % 8)
@@ -100,16 +101,16 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     const bool jactive = tid < NJOB;
     const int jj = tid & 3, jg = (tid >> 2) & 7, jtr = tid >> 5;
     const int ntile_last = (N >> 4) - 1;
-    auto dma_w4 = [&](int kt, char* raw) {
+    auto dma_w4 = [&](int kt, unsigned raw) {  // raw: LDS offset of the raw record buffer
         if (wave < BN / 32) {
             const int tl = min((n0 >> 4) + 2 * wave + ((lane >> 3) & 1), ntile_last);
-            dma16(q + ((size_t)tl * (K >> 6) + kt) * 32 + 4 * (lane & 7) + (lane >> 4), raw + wave * 1024);
+            dma16(q + ((size_t)tl * (K >> 6) + kt) * 32 + 4 * (lane & 7) + (lane >> 4), lds32 + raw + wave * 1024);
         }
     };
-    auto dma_sc = [&](int grp, char* sc) {  // [BN / 16 tiles][16] scales of group grp; lane i: dword i % 8 of tile i / 8
+    auto dma_sc = [&](int grp, unsigned sc) {  // [BN / 16 tiles][16] scales of group grp; lane i: dword i % 8 of tile i / 8
         if (wave < BN / 128) {
             const int tl = min((n0 >> 4) + 8 * wave + (lane >> 3), ntile_last);
-            dma4(s + ((size_t)tl * G + grp) * 16 + 2 * (lane & 7), sc + wave * 256);
+            dma4(s + ((size_t)tl * G + grp) * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
         }
     };
     // dequantize half h (0: row g, 1: row g + 8) of this thread's job from the raw records into the W tile
@@ -185,20 +186,25 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             for (int r = 0; r < 16; r++) acc[a][bb][r] = 0.f;
 
     // one k step: MFMAs on stage kt % 2 while the next step's tiles go into the other stage
+    int lane_off[BK / 16];  // swz(l % 32, 2 ks + l / 32) of this lane
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ks++) lane_off[ks] = swz(lane & 31, 2 * ks + (lane >> 5));
     auto mfma_step = [&](int kt, auto&& store_part) {
         const char* xt = lds + (kt & 1) * C::kStage;
         const char* wt = xt + BM * BK * 2;
         // fragments of lane l: row l % 32, k = 16 ks + 8 (l / 32) .. + 8 -> chunk 2 ks + l / 32; the reads of k16
         // step ks + 1 are issued before the MFMAs of step ks
+        // (every fragment row block is 32-aligned, so the swizzled offset is a per-lane part + a constant)
         bf16x8_v af[2][WMT], bfr[2][WNT];
         auto read_frags = [&](int ks, int buf) {
-            const int fr = lane & 31, fc = 2 * ks + (lane >> 5);
+            const char* xl = xt + lane_off[ks];
+            const char* wl = wt + lane_off[ks];
 #pragma unroll
             for (int a = 0; a < WMT; a++)
-                af[buf][a] = *reinterpret_cast<const bf16x8_v*>(xt + swz(wm * 32 * WMT + a * 32 + fr, fc));
+                af[buf][a] = *reinterpret_cast<const bf16x8_v*>(xl + (wm * 32 * WMT + a * 32) * 128);
 #pragma unroll
             for (int bb = 0; bb < WNT; bb++)
-                bfr[buf][bb] = *reinterpret_cast<const bf16x8_v*>(wt + swz(wn * 32 * WNT + bb * 32 + fr, fc));
+                bfr[buf][bb] = *reinterpret_cast<const bf16x8_v*>(wl + (wn * 32 * WNT + bb * 32) * 128);
         };
         read_frags(0, 0);
 #pragma unroll
@@ -219,22 +225,23 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         // barrier that publishes them. Step kt: DMA X of step kt + 1 into the other stage and the raw W of step
         // kt + 2 (plus the scales of its group when it starts one), then the MFMAs of step kt with the dequantization
         // of step kt + 1 (raw records published by the previous step) into the other stage.
-        char* raw = lds + 2 * C::kStage;
-        char* scb = raw + 2 * C::kRaw;
-        dma_x(0, lds);
-        dma_w4(0, raw);
-        dma_w4(1, raw + C::kRaw);
-        dma_sc(0, scb);
+        constexpr unsigned kRawOff = 2 * C::kStage, kScOff = kRawOff + 2 * C::kRaw;
+        char* raw = lds + kRawOff;
+        char* scb = lds + kScOff;
+        dma_x(0, 0);
+        dma_w4(0, kRawOff);
+        dma_w4(1, kRawOff + C::kRaw);
+        dma_sc(0, kScOff);
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
         store_w4(lds + BM * BK * 2, raw, scb, 0);
         store_w4(lds + BM * BK * 2, raw, scb, 1);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         for (int kt = 0; kt < KT; kt++) {
             char* st = lds + ((kt + 1) & 1) * C::kStage;
-            if (kt + 1 < KT) dma_x(kt + 1, st);
+            if (kt + 1 < KT) dma_x(kt + 1, ((kt + 1) & 1) * C::kStage);
             if (kt + 2 < KT) {
-                dma_w4(kt + 2, raw + (kt & 1) * C::kRaw);
-                if (((kt + 2) & 1) == 0) dma_sc((kt + 2) >> 1, scb + (((kt + 2) >> 1) & 1) * C::kSc);
+                dma_w4(kt + 2, kRawOff + (kt & 1) * C::kRaw);
+                if (((kt + 2) & 1) == 0) dma_sc((kt + 2) >> 1, kScOff + (((kt + 2) >> 1) & 1) * C::kSc);
             }
             const bool more = kt + 1 < KT;
             const char* rnext = raw + ((kt + 1) & 1) * C::kRaw;

@@ -8,11 +8,12 @@ namespace qe_tile {
 typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
 
 // byte offset of the 16-byte chunk `c` (0..7) of row `r` in a [rows][64] bf16 tile: 128-byte rows, chunks XOR-swizzled
-// by f(r) = (r & 7) ^ ((r >> 3) & 7). Measured on gfx950 (SQ_LDS_BANK_CONFLICT): with this f the MFMA fragment
+// by f(r) = (r & 7) ^ ((r >> 3) & 3). Measured on gfx950 (SQ_LDS_BANK_CONFLICT): with this f the MFMA fragment
 // reads (32 consecutive rows x one 16-byte chunk per half-wave), the 4-byte dequantized-weight stores of two
 // 16-row tiles per wave and the 16-byte row-pair stores are all conflict-free; with f = r & 7 the fragment reads
-// take 4 extra cycles per instruction.
-__device__ __forceinline__ int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 7); }
+// take 4 extra cycles per instruction. f depends on r % 32 only, so the fragment rows of a 32-aligned block share
+// one set of per-lane offsets.
+__device__ __forceinline__ int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 3); }
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_f(r)) << 4); }
 
 // v_cvt_f32_ubyte{B}: byte B of v as float (the compiler would extract a 4-bit field and convert byte 0 instead)
