@@ -50,33 +50,36 @@ __device__ __forceinline__ const char* rec_ptr(const char* recs, const MoeShape&
     return recs + ((size_t)e * sh.ngrp + g) * sh.rec;
 }
 
-// ------------------------------------------------------------------ router: one block (256 threads) per token
-constexpr int kRouteThreads = 256;
+// ------------------------------------------------------------------ router: one wave per token
+constexpr int kRouteThreads = 256;  // 4 tokens per block
 constexpr int kMaxExperts = 1024;
 
-__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int E, int topk,
-                                                                  int32_t* __restrict__ sel, float* __restrict__ w) {
-    __shared__ float bv[kRouteThreads / 64];
-    __shared__ int bi[kRouteThreads / 64];
-    __shared__ float sv[32];
-    __shared__ int si[32];
-    const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    constexpr int PER = kMaxExperts / kRouteThreads;
+// Lane l holds the logits of experts l + 64 i. Each of the topk rounds takes the lane's best untaken expert (value
+// desc; its experts ascend with i, so the first maximum is the lowest index) and reduces over the wave with the
+// tie rule (value desc, index asc): shuffles only, no barriers.
+__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
+                                                                  int topk, int32_t* __restrict__ sel,
+                                                                  float* __restrict__ w) {
+    const int lane = threadIdx.x & 63, t = blockIdx.x * (kRouteThreads / 64) + (threadIdx.x >> 6);
+    if (t >= T) return;
+    constexpr int PER = kMaxExperts / 64;
     float v[PER];
     const float* l = logits + (size_t)t * E;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
-        const int e = tid + i * kRouteThreads;
+        const int e = lane + 64 * i;
         v[i] = e < E ? l[e] : -INFINITY;
     }
     unsigned taken = 0;
+    float myv = 0.f;  // lane k keeps round k's value and index
+    int myi = 0;
+    float v0 = 0.f;
     for (int k = 0; k < topk; k++) {
-        // this thread's best untaken expert (value desc, index asc: its own experts come in ascending order)
         float bvv = -INFINITY;
         int bii = 0x7fffffff;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int e = tid + i * kRouteThreads;
+            const int e = lane + 64 * i;
             if (e < E && !(taken >> i & 1u) && (v[i] > bvv || bii == 0x7fffffff)) {
                 bvv = v[i];
                 bii = e;
@@ -91,31 +94,19 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
                 bii = i2;
             }
         }
-        if (lane == 0) {
-            bv[wave] = bvv;
-            bi[wave] = bii;
+        if ((bii & 63) == lane) taken |= 1u << (bii >> 6);
+        if (lane == k) {
+            myv = bvv;
+            myi = bii;
         }
-        __syncthreads();
-        float V = bv[0];
-        int I = bi[0];
-#pragma unroll
-        for (int q = 1; q < kRouteThreads / 64; q++)
-            if (bv[q] > V || (bv[q] == V && bi[q] < I)) {
-                V = bv[q];
-                I = bi[q];
-            }
-        if (I % kRouteThreads == tid) taken |= 1u << (I / kRouteThreads);
-        if (tid == 0) {
-            sv[k] = V;
-            si[k] = I;
-        }
-        __syncthreads();
+        if (k == 0) v0 = bvv;
     }
-    if (tid < topk) {
-        float tot = 0.f;
-        for (int k = 0; k < topk; k++) tot += expf(sv[k] - sv[0]);
-        sel[(size_t)t * topk + tid] = si[tid];
-        w[(size_t)t * topk + tid] = expf(sv[tid] - sv[0]) / tot;
+    // weights exp(l_k - l_max) / sum, the sum in k order
+    float tot = 0.f;
+    for (int k = 0; k < topk; k++) tot += expf(__shfl(myv, k) - v0);
+    if (lane < topk) {
+        sel[(size_t)t * topk + lane] = myi;
+        w[(size_t)t * topk + lane] = expf(myv - v0) / tot;
     }
 }
 
@@ -143,17 +134,40 @@ __global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t*
     __syncthreads();
     for (int i = tid; i < P; i += kSegThreads) atomicAdd(&cnt[sel[i]], 1);
     __syncthreads();
-    if (tid == 0) {  // exclusive scans over E <= 1024 entries (one thread: ~E additions)
-        int a = 0, b = 0;
-        for (int e = 0; e < E; e++) {
-            pre[e] = a;
-            jpre[e] = b;
-            a += cnt[e];
-            b += (cnt[e] + chunk - 1) / chunk;
+    {  // exclusive scans of the counts and the job counts over the E <= 1024 experts: thread e, wave scans by
+       // shuffles, then the 16 wave totals
+        __shared__ int wa[kSegThreads / 64], wb[kSegThreads / 64];
+        const int lane = tid & 63, wv = tid >> 6;
+        const int c0 = tid < E ? cnt[tid] : 0;
+        const int j0 = (c0 + chunk - 1) / chunk;
+        int a = c0, bsum = j0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const int a2 = __shfl_up(a, o), b2 = __shfl_up(bsum, o);
+            if (lane >= o) {
+                a += a2;
+                bsum += b2;
+            }
         }
-        pre[E] = a;
-        jpre[E] = b;
-        *njobs = b;
+        if (lane == 63) {
+            wa[wv] = a;
+            wb[wv] = bsum;
+        }
+        __syncthreads();
+        int ao = 0, bo = 0;
+        for (int q = 0; q < wv; q++) {
+            ao += wa[q];
+            bo += wb[q];
+        }
+        if (tid < E) {
+            pre[tid] = ao + a - c0;
+            jpre[tid] = bo + bsum - j0;
+        }
+        if (tid == E - 1) {
+            pre[E] = ao + a;
+            jpre[E] = bo + bsum;
+            *njobs = bo + bsum;
+        }
     }
     __syncthreads();
     for (int e = tid; e <= E; e += kSegThreads) off[e] = pre[e];
@@ -369,10 +383,16 @@ __global__ void __launch_bounds__(PNTH) moe_pf_kernel(const char* __restrict__ r
 __global__ void moe_combine_kernel(const uint16_t* __restrict__ slot_out, const int32_t* __restrict__ inv, int topk,
                                    int H, void* __restrict__ out, int out_bf16) {
     const int t = blockIdx.x;
+    // the token's slots, loaded once (topk <= 16), so the slot loads of all columns issue together
+    int sl[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) sl[k] = k < topk ? inv[t * topk + k] : 0;
     for (int c = threadIdx.x * 2; c < H; c += blockDim.x * 2) {
         float a0 = 0.f, a1 = 0.f;
-        for (int k = 0; k < topk; k++) {
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(slot_out + (size_t)inv[t * topk + k] * H + c);
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            if (k >= topk) break;
+            const uint32_t v = *reinterpret_cast<const uint32_t*>(slot_out + (size_t)sl[k] * H + c);
             a0 += bf16_to_f32((uint16_t)v);
             a1 += bf16_to_f32((uint16_t)(v >> 16));
         }
@@ -438,7 +458,8 @@ extern "C" {
 void qe_moe_route(const float* logits, int T, int E, int topk, int32_t* sel, float* w, void* stream) {
     CHECK(T >= 1 && E >= 1 && E <= kMaxExperts && topk >= 1 && topk <= 32 && topk <= E, "moe_route T %d E %d topk %d",
           T, E, topk);
-    moe_route_kernel<<<T, kRouteThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(logits, E, topk, sel, w);
+    moe_route_kernel<<<(T + 3) / 4, kRouteThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(logits, T, E, topk, sel,
+                                                                                              w);
     HIP_CHECK(hipGetLastError());
 }
 
@@ -470,7 +491,7 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     const int chunk = decode ? kDecRows : PBM;
     const int mj = max_jobs(T, E, topk, chunk);
 
-    moe_route_kernel<<<T, kRouteThreads, 0, st>>>(logits, E, topk, ws.sel, ws.w);
+    moe_route_kernel<<<(T + 3) / 4, kRouteThreads, 0, st>>>(logits, T, E, topk, ws.sel, ws.w);
     HIP_CHECK(hipGetLastError());
     moe_segment_kernel<<<1, kSegThreads, 0, st>>>(ws.sel, ws.w, T, E, topk, chunk, ws.off, ws.slot_pair, ws.slot_tok,
                                                   ws.slot_w, ws.inv, ws.jobs, ws.njobs);
