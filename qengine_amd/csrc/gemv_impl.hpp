@@ -59,6 +59,19 @@ __device__ __forceinline__ int x_dword(int c, int sl) {
     else return 16 * (2 * (sl >> 2) + h) + 4 * (sl & 3) + t;  // W8: load e = sl/4, dword d = sl%4
 }
 
+// inverse of x_dword: LDS position 8 c + sl of the class-major staging that holds dword d (0..63) of a group
+template <int FMT>
+__device__ __forceinline__ int x_slot(int d) {
+    if constexpr (FMT == kFmtW4) {  // d = 32 h + 8 (sl / 2) + 4 (sl % 2) + t
+        const int c = 4 * (d >> 5) + (d & 3), sl = 2 * ((d >> 3) & 3) + ((d >> 2) & 1);
+        return 8 * c + sl;
+    } else {  // d = 16 (2 (sl / 4) + h) + 4 (sl % 4) + t
+        const int q = d >> 4, r = d & 15;
+        const int c = 4 * (q & 1) + (r & 3), sl = 4 * (q >> 1) + (r >> 2);
+        return 8 * c + sl;
+    }
+}
+
 template <int SDT>
 __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
     if constexpr (SDT >= 0) return scale_to_f32<SDT>(v);
@@ -71,9 +84,10 @@ __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
 // (sp: [ng][16] rows of the tile, W8C: [16]) and, per activation row, the dword pointer of the slice's first group
 // (xw[tok], 64 dwords per group). On return (after a barrier) red[S][2][MT][16] holds the partial sums; rsum()
 // below adds them in a fixed order.
-// SDT < 0: scale dtype chosen at run time (`sdt`). PF: the activation dwords of every group are loaded up front;
-// with even slices (NG > 0) before all weights, and staged while the weights are in flight, else interleaved with
-// the weight loads of the same group (w_i, x_i, ...). !PF: loaded when the group is reached (large m).
+// SDT < 0: scale dtype chosen at run time (`sdt`). PF: the activations of every group are loaded up front; with
+// even slices (NG > 0, "UP") as 16-byte pieces before all weights (xw rows 16-byte aligned), staged and summed per
+// class while the weights are in flight, else interleaved with the weight loads of the same group (w_i, x_i, ...).
+// !PF: loaded when the group is reached (large m).
 // LDS (`lds`): per wave xl [XG][MT][64] u32 + xsum [XG][MT][8] + the slice's scales [NGM][16] half, then red
 // (XG = NG groups when PF with even slices, else 1).
 template <int MT, int FMT, int SDT, int NG, bool PF>
@@ -107,13 +121,20 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
         if (L < ndw) reinterpret_cast<uint32_t*>(sl16)[L] = reinterpret_cast<const uint32_t*>(sp)[L];
     }
     u32x4_v wv[NGM][LPG];
-    uint32_t xr[PF ? MT : 1][PF ? NGM : 1];
+    uint32_t xr[PF && !UP ? MT : 1][PF && !UP ? NGM : 1];
+    // UP: lane L loads dwords [8 L, 8 L + 8) of each row's slice (NG groups x 64 dwords) with two 16-byte loads
+    // (the slice starts 16-byte aligned: launch_gemv checks x and ldx)
+    constexpr int XL = UP ? NGM * 8 : 1;  // lanes holding activations
+    u32x4_v xv[UP ? MT : 1][2];
     qp += L;
     if constexpr (UP) {
 #pragma unroll
-        for (int i = 0; i < NGM; i++)
-#pragma unroll
-            for (int tok = 0; tok < MT; tok++) xr[tok][i] = ldx_group(tok, i);
+        for (int tok = 0; tok < MT; tok++) {
+            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xw[tok]) + 2 * L;
+            const bool ok = tok < m && L < XL;
+            xv[tok][0] = ok ? src[0] : u32x4_v{0u, 0u, 0u, 0u};
+            xv[tok][1] = ok ? src[1] : u32x4_v{0u, 0u, 0u, 0u};
+        }
     }
 #pragma unroll
     for (int i = 0; i < NGM; i++) {
@@ -138,7 +159,7 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     auto stage = [&](int i) {
 #pragma unroll
         for (int tok = 0; tok < MT; tok++) {
-            const uint32_t v = PF ? xr[PF ? tok : 0][PF ? i : 0] : ldx_group(tok, i);
+            const uint32_t v = PF && !UP ? xr[PF && !UP ? tok : 0][PF && !UP ? i : 0] : ldx_group(tok, i);
             const int xi = (UP ? i : 0) * MT + tok;
             xl[xi * 64 + L] = v;
             float sm = dot2_bf16(v, 0x3F803F80u, 0.f);  // x_lo + x_hi (bf16 (1, 1))
@@ -149,8 +170,32 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
         }
     };
     if constexpr (UP) {
+        // dword e of lane L is dword d = 8 (L % 8) + e of group L / 8, stored at its (class, slot) (x_slot, the
+        // inverse of x_dword); then lane L adds up class L % 8 of group L / 8 (16 values, in order)
+        const int gi = L >> 3, l8 = L & 7;
+        if (L < XL) {
 #pragma unroll
-        for (int i = 0; i < NGM; i++) stage(i);
+            for (int tok = 0; tok < MT; tok++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    xl[(gi * MT + tok) * 64 + x_slot<FMT>(8 * l8 + e)] = xv[tok][e >> 2][e & 3];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (L < XL) {
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) {
+                const u32x4_v* cl = reinterpret_cast<const u32x4_v*>(&xl[(gi * MT + tok) * 64 + l8 * 8]);
+                const u32x4_v a0 = cl[0], a1 = cl[1];
+                float sm = 0.f;
+#pragma unroll
+                for (int e = 0; e < 4; e++) sm = dot2_bf16(a0[e], 0x3F803F80u, sm);  // x_lo + x_hi (bf16 (1, 1))
+#pragma unroll
+                for (int e = 0; e < 4; e++) sm = dot2_bf16(a1[e], 0x3F803F80u, sm);
+                xsum[(gi * MT + tok) * 8 + l8] = bias * sm;
+            }
+        }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -312,7 +357,9 @@ void launch_gemv(const uint4* q, const uint16_t* s, int n, int k, const uint16_t
     const Slicing sc = gemv_slicing(n, k);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
     const int ngm = sc.ng > 0 ? sc.ng : kGenericNG;
-    const bool pf = mt * ngm <= 16;  // activation prefetch registers
+    // activation prefetch registers; the up-front staging of even slices loads 16-byte pieces of x
+    const bool aligned = ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
+    const bool pf = mt * ngm <= 16 && (aligned || sc.ng == 0);
     const int xg = pf && sc.ng > 0 ? sc.ng : 1;  // activation groups staged at once (gemv_tile's XG)
     const size_t lds = (size_t)sc.S * (xg * mt * 72 + ngm * 8) * 4 + (size_t)sc.S * 2 * mt * 16 * 4;  // gemv_lds_bytes
     const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);

@@ -486,6 +486,7 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     const MoeShape sh = moe_shape(E, topk, H, I);
     const MoeWs ws = moe_ws(workspace, T, E, topk, H, I);
     CHECK(workspace && ws_bytes >= ws.bytes, "moe workspace %zu < %zu bytes", ws_bytes, ws.bytes);
+    CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)workspace & 255) == 0, "moe x 16-byte / workspace 256-byte alignment");
     const char* recs = reinterpret_cast<const char*>(records);
     const bool decode = T <= 32;
     const int chunk = decode ? kDecRows : PBM;
