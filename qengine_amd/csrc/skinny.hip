@@ -75,8 +75,7 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
         const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)tile * G + gb) * 16);
         if (L < ng * 8) reinterpret_cast<uint32_t*>(sl16)[L] = sp[L];
     }
-    constexpr int XR = UPX ? NGM : D;  // activation register slots
-    uint32_t xr[XR][MT];
+    uint32_t xr[UPX ? 1 : D][MT];  // activation register slots (per-group staging)
     const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + 4 * g + qg;
     u32x4_v wv[D][2];
     auto ldw = [&](int slot, int ii) {
@@ -84,17 +83,28 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
         wv[slot][1] = ld_stream(qp + (size_t)ii * 64 + 32);
     };
     if constexpr (UPX) {
+        // lane L loads dwords [8 L, 8 L + 8) of each row's slice (16-byte pieces; x and ldx are 16-byte aligned)
+        // and stores dword 8 (L % 8) + e of group L / 8 at its class-major position
+        constexpr int XL = NGM * 8;
+        u32x4_v xv[MT][2];
+        const uint32_t* xs0 = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64;
 #pragma unroll
-        for (int ii = 0; ii < NGM; ii++)
-#pragma unroll
-            for (int tok = 0; tok < MT; tok++) xr[ii][tok] = ldxg(tok, ii);
+        for (int tok = 0; tok < MT; tok++) {
+            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xs0 + tok * xs) + 2 * L;
+            const bool ok = tok < m && L < XL;
+            xv[tok][0] = ok ? src[0] : u32x4_v{0u, 0u, 0u, 0u};
+            xv[tok][1] = ok ? src[1] : u32x4_v{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
         for (int ii = 0; ii < D; ii++)
             if (ii < ng) ldw(ii, ii);
+        if (L < XL) {
 #pragma unroll
-        for (int ii = 0; ii < NGM; ii++)
+            for (int tok = 0; tok < MT; tok++)
 #pragma unroll
-            for (int tok = 0; tok < MT; tok++) xl[(ii * MT + tok) * 64 + L] = xr[ii][tok];
+                for (int e = 0; e < 8; e++)
+                    xl[((L >> 3) * MT + tok) * 64 + x_slot<kFmtW4>(8 * (L & 7) + e)] = xv[tok][e >> 2][e & 3];
+        }
     } else {
 #pragma unroll
         for (int ii = 0; ii < D; ii++) {
