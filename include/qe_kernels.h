@@ -74,9 +74,32 @@ void qe_quantize_w8(const uint16_t* w, int n, int k, void* dq, void* ds);
 void qe_gemv_w8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m);
 
 /* gate/up row interleave into the GLU tile order (8 gate rows, 8 up rows per tile) of a compressed-tensors
- * matrix, bits 4 (int32 [n][k/8]) or 8 (int32 [n][k/4]). Replaces reference src/capi.cpp:24 (qe_glu_rows8) and
+ * matrix, bits 4 (int32 [n][k/8]) or 8 (int32 [n][k/4]). Replaces reference src/capi.cpp:23 (qe_glu_rows8) and
  * glu_interleave_rows (gemv.cu:1371-1375) for both widths. */
 void qe_glu_rows(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq, uint16_t* ds, int bits);
+
+/* ---- Q8: INT8 layer weights in the reference's Q8 byte order (src/kernels/q8_layout.h:1-37), bf16 group-128 scales
+ * in the W4 scale layout ---- */
+
+/* compressed-tensors 8-bit int32 [n][k/4] (byte b of word j = k 4j + b, u = w + 128) + bf16 [n][k/128] -> Q8 (dq:
+ * n * k bytes, ds: W4 scale layout). Replaces reference src/capi.cpp:19 (repack_q8, gemv.cu:940-957,1377-1383). */
+void qe_repack_q8(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds);
+
+/* gate/up row interleave of an 8-bit compressed-tensors matrix (GLU layout, before qe_repack_q8).
+ * Replaces reference src/capi.cpp:23 (glu_interleave_rows, bits 8). */
+void qe_glu_rows8(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq, uint16_t* ds);
+
+/* decode GEMV of a Q8 matrix, y fp32 [m][n] (glu: the bf16 activation [m][n/2]), any m (row blocks of 16).
+ * Replaces reference src/capi.cpp:28. h16 selects the reference's fp16-accumulate XH numerics there; this build
+ * computes fp32 accumulation of bf16 products for both values (xh_ws unused) and does not produce the XH copy
+ * (yh must be NULL). */
+void qe_gemv_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu, int h16,
+                void* xh_ws, void* yh);
+
+/* prefill GEMM of a Q8 matrix (bf16 MFMA on bf16_rn(w * s) tiles), y fp32 [t][n] (or bf16 after
+ * qe_gemm_set_out_bf16(1); glu: the bf16 activation [t][n/2]). Replaces reference src/capi.cpp:41. G / ci select the
+ * reference's W8A8 activation grouping and kernel candidate; this build has one numerics for every value. */
+void qe_gemm_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, int glu, int G, int ci);
 
 /* ---- build-defined entry points (no reference counterpart; BASELINE workloads: fp16 scales, bf16 out) ---- */
 

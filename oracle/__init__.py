@@ -15,6 +15,10 @@ Parity pins (each function is checked against something other than itself in tes
   w8_pos / tile_w8  bijection + inverse map of src/tools/qe_w8q.cu:34-45 + A-fragment decoder
   moe_route         brute force sort with the tie rule (numpy lexsort) + softmax renormalisation
   moe_segment       invariants (counts, contiguity, every pair once, stable order) + numpy argsort(stable)
+  q8_pos / repack_q8 the reference's own q8_layout.h (compiled into oracle/_ref when /root/reference is present)
+                    for every position, the reference's unit test (tests/q8_layout_unit.cpp, built and run there),
+                    bijection, known answers written from the layout comment (q8_layout.h:5-12)
+  dequant_q8        closed form bf16_rn((u - 128) * s) in numpy
   moe_pack          records decoded back to the source rows with the independent fragment decoder
   moe_ref           float64 composite of the pinned pieces above (the layer's checker)
 """
@@ -48,6 +52,8 @@ def lib():
         f.or_f16_to_f32.argtypes = [ctypes.c_uint16]
         f.or_w8_pos.restype = ctypes.c_size_t
         f.or_w8_pos.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        f.or_q8_pos.restype = ctypes.c_size_t
+        f.or_q8_pos.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
         f.or_silu_mul.restype = ctypes.c_float
         f.or_silu_mul.argtypes = [ctypes.c_float, ctypes.c_float]
     return _lib
@@ -172,6 +178,31 @@ def dequant_w8(q, s, n, k, per_channel, sdt):
     s = _c(s, np.uint16)
     out = np.empty((n, k), np.uint16)
     lib().or_dequant_w8(_p(q), _p(s), n, k, int(per_channel), int(sdt), _p(out))
+    return out
+
+
+# ---------------------------------------------------------------- Q8
+def q8_pos(row, k, K):
+    return lib().or_q8_pos(row, k, K)
+
+
+def repack_q8(q, s, n, k):
+    """compressed-tensors 8-bit int32 [n][k/4] (u = w + 128) + bf16 scales [n][k/128] -> (Q8 bytes [n*k],
+    scales in the W4 layout)"""
+    q = _c(q, np.int32)
+    s = _c(s, np.uint16)
+    dq = np.empty(n * k, np.uint8)
+    ds = np.empty(n * (k // 128), np.uint16)
+    lib().or_repack_q8(_p(q), _p(s), n, k, _p(dq), _p(ds))
+    return dq, ds
+
+
+def dequant_q8(q, s, n, k):
+    """-> bf16 bits [n][k] of bf16_rn((u - 128) * s) from the compressed-tensors source"""
+    q = _c(q, np.int32)
+    s = _c(s, np.uint16)
+    out = np.empty((n, k), np.uint16)
+    lib().or_dequant_q8(_p(q), _p(s), n, k, _p(out))
     return out
 
 

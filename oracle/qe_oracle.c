@@ -213,6 +213,44 @@ void or_dequant_w8(const int8_t* q, const uint16_t* s, int n, int k, int per_cha
         }
 }
 
+/* ------------------------------------------------------------------ Q8 (INT8 layer weights) */
+/* Byte position of weight (row, k) of an [N][K] matrix in the Q8 layout (reference src/kernels/q8_layout.h:29-37):
+ * q [N/16][K/32][32 lanes][16 B]; lane (g, t) of tile r, 32-k chunk c: word 2 s + hi = row 16 r + g + 8 hi,
+ * byte i = k 32 c + 16 s + 2 t + {0, 8, 1, 9}[i]. Restated from the layout comment; pinned against the header
+ * itself (oracle/_ref) and by bijection / known answers in the tests. */
+size_t or_q8_pos(int row, int k, int K) {
+    const int r = row / 16, rr = row % 16, g = rr % 8, hi = rr / 8;
+    const int c = k / 32, s = (k / 16) % 2, kk = k % 16;
+    const int t = (kk % 8) / 2;                 /* kk = 2 t + {0, 8, 1, 9} */
+    const int i = (kk >= 8 ? 1 : 0) + 2 * (kk % 2);
+    return (((size_t)r * (K / 32) + c) * 32 + g * 4 + t) * 16 + (2 * s + hi) * 4 + i;
+}
+
+/* compressed-tensors 8-bit (int32 [n][k/4], byte b of word j = k 4 j + b, stored u = w + 128; reference
+ * tools/quant_int8.py:102-105) + bf16 group-128 scales [n][k/128] -> Q8 bytes (signed w) + W4 scale layout
+ * (reference repack_q8 gemv.cu:940-957, 1377-1383) */
+void or_repack_q8(const int32_t* q, const uint16_t* s, int n, int k, uint8_t* dq, uint16_t* ds) {
+    for (int r = 0; r < n; r++)
+        for (int c = 0; c < k; c++) {
+            const uint32_t u = ((uint32_t)q[(size_t)r * (k / 4) + c / 4] >> (8 * (c % 4))) & 0xFFu;
+            dq[or_q8_pos(r, c, k)] = (uint8_t)(u ^ 0x80u);
+        }
+    const int G = k / 128;
+    for (int r = 0; r < n; r++)
+        for (int gi = 0; gi < G; gi++) ds[((size_t)(r / 16) * G + gi) * 16 + r % 16] = s[(size_t)r * G + gi];
+}
+
+/* compressed-tensors 8-bit source -> bf16 [n][k] = bf16_rn((u - 128) * s) */
+void or_dequant_q8(const int32_t* q, const uint16_t* s, int n, int k, uint16_t* out) {
+    const int G = k / 128;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < n; r++)
+        for (int c = 0; c < k; c++) {
+            const int u = (int)(((uint32_t)q[(size_t)r * (k / 4) + c / 4] >> (8 * (c % 4))) & 0xFFu);
+            out[(size_t)r * k + c] = or_f32_to_bf16((float)(u - 128) * or_bf16_to_f32(s[(size_t)r * G + c / 128]));
+        }
+}
+
 /* ------------------------------------------------------------------ MoE */
 /* Router (reference flash_kernels.cuh:4351-4399 k_topk_rows; 4006-4089 k_route): top-`topk` experts of each
  * row by logit, ties: lower index first; weights w_i = exp(l_i - l_max) / sum_sel exp(l_j - l_max) (softmax

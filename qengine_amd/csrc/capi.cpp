@@ -111,6 +111,41 @@ void qe_glu_rows(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq,
     glu_interleave_rows(q, s, n, k, dq, ds, 0, bits);
 }
 
+// ---- Q8 (INT8 layer weights in the q8_layout.h byte order) ----
+void qe_repack_q8(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds) {
+    repack_q8(q, s, n, k, reinterpret_cast<uint4*>(dq), reinterpret_cast<uint16_t*>(ds), 0);
+}
+
+void qe_glu_rows8(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq, uint16_t* ds) {
+    glu_interleave_rows(q, s, n, k, dq, ds, 0, 8);
+}
+
+void qe_gemv_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu, int h16,
+                void* xh_ws, void* yh) {
+    (void)h16;
+    (void)xh_ws;
+    CHECK(yh == nullptr, "qe_gemv_q8: the fp16 (XH) activation copy yh is not produced by this build");
+    gemv_workspace_init();
+    W8 w = mk_w8(q, s, n, k, false, kScaleBF16);
+    w.q8 = true;
+    w.glu = glu != 0;
+    const int ldy = glu ? n / 2 : n;
+    const size_t esz = glu ? 2 : 4;
+    for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
+        const int mm = m - r0 < kMaxGemvRows ? m - r0 : kMaxGemvRows;
+        gemv_w8(w, x + (size_t)r0 * k, k, reinterpret_cast<char*>(y) + (size_t)r0 * ldy * esz, ldy, mm, false, 0);
+    }
+}
+
+void qe_gemm_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, int glu, int G, int ci) {
+    (void)G;
+    (void)ci;
+    W8 w = mk_w8(q, s, n, k, false, kScaleBF16);
+    w.q8 = true;
+    w.glu = glu != 0;
+    gemm_w8(w, x, k, y, glu ? n / 2 : n, t, !glu && gemm_out_bf16(), 0);
+}
+
 // ---------------------------------------------------------------- build-defined entry points
 void qe_dequant_w4(const void* q, const void* s, int n, int k, int flags, uint16_t* out, void* st) {
     dequant_w4(mk_w4(q, s, n, k, false, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), out, as_stream(st));

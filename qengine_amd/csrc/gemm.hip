@@ -20,7 +20,7 @@ namespace {
 using namespace qe_tile;
 constexpr int BK = 64, NTH = 512;
 
-enum Fmt : int { kFmtW4 = 0, kFmtW8G = 1, kFmtW8C = 2 };
+enum Fmt : int { kFmtW4 = 0, kFmtW8G = 1, kFmtW8C = 2, kFmtQ8 = 3 };
 enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
 
 template <int WMT, int WNT>
@@ -170,8 +170,10 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             rec_of(e, tr, slab, wl);
             const int wrow = tr * 16 + (wl >> 2), wt4 = wl & 3;
             const float s_lo = scale_rt<SDT>(sr_lo[e], sdt), s_hi = scale_rt<SDT>(sr_hi[e], sdt);
-            // slab covers k 32 slab .. + 31; dword d: k step d / 2, half d % 2
-            dq_w8_dword(wr[e][d], s_lo, s_hi, wtile, wrow, 32 * slab + 16 * (d >> 1) + 8 * (d & 1) + 2 * wt4);
+            if constexpr (FMT == kFmtQ8)  // word d = 2 s + hi: row + 8 hi, k 32 slab + 16 s + 2 t (+1, +8, +9)
+                dq_q8_word(wr[e][d], (d & 1) ? s_hi : s_lo, wtile, wrow + 8 * (d & 1), 32 * slab + 16 * (d >> 1) + 2 * wt4);
+            else  // slab covers k 32 slab .. + 31; dword d: k step d / 2, half d % 2
+                dq_w8_dword(wr[e][d], s_lo, s_hi, wtile, wrow, 32 * slab + 16 * (d >> 1) + 8 * (d & 1) + 2 * wt4);
         }
     };
 
@@ -347,9 +349,11 @@ void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, b
 }
 
 void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st) {
-    gemm_check(w.n, w.k, x, ldx, ldc, t, false);
-    const int out = out_bf16 ? kOutBF16 : kOutF32;
-    if (w.per_channel) launch_gemm<kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
+    gemm_check(w.n, w.k, x, ldx, ldc, t, w.glu);
+    CHECK(!w.glu || w.q8, "gemm_w8: GLU is for Q8 matrices");
+    const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    if (w.q8) launch_gemm<kFmtQ8, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
+    else if (w.per_channel) launch_gemm<kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
     else launch_gemm<kFmtW8G, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
 }
 

@@ -23,7 +23,7 @@ namespace qe_gemv {
 
 typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
 
-enum Fmt : int { kFmtW4 = 0, kFmtW8G = 1, kFmtW8C = 2 };
+enum Fmt : int { kFmtW4 = 0, kFmtW8G = 1, kFmtW8C = 2, kFmtQ8 = 3 };
 enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
 constexpr int kMaxWaves = 8;      // K slices per block (even slicing)
 constexpr int kGenericNG = 16;    // max groups per slice of the generic (uneven slices) variant
@@ -242,6 +242,33 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
                     a_hi[tok] = dot2_bf16(p[j][1], xv[2 * j], a_hi[tok]);
                     a_hi[tok] = dot2_bf16(p[j][3], xv[2 * j + 1], a_hi[tok]);
                 }
+            }
+        } else if constexpr (FMT == kFmtQ8) {
+            // word 2 s + hi of wave-load e: row g + 8 hi, bytes (k0, k0 + 8, k0 + 1, k0 + 9) with k0 = the x slot
+            // 4 e + 2 s; bytes 0 / 2 pair with slot 4 e + 2 s, bytes 1 / 3 with 4 e + 2 s + 1
+            uint32_t plo[2][4], phi[2][4];  // [e][2 s + b]
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+#pragma unroll
+                for (int sq = 0; sq < 2; sq++) {
+                    const uint32_t ug = wv[i][e][2 * sq] ^ 0x80808080u, uh = wv[i][e][2 * sq + 1] ^ 0x80808080u;
+                    plo[e][2 * sq] = pack_bf16x2((float)(ug & 0xffu), (float)((ug >> 16) & 0xffu));
+                    plo[e][2 * sq + 1] = pack_bf16x2((float)((ug >> 8) & 0xffu), (float)(ug >> 24));
+                    phi[e][2 * sq] = pack_bf16x2((float)(uh & 0xffu), (float)((uh >> 16) & 0xffu));
+                    phi[e][2 * sq + 1] = pack_bf16x2((float)((uh >> 8) & 0xffu), (float)(uh >> 24));
+                }
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) {
+                const u32x4_v x0 = *reinterpret_cast<const u32x4_v*>(&xl[(xg + tok) * 64 + cls * 8]);
+                const u32x4_v x1 = *reinterpret_cast<const u32x4_v*>(&xl[(xg + tok) * 64 + cls * 8 + 4]);
+                const uint32_t xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                for (int e = 0; e < 2; e++)
+#pragma unroll
+                    for (int d = 0; d < 4; d++) {
+                        a_lo[tok] = dot2_bf16(plo[e][d], xv[4 * e + d], a_lo[tok]);
+                        a_hi[tok] = dot2_bf16(phi[e][d], xv[4 * e + d], a_hi[tok]);
+                    }
             }
         } else {
             uint32_t plo[2][4], phi[2][4];

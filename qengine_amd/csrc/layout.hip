@@ -135,7 +135,36 @@ __global__ void dequant_w8_kernel(const uint8_t* __restrict__ q, const uint16_t*
 
 unsigned grid_for(size_t items, int block) { return (unsigned)((items + block - 1) / block); }
 
+// compressed-tensors 8-bit -> Q8: one thread per destination word (lane (g, t), word 2 s + hi of tile r, 32-k chunk
+// c): its 4 bytes are rows g + 8 hi at k = 32 c + 16 s + 2 t + {0, 8, 1, 9}, each u ^ 0x80 = the signed weight
+__global__ void repack_q8_kernel(const int32_t* __restrict__ src, int N, int K, uint32_t* __restrict__ dst) {
+    const size_t idx = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (idx >= (size_t)N * K / 4) return;
+    const int word = idx & 3, lane = (idx >> 2) & 31;
+    const size_t tc = idx >> 7;  // tile * (K / 32) + chunk
+    const int r = (int)(tc / (K >> 5)), c = (int)(tc % (K >> 5));
+    const int row = 16 * r + (lane >> 2) + 8 * (word & 1);
+    const int k0 = 32 * c + 16 * (word >> 1) + 2 * (lane & 3);
+    const uint32_t* sr = reinterpret_cast<const uint32_t*>(src) + (size_t)row * (K >> 2);
+    uint32_t v = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int k = k0 + (i & 1) * 8 + (i >> 1);
+        v |= (((sr[k >> 2] >> (8 * (k & 3))) & 0xFFu) ^ 0x80u) << (8 * i);
+    }
+    dst[idx] = v;
+}
+
 }  // namespace
+
+void repack_q8(const int32_t* src_q, const uint16_t* src_s, int n, int k, uint4* dst_q, uint16_t* dst_s,
+               hipStream_t st) {
+    CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0, "repack_q8 %d %d", n, k);
+    const size_t words = (size_t)n * k / 4, ns = (size_t)n * (k / 128);
+    repack_q8_kernel<<<grid_for(words, 256), 256, 0, st>>>(src_q, n, k, reinterpret_cast<uint32_t*>(dst_q));
+    repack_scales_kernel<<<grid_for(ns, 256), 256, 0, st>>>(src_s, n, k / 128, dst_s);
+    HIP_CHECK(hipGetLastError());
+}
 
 void repack_w4(const int32_t* src_q, const uint16_t* src_s, int n, int k, uint4* dst_q, uint16_t* dst_s,
                hipStream_t st) {

@@ -18,12 +18,16 @@ struct W4 {
 };
 // W8 layout (symmetric INT8), reference gemv.cuh:33-40: q [N/16][K/32][32 lanes][16 bytes].
 // group 128 (reference): s [N/16][K/128][16] bf16. per-channel (this build): s [N] fp16 (group = K).
+// Q8 layout (reference q8_layout.h:1-37, INT8 layer weights): same [N/16][K/32][32][16 B] records, word 2 s + hi =
+// row g + 8 hi, bytes i = k 32 c + 16 s + 2 t + {0, 8, 1, 9}[i]; group-128 scales in the W4 scale layout.
 struct W8 {
     const uint4* q = nullptr;
     const uint16_t* s = nullptr;
     int n = 0, k = 0;
     bool per_channel = false;
     int sdt = kScaleBF16;
+    bool q8 = false;   // Q8 byte order instead of W8
+    bool glu = false;  // GLU matrix (Q8 layer weights)
 };
 
 // ---- layouts (load time) ----
@@ -36,6 +40,9 @@ void quantize_w8(const uint16_t* src, int n, int k, uint4* dst_q, uint16_t* dst_
 void tile_w8(const int8_t* src, const uint16_t* ssrc, int n, int k, uint4* dst_q, uint16_t* dst_s,
              bool per_channel, hipStream_t st);
 void dequant_w8(const W8& w, uint16_t* out, hipStream_t st);  // bf16 [n][k] = bf16_rn(w * s)
+// compressed-tensors 8-bit int32 [n][k/4] (u = w + 128) + [n][k/128] scales -> Q8 bytes + W4 scale layout
+void repack_q8(const int32_t* src_q, const uint16_t* src_s, int n, int k, uint4* dst_q, uint16_t* dst_s,
+               hipStream_t st);
 
 // ---- decode GEMV / skinny GEMM (m = 1..16), VALU, deterministic split-K ----
 void gemv_workspace_init();

@@ -161,6 +161,49 @@ def gemm_w8(w: W8, x, out_bf16=False, y=None):
     return y
 
 
+@dataclass
+class Q8:
+    """INT8 layer weights in the reference's Q8 byte order (src/kernels/q8_layout.h), bf16 group-128 scales"""
+    q: torch.Tensor
+    s: torch.Tensor
+    n: int
+    k: int
+    glu: bool = False
+
+
+def repack_q8(q, s, glu=False):
+    """compressed-tensors 8-bit int32 [n][k/4] (u = w + 128) + bf16 scales [n][k/128] -> Q8 (reference hooks
+    qe_glu_rows8 / qe_repack_q8)"""
+    n, k = q.shape[0], q.shape[1] * 4
+    assert s.dtype == torch.bfloat16 and s.shape == (n, k // 128)
+    if glu:
+        q2, s2 = torch.empty_like(q), torch.empty_like(s)
+        call("qe_glu_rows8", q.contiguous(), s.contiguous(), n, k, q2, s2)
+        q, s = q2, s2
+    dq = torch.empty(n * k, dtype=torch.uint8, device=q.device)
+    ds = torch.empty(n * (k // 128), dtype=torch.bfloat16, device=q.device)
+    call("qe_repack_q8", q.contiguous(), s.contiguous(), n, k, dq, ds)
+    return Q8(dq, ds, n, k, glu)
+
+
+def gemv_q8(w: Q8, x):
+    """decode GEMV (any m): fp32 [m][n], or the GLU bf16 activation [m][n/2] (reference hook qe_gemv_q8)"""
+    m = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.is_contiguous()
+    y = _out(m, w.n, False, w.glu, x.device)
+    call("qe_gemv_q8", w.q, w.s, w.n, w.k, x, y, m, int(w.glu), 0, None, None)
+    return y
+
+
+def gemm_q8(w: Q8, x):
+    """prefill GEMM: fp32 [t][n], or the GLU bf16 activation [t][n/2] (reference hook qe_gemm_q8)"""
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.is_contiguous()
+    y = _out(t, w.n, False, w.glu, x.device)
+    call("qe_gemm_q8", w.q, w.s, w.n, w.k, x, y, t, int(w.glu), 0, 0)
+    return y
+
+
 class MoE:
     """One MoE layer of E INT4 experts in the group-record format (see include/qe_kernels.h)."""
 

@@ -1,6 +1,10 @@
 """Pins of the CPU oracle (oracle/qe_oracle.c) against checks that do not restate its own formulas:
 library dtype conversions, the PTX ISA mma.m16n8k16 A-fragment table, hand-computed known answers, numpy
 float64 matmul, brute-force ranking, invariants. CPU only."""
+import ctypes
+import os
+import subprocess
+
 import numpy as np
 import pytest
 import torch
@@ -276,3 +280,56 @@ def test_moe_pack_decodes_to_source_rows():
             ud = _decode_w4_fragments(parts[2].view(np.uint32), H, 128)
             assert np.array_equal(ud, oracle.unpack_w4(dq[e], H, I)[:, 128 * g:128 * g + 128] + 8)
             assert np.array_equal(parts[3].view(np.uint16), ds[e][:, g])
+
+
+# ---------------------------------------------------------------- Q8 layout (reference src/kernels/q8_layout.h)
+_REF_DIR = os.path.join(os.path.dirname(oracle.__file__), "_ref")
+
+
+def test_q8_pos_known_answers_and_bijection():
+    """positions written from the layout comment (q8_layout.h:5-12): word 2 s + hi of lane (g, t) of tile r and
+    32-k chunk c holds row 16 r + g + 8 hi, bytes i = k 32 c + 16 s + 2 t + {0, 8, 1, 9}[i]"""
+    K = 256
+    kat = {(0, 0): 0, (0, 8): 1, (0, 1): 2, (0, 9): 3, (8, 0): 4, (0, 16): 8, (8, 16): 12,
+           (0, 2): 16, (1, 0): 64, (0, 32): 512, (16, 0): (K // 32) * 512, (17, 35): (K // 32) * 512 + 512 + 4 * 16 + 16 + 2}
+    for (r, k), pos in kat.items():
+        assert oracle.q8_pos(r, k, K) == pos, (r, k)
+    n = 32
+    pos = [oracle.q8_pos(r, k, K) for r in range(n) for k in range(K)]
+    assert sorted(pos) == list(range(n * K))
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(_REF_DIR, "libq8ref.so")), reason="oracle/_ref not built")
+def test_q8_pos_matches_reference_header():
+    ref = ctypes.CDLL(os.path.join(_REF_DIR, "libq8ref.so"))
+    ref.ref_q8_pos.restype = ctypes.c_size_t
+    ref.ref_q8_pos.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int]
+    for n, K in ((64, 256), (48, 512)):
+        for r in range(n):
+            for k in range(K):
+                assert oracle.q8_pos(r, k, K) == ref.ref_q8_pos(r, k, K), (r, k, K)
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(_REF_DIR, "q8_layout_unit")), reason="oracle/_ref not built")
+def test_q8_reference_unit_test_passes():
+    """the reference's own known-answer test of the Q8 layout (tests/q8_layout_unit.cpp), built from its sources"""
+    out = subprocess.run([os.path.join(_REF_DIR, "q8_layout_unit")], capture_output=True, text=True, timeout=60)
+    assert out.returncode == 0 and "ok (0 failures)" in out.stdout, out.stdout
+
+
+def test_repack_q8_places_signed_weights():
+    """compressed-tensors source (byte b of word j = k 4 j + b, u = w + 128) -> Q8 byte at q8_pos = w (int8)"""
+    n, k = 32, 256
+    rng = np.random.default_rng(3)
+    w = rng.integers(-128, 128, size=(n, k)).astype(np.int32)
+    u = (w + 128).astype(np.uint32).reshape(n, k // 4, 4)
+    q = (u[..., 0] | (u[..., 1] << 8) | (u[..., 2] << 16) | (u[..., 3] << 24)).view(np.int32)
+    s = synth.np_bf16(np.abs(rng.standard_normal((n, k // 128))).astype(np.float32) * 0.01)
+    dq, ds = oracle.repack_q8(q, s, n, k)
+    for r in range(0, n, 7):
+        for c in range(0, k, 5):
+            assert dq[oracle.q8_pos(r, c, k)].astype(np.int8) == w[r, c]
+    assert np.array_equal(ds.reshape(n // 16, k // 128, 16).transpose(0, 2, 1).reshape(n, k // 128), s)
+    deq = oracle.dequant_q8(q, s, n, k)
+    ref = synth.np_bf16(w.astype(np.float32) * np.repeat(oracle.bf16_to_f32(s), 128, axis=1))
+    assert np.array_equal(deq, ref)
