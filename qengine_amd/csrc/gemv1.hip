@@ -1,0 +1,227 @@
+// Decode GEMV for one activation row (m = 1) on the W4 layout, with the multiply-adds on the matrix cores.
+//
+// The VALU GEMV (gemv_impl.hpp) spends one v_dot2 per weight pair next to the unpack, and at m = 1 its VALU
+// work, not HBM, sets the time. Here each lane keeps the W4 record it loads (one coalesced 1 KB wave-load per
+// 128-k group, the layout unchanged) and v_mfma_f32_16x16x32_bf16 does the products:
+//   * lane L = 16 q + c holds W4 lane L % 32 of chunk L / 32: rows g = 4 (q & 1) + c / 4 (low nibbles) and
+//     g + 8 (high nibbles), k = 64 h + 16 j + 2 t + {0, 1, 8, 9}, h = q / 2, t = c % 4, j = 0..3. As an MFMA A
+//     operand, lane (q, c) is A row c with k slots 8 q .. 8 q + 7; its eight values of one row for words j, j + 1
+//     are one operand: ((w >> sh) & 0x000F000F) | 0x43004300 is the bf16 pair 128 + u of k, k + 1 (sh = 0 / 8
+//     for row g, 4 / 12 for row g + 8).
+//   * Lanes of one A row c hold different k sets (t = c % 4 and h differ), so B is block diagonal: column
+//     4 q + t of k block q holds the activations of class (h = q / 2, t), every other entry is 0. Output entry
+//     D[c][4 q + (c % 4)] is then exactly lane (q, c)'s own dot product; lane L of D holds it in register c % 4
+//     (D rows 4 q' .. 4 q' + 3 of column c'), for row g = 4 ((c' / 4) & 1) + q' of class (h = c' / 8, t = c' % 4).
+//     The activations are staged class-major in LDS, so a B operand is one ds_read_b128; lanes off the diagonal
+//     read a zeroed block.
+//   * The bias (u = w + 8 over the 128 of the magic) enters as the MFMA's initial C: -136 times the class sum
+//     of the activations, computed once per group at staging. D = sum (u - 8) x exactly (products exact in fp32).
+//   * Per group: acc += s * D (the group scale of the lane's row), the other three registers are carried along
+//     unused. At the end the lane keeps register c % 4, the quad (t) and the two chunk halves (h) are added by
+//     DPP, and the K slices (waves) through LDS in a fixed order: deterministic.
+// Per lane and group that is 28 VALU for the unpack and 8 for the scales, against about 60 for the VALU GEMV.
+#include "gemv_impl.hpp"
+
+namespace qe_gemv1 {
+using namespace qe_gemv;
+
+// LDS per wave (dwords): xl [NG][64] activations class-major, zero [NG][64], xsum [NG][8] (-136 x class sums),
+// scales [NG][16] half; then red [S][16] floats for the block
+template <int NG>
+constexpr int wave_dwords() {
+    return NG * 64 * 2 + NG * 8 + NG * 8;
+}
+
+// NG groups per wave (K slice), D weight records in flight per lane (a sliding window: the load of group i + D is
+// issued once group i has been unpacked). Every wave then receives its weights spread over the whole stream
+// instead of in one burst, so the compute left after the last bytes arrive is one group, not a whole slice.
+template <int NG, int D, int SDT>
+__global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
+gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K,
+             const uint16_t* __restrict__ x, void* __restrict__ y, int out) {
+    constexpr int WSZ = wave_dwords<NG>();
+    constexpr int NP = NG * 8;              // 8-dword activation pieces (and scale dwords, class sums) of a slice
+    constexpr int NR = (NP + 63) / 64;      // pieces per lane
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const int tile = blockIdx.x, G = K >> 7, gb = w * NG;
+    uint32_t* xl = lds + (size_t)w * WSZ;                          // [NG][64]
+    uint32_t* zr = xl + NG * 64;                                     // [NG][64] zeros
+    float* xsum = reinterpret_cast<float*>(zr + NG * 64);            // [NG][8]
+    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xsum + NG * 8);     // [NG][16]
+    float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][16]
+
+    // 1. loads, no wait between them: the activation pieces of the slice (piece p = L + 64 r: dwords 8 p .. 8 p + 7,
+    //    group p / 8), the slice's scales (dword p), then the first D groups of weight records. Addresses are
+    //    clamped rather than branched on, so nothing waits before the weight stream starts.
+    const uint32_t* xs0 = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64;
+    const uint32_t* ss0 = reinterpret_cast<const uint32_t*>(s + ((size_t)tile * G + gb) * 16);
+    u32x4_v xv[NR][2];
+    uint32_t sraw[NR];
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int p = L + 64 * r < NP ? L + 64 * r : NP - 1;
+        xv[r][0] = reinterpret_cast<const u32x4_v*>(xs0)[2 * p];
+        xv[r][1] = reinterpret_cast<const u32x4_v*>(xs0)[2 * p + 1];
+        sraw[r] = ss0[p];
+    }
+    const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + L;
+    u32x4_v wv[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) wv[i] = ld_stream(qp + (size_t)i * 64);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. staging: zero block, scales, activations class-major (x_slot), then the class sums times -136
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int p = L + 64 * r;
+        if (p < NP) {
+            const int gi = p >> 3, l8 = p & 7;
+            const u32x4_v z4 = {0u, 0u, 0u, 0u};
+            *reinterpret_cast<u32x4_v*>(&zr[8 * p]) = z4;
+            *reinterpret_cast<u32x4_v*>(&zr[8 * p + 4]) = z4;
+            reinterpret_cast<uint32_t*>(sl16)[p] = sraw[r];
+#pragma unroll
+            for (int e = 0; e < 8; e++) xl[gi * 64 + x_slot<kFmtW4>(8 * l8 + e)] = e < 4 ? xv[r][0][e] : xv[r][1][e - 4];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int r = 0; r < NR; r++) {
+        const int p = L + 64 * r;
+        if (p < NP) {
+            const u32x4_v* cl = reinterpret_cast<const u32x4_v*>(&xl[(p >> 3) * 64 + (p & 7) * 8]);
+            const u32x4_v a0 = cl[0], a1 = cl[1];
+            float sm = 0.f;
+#pragma unroll
+            for (int e = 0; e < 4; e++) sm = dot2_bf16(a0[e], 0x3F803F80u, sm);  // x_lo + x_hi (bf16 (1, 1))
+#pragma unroll
+            for (int e = 0; e < 4; e++) sm = dot2_bf16(a1[e], 0x3F803F80u, sm);
+            xsum[p] = -136.f * sm;
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 3. per group: 4 MFMAs (rows g / g + 8 x words 0-1 / 2-3), acc += s * D
+    const int qb = L >> 4, c = L & 15;
+    const bool diag = (c >> 2) == qb;
+    // B operand base: class 4 (q / 2) + c % 4 of the staged activations on the diagonal, else the zero block
+    const uint32_t* bb = diag ? &xl[(4 * (qb >> 1) + (c & 3)) * 8] : zr;
+    const float* cb = &xsum[4 * (c >> 3)];  // class sums of classes 4 (c / 8) .. + 3 (register r <-> t = r)
+    const int grow = 4 * ((c >> 2) & 1) + qb;  // row (low nibbles) of the lane's useful D entry
+    const uint32_t kMask = 0x000F000Fu, kMagic = 0x43004300u;
+    f32x4_v acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const u32x4_v b01 = *reinterpret_cast<const u32x4_v*>(bb + i * 64);
+        const u32x4_v b23 = *reinterpret_cast<const u32x4_v*>(bb + i * 64 + 4);
+        const f32x4_v c0 = *reinterpret_cast<const f32x4_v*>(cb + i * 8);
+        const float s_lo = scale_to_f32<SDT>(sl16[i * 16 + grow]);
+        const float s_hi = scale_to_f32<SDT>(sl16[i * 16 + grow + 8]);
+        const u32x4_v r = wv[i % D];
+        // the eight values of row g (sh = 0) or g + 8 (sh = 4) in words j, j + 1
+        auto opnd = [&](int j, int sh) {
+            const u32x4_v a = {and_or(r[j] >> sh, kMask, kMagic), and_or(r[j] >> (sh + 8), kMask, kMagic),
+                               and_or(r[j + 1] >> sh, kMask, kMagic), and_or(r[j + 1] >> (sh + 8), kMask, kMagic)};
+            return __builtin_bit_cast(bf16x8_v, a);
+        };
+        const bf16x8_v A0 = opnd(0, 0), A1 = opnd(0, 4), A2 = opnd(2, 0), A3 = opnd(2, 4);
+        // the window: group i's record is unpacked, its registers take group i + D
+        if (i + D < NG) wv[i % D] = ld_stream(qp + (size_t)(i + D) * 64);
+        const bf16x8_v B01 = __builtin_bit_cast(bf16x8_v, b01), B23 = __builtin_bit_cast(bf16x8_v, b23);
+        f32x4_v dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B01, c0, 0, 0, 0);
+        f32x4_v dh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B01, c0, 0, 0, 0);
+        dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A2, B23, dl, 0, 0, 0);
+        dh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A3, B23, dh, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            acc_lo[e] = fmaf(s_lo, dl[e], acc_lo[e]);
+            acc_hi[e] = fmaf(s_hi, dh[e], acc_hi[e]);
+        }
+        // the accumulators are consumed here (an empty asm), so the FMAs are not sunk to the end of the kernel
+        // (the compiler would keep every group's D live)
+        asm volatile("" : "+v"(acc_lo), "+v"(acc_hi));
+    }
+
+    // 4. the lane's entry is register c % 4; add the quad (t) and the two chunks (h, lanes c and c + 8)
+    const int rr = c & 3;
+    float vlo = rr == 0 ? acc_lo[0] : rr == 1 ? acc_lo[1] : rr == 2 ? acc_lo[2] : acc_lo[3];
+    float vhi = rr == 0 ? acc_hi[0] : rr == 1 ? acc_hi[1] : rr == 2 ? acc_hi[2] : acc_hi[3];
+    vlo = dpp_add<kDppXor1>(vlo);
+    vhi = dpp_add<kDppXor1>(vhi);
+    vlo = dpp_add<kDppXor2>(vlo);
+    vhi = dpp_add<kDppXor2>(vhi);
+    constexpr int kDppRowRor8 = 0x128;  // row_ror:8 (lane c <- lane (c + 8) % 16 of the row)
+    vlo = dpp_add<kDppRowRor8>(vlo);
+    vhi = dpp_add<kDppRowRor8>(vhi);
+    if ((c & 11) == 0) {  // c = 0: rows q, q + 8; c = 4: rows 4 + q, 12 + q
+        red[w * 16 + grow] = vlo;
+        red[w * 16 + grow + 8] = vhi;
+    }
+    __syncthreads();
+    const int row0 = 16 * tile;
+    if (out == kOutGLU) {
+        if (threadIdx.x < 8) {
+            const int gg = threadIdx.x;
+            float a = 0.f, b = 0.f;
+            for (int ws = 0; ws < S; ws++) {
+                a += red[ws * 16 + gg];
+                b += red[ws * 16 + gg + 8];
+            }
+            reinterpret_cast<uint16_t*>(y)[row0 / 2 + gg] = f32_to_bf16(silu_f32(a) * b);
+        }
+    } else if (threadIdx.x < 16) {
+        const int rw = threadIdx.x;
+        float v = 0.f;
+        for (int ws = 0; ws < S; ws++) v += red[ws * 16 + rw];
+        if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[row0 + rw] = f32_to_bf16(v);
+        else reinterpret_cast<float*>(y)[row0 + rw] = v;
+    }
+}
+
+// K slicing of the m = 1 kernel: groups per wave NG in {10, 8, 5, 4, 2} dividing K / 128 with at most 8 waves
+// per block, the largest NG whose grid still gives ~12 waves per CU (the window keeps the loads in flight, so
+// fewer, longer waves pay less per-wave staging); 0 when none divides
+int gemv1_groups(int n, int k) {
+    const int tiles = n / 16, G = k / 128;
+    int pick = 0;
+    for (int ng : {10, 8, 5, 4, 2}) {
+        if (G % ng || G / ng > kMaxWaves) continue;
+        pick = ng;
+        if ((long)tiles * (G / ng) >= 12L * qe_num_cus()) break;
+    }
+    return pick;
+}
+
+}  // namespace qe_gemv1
+
+// m = 1 on the matrix cores when K / 128 splits evenly into slices of 10, 8, 5, 4 or 2 groups and x is 16-byte
+// aligned; returns false otherwise (the caller takes the VALU GEMV)
+bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) {
+    using namespace qe_gemv1;
+    const int ng = gemv1_groups(w.n, w.k);
+    if (ng == 0 || ((uintptr_t)x & 15) != 0) return false;
+    const int S = w.k / 128 / ng;
+    const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
+#define QE_GEMV1(NG_, SDT_)                                                                                  \
+    gemv1_kernel<NG_, (NG_ < 3 ? NG_ : 3), SDT_><<<grid, block, ((size_t)S * wave_dwords<NG_>() + (size_t)S * 16) * 4, \
+                                                    st>>>(w.q, w.s, w.n, w.k, x, y, out)
+#define QE_GEMV1_NG(SDT_)                        \
+    do {                                         \
+        if (ng == 10) QE_GEMV1(10, SDT_);        \
+        else if (ng == 8) QE_GEMV1(8, SDT_);     \
+        else if (ng == 5) QE_GEMV1(5, SDT_);     \
+        else if (ng == 4) QE_GEMV1(4, SDT_);     \
+        else QE_GEMV1(2, SDT_);                  \
+    } while (0)
+    if (w.sdt == kScaleF16) QE_GEMV1_NG(kScaleF16);
+    else QE_GEMV1_NG(kScaleBF16);
+#undef QE_GEMV1_NG
+#undef QE_GEMV1
+    HIP_CHECK(hipGetLastError());
+    return true;
+}

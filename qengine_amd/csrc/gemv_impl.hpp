@@ -114,12 +114,13 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     const int xoff = x_dword<FMT>(c_st, sl_st);
     auto ldx_group = [&](int tok, int i) { return tok < m ? xw[tok][i * 64 + xoff] : 0u; };
 
-    // 1. loads, per group in the order they are consumed (vmcnt retires in order); the scales first, one dword
-    //    per lane, staged in LDS
-    {
-        const int ndw = FMT == kFmtW8C ? 8 : ng * 8;
-        if (L < ndw) reinterpret_cast<uint32_t*>(sl16)[L] = reinterpret_cast<const uint32_t*>(sp)[L];
-    }
+    // 1. loads, in the order they are consumed (vmcnt retires in order) and with no wait between them: (UP) the
+    //    activation pieces, the slice's scales (one dword per lane), then the weight records group by group. The
+    //    addresses are clamped rather than branched on (xw rows past m point at row 0), so no load has to
+    //    complete before the weight stream starts; out-of-range values are dropped when staged. The LDS writes
+    //    that consume the early loads come after the last weight load (sched_barrier), so waiting for them
+    //    never waits for weights.
+    const int ndw = FMT == kFmtW8C ? 8 : ng * 8;  // scale dwords of the slice
     u32x4_v wv[NGM][LPG];
     uint32_t xr[PF && !UP ? MT : 1][PF && !UP ? NGM : 1];
     // UP: lane L loads dwords [8 L, 8 L + 8) of each row's slice (NG groups x 64 dwords) with two 16-byte loads
@@ -130,12 +131,12 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     if constexpr (UP) {
 #pragma unroll
         for (int tok = 0; tok < MT; tok++) {
-            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xw[tok]) + 2 * L;
-            const bool ok = tok < m && L < XL;
-            xv[tok][0] = ok ? src[0] : u32x4_v{0u, 0u, 0u, 0u};
-            xv[tok][1] = ok ? src[1] : u32x4_v{0u, 0u, 0u, 0u};
+            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xw[tok]) + 2 * (L < XL ? L : XL - 1);
+            xv[tok][0] = src[0];
+            xv[tok][1] = src[1];
         }
     }
+    const uint32_t sraw = reinterpret_cast<const uint32_t*>(sp)[L < ndw ? L : ndw - 1];
 #pragma unroll
     for (int i = 0; i < NGM; i++) {
         if (NG == 0 && i >= ng) break;
@@ -143,9 +144,11 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
         for (int e = 0; e < LPG; e++) wv[i][e] = ld_stream(qp + (size_t)(i * LPG + e) * 64);
         if constexpr (PF && !UP) {
 #pragma unroll
-            for (int tok = 0; tok < MT; tok++) xr[tok][i] = ldx_group(tok, i);
+            for (int tok = 0; tok < MT; tok++) xr[tok][i] = xw[tok][i * 64 + xoff];
         }
     }
+    __builtin_amdgcn_sched_barrier(0);
+    if (L < ndw) reinterpret_cast<uint32_t*>(sl16)[L] = sraw;
 
     // 2. per group: stage x (class-major, class sums times the bias), then the dot products
     constexpr float bias = FMT == kFmtW4 ? 136.f : 128.f;
@@ -159,7 +162,8 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     auto stage = [&](int i) {
 #pragma unroll
         for (int tok = 0; tok < MT; tok++) {
-            const uint32_t v = PF && !UP ? xr[PF && !UP ? tok : 0][PF && !UP ? i : 0] : ldx_group(tok, i);
+            const uint32_t v = PF && !UP ? (tok < m ? xr[PF && !UP ? tok : 0][PF && !UP ? i : 0] : 0u)
+                                         : ldx_group(tok, i);
             const int xi = (UP ? i : 0) * MT + tok;
             xl[xi * 64 + L] = v;
             float sm = dot2_bf16(v, 0x3F803F80u, 0.f);  // x_lo + x_hi (bf16 (1, 1))
@@ -178,7 +182,7 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
             for (int tok = 0; tok < MT; tok++)
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    xl[(gi * MT + tok) * 64 + x_slot<FMT>(8 * l8 + e)] = xv[tok][e >> 2][e & 3];
+                    xl[(gi * MT + tok) * 64 + x_slot<FMT>(8 * l8 + e)] = tok < m ? xv[tok][e >> 2][e & 3] : 0u;
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();

@@ -22,6 +22,7 @@ static void gemv_check(int n, int k, const void* x, int ldx, int ldy, int m, boo
 void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
     gemv_check(w.n, w.k, x, ldx, ldy, m, w.glu);
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    if (m == 1 && gemv1_w4(w, x, y, out, st)) return;
     // the skinny kernel loads activations as 16-byte pieces; unaligned rows take the decode GEMV for every m
     if (m >= skinny_min_m() && ((uintptr_t)x & 15) == 0 && ldx % 8 == 0) {
         skinny_w4_mfma(w, x, ldx, y, ldy, m, out, st);
