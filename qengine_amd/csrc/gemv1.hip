@@ -25,16 +25,34 @@
 namespace qe_gemv1 {
 using namespace qe_gemv;
 
-// LDS per wave (dwords): xl [NG][64] activations class-major, zero [NG][64], xsum [NG][8] (-136 x class sums),
-// scales [NG][16] half; then red [S][16] floats for the block
-template <int NG>
-constexpr int wave_dwords() {
-    return NG * 64 * 2 + NG * 8 + NG * 8;
+// register r of a (r = 2 b2 + b1, b1 / b2: the lane's bit in m1 / m2) with v_cndmask_b32
+__device__ __forceinline__ float pick4(f32x4_v a, uint64_t m1, uint64_t m2) {
+    float lo, hi, r;
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(lo) : "v"(a[0]), "v"(a[1]), "s"(m1));
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(hi) : "v"(a[2]), "v"(a[3]), "s"(m1));
+    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(lo), "v"(hi), "s"(m2));
+    return r;
 }
 
-// NG groups per wave (K slice), D weight records in flight per lane (a sliding window: the load of group i + D is
-// issued once group i has been unpacked). Every wave then receives its weights spread over the whole stream
-// instead of in one burst, so the compute left after the last bytes arrive is one group, not a whole slice.
+// Staging works on 8-dword pieces of the wave's activation slice, 64 pieces (one per lane) per round; the arrays
+// are padded to whole rounds so every lane stages unconditionally (lanes past the slice write duplicates into the
+// padding): a staging branch would let the compiler sink the early activation loads into it, behind the weight
+// loads, and vmcnt retires in order.
+template <int NG>
+constexpr int stage_groups() {
+    return (NG * 8 + 63) / 64 * 8;
+}
+// LDS per wave (dwords): xl [GP][64] activations class-major, zero [GP][8] (the B operand of lanes off the
+// diagonal), xsum [GP][8] (-136 x class sums), scales [GP][8] pairs (s[g], s[g + 8]) of 16-bit values, GP =
+// stage_groups; then red [S][16] floats for the block
+template <int NG>
+constexpr int wave_dwords() {
+    return stage_groups<NG>() * (64 + 8 + 8 + 8);
+}
+
+// NG groups per wave (K slice), D weight records in flight per lane (D < NG: a sliding window, the load of group
+// i + D is issued once group i has been unpacked, so a wave receives its weights spread over the stream instead
+// of in one burst and the compute left after its last bytes arrive is one group, not a whole slice).
 template <int NG, int D, int SDT>
 __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
 gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K,
@@ -42,18 +60,19 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     constexpr int WSZ = wave_dwords<NG>();
     constexpr int NP = NG * 8;              // 8-dword activation pieces (and scale dwords, class sums) of a slice
     constexpr int NR = (NP + 63) / 64;      // pieces per lane
+    constexpr int GP = stage_groups<NG>();  // staged groups including the padding
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
     const int tile = blockIdx.x, G = K >> 7, gb = w * NG;
-    uint32_t* xl = lds + (size_t)w * WSZ;                          // [NG][64]
-    uint32_t* zr = xl + NG * 64;                                     // [NG][64] zeros
-    float* xsum = reinterpret_cast<float*>(zr + NG * 64);            // [NG][8]
-    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xsum + NG * 8);     // [NG][16]
+    uint32_t* xl = lds + (size_t)w * WSZ;                          // [GP][64]
+    uint32_t* zr = xl + GP * 64;                                     // [GP][8] zeros
+    float* xsum = reinterpret_cast<float*>(zr + GP * 8);             // [GP][8]
+    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xsum + GP * 8);     // [GP][8][2]: (s[g], s[g + 8])
     float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][16]
 
     // 1. loads, no wait between them: the activation pieces of the slice (piece p = L + 64 r: dwords 8 p .. 8 p + 7,
-    //    group p / 8), the slice's scales (dword p), then the first D groups of weight records. Addresses are
-    //    clamped rather than branched on, so nothing waits before the weight stream starts.
+    //    group p / 8), the slice's scales (dword p), then the first D groups of weight records.
+    //    Addresses are clamped rather than branched on, so nothing waits before the weight stream starts.
     const uint32_t* xs0 = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64;
     const uint32_t* ss0 = reinterpret_cast<const uint32_t*>(s + ((size_t)tile * G + gb) * 16);
     u32x4_v xv[NR][2];
@@ -71,19 +90,20 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     for (int i = 0; i < D; i++) wv[i] = ld_stream(qp + (size_t)i * 64);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 2. staging: zero block, scales, activations class-major (x_slot), then the class sums times -136
+    // 2. staging (every lane, whole rounds): scales as (s[g], s[g + 8]) pairs, activations class-major (x_slot),
+    //    then the class sums times -136. Scale dword p holds rows 2 (p % 8) and 2 (p % 8) + 1 of group p / 8.
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         const int p = L + 64 * r;
-        if (p < NP) {
-            const int gi = p >> 3, l8 = p & 7;
-            const u32x4_v z4 = {0u, 0u, 0u, 0u};
-            *reinterpret_cast<u32x4_v*>(&zr[8 * p]) = z4;
-            *reinterpret_cast<u32x4_v*>(&zr[8 * p + 4]) = z4;
-            reinterpret_cast<uint32_t*>(sl16)[p] = sraw[r];
+        const int gi = p >> 3, l8 = p & 7;
+        zr[p] = 0u;
 #pragma unroll
-            for (int e = 0; e < 8; e++) xl[gi * 64 + x_slot<kFmtW4>(8 * l8 + e)] = e < 4 ? xv[r][0][e] : xv[r][1][e - 4];
+        for (int e = 0; e < 2; e++) {
+            const int row = 2 * l8 + e;
+            sl16[(gi * 8 + (row & 7)) * 2 + (row >> 3)] = (uint16_t)(sraw[r] >> (16 * e));
         }
+#pragma unroll
+        for (int e = 0; e < 8; e++) xl[gi * 64 + x_slot<kFmtW4>(8 * l8 + e)] = e < 4 ? xv[r][0][e] : xv[r][1][e - 4];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -91,16 +111,14 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         const int p = L + 64 * r;
-        if (p < NP) {
-            const u32x4_v* cl = reinterpret_cast<const u32x4_v*>(&xl[(p >> 3) * 64 + (p & 7) * 8]);
-            const u32x4_v a0 = cl[0], a1 = cl[1];
-            float sm = 0.f;
+        const u32x4_v* cl = reinterpret_cast<const u32x4_v*>(&xl[(p >> 3) * 64 + (p & 7) * 8]);
+        const u32x4_v a0 = cl[0], a1 = cl[1];
+        float sm = 0.f;
 #pragma unroll
-            for (int e = 0; e < 4; e++) sm = dot2_bf16(a0[e], 0x3F803F80u, sm);  // x_lo + x_hi (bf16 (1, 1))
+        for (int e = 0; e < 4; e++) sm = dot2_bf16(a0[e], 0x3F803F80u, sm);  // x_lo + x_hi (bf16 (1, 1))
 #pragma unroll
-            for (int e = 0; e < 4; e++) sm = dot2_bf16(a1[e], 0x3F803F80u, sm);
-            xsum[p] = -136.f * sm;
-        }
+        for (int e = 0; e < 4; e++) sm = dot2_bf16(a1[e], 0x3F803F80u, sm);
+        xsum[p] = -136.f * sm;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -109,19 +127,24 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     // 3. per group: 4 MFMAs (rows g / g + 8 x words 0-1 / 2-3), acc += s * D
     const int qb = L >> 4, c = L & 15;
     const bool diag = (c >> 2) == qb;
-    // B operand base: class 4 (q / 2) + c % 4 of the staged activations on the diagonal, else the zero block
+    // B operand: class 4 (q / 2) + c % 4 of the staged activations on the diagonal, else 8 zeros; group i is
+    // 64 dwords further for the diagonal lanes, 8 for the others (no branch in the loop: a branch per group would
+    // let the compiler sink every group's FMAs to the end and keep all D results live)
     const uint32_t* bb = diag ? &xl[(4 * (qb >> 1) + (c & 3)) * 8] : zr;
+    const int bstep = diag ? 64 : 8;
     const float* cb = &xsum[4 * (c >> 3)];  // class sums of classes 4 (c / 8) .. + 3 (register r <-> t = r)
     const int grow = 4 * ((c >> 2) & 1) + qb;  // row (low nibbles) of the lane's useful D entry
     const uint32_t kMask = 0x000F000Fu, kMagic = 0x43004300u;
     f32x4_v acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NG; i++) {
-        const u32x4_v b01 = *reinterpret_cast<const u32x4_v*>(bb + i * 64);
-        const u32x4_v b23 = *reinterpret_cast<const u32x4_v*>(bb + i * 64 + 4);
+        const u32x4_v b01 = *reinterpret_cast<const u32x4_v*>(bb + i * bstep);
+        const u32x4_v b23 = *reinterpret_cast<const u32x4_v*>(bb + i * bstep + 4);
         const f32x4_v c0 = *reinterpret_cast<const f32x4_v*>(cb + i * 8);
-        const float s_lo = scale_to_f32<SDT>(sl16[i * 16 + grow]);
-        const float s_hi = scale_to_f32<SDT>(sl16[i * 16 + grow + 8]);
+        const bf16x8_v B01 = __builtin_bit_cast(bf16x8_v, b01), B23 = __builtin_bit_cast(bf16x8_v, b23);
+        const uint32_t sp = reinterpret_cast<const uint32_t*>(sl16)[i * 8 + grow];
+        const float s_lo = scale_to_f32<SDT>((uint16_t)(sp & 0xffffu));
+        const float s_hi = scale_to_f32<SDT>((uint16_t)(sp >> 16));
         const u32x4_v r = wv[i % D];
         // the eight values of row g (sh = 0) or g + 8 (sh = 4) in words j, j + 1
         auto opnd = [&](int j, int sh) {
@@ -132,7 +155,6 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
         const bf16x8_v A0 = opnd(0, 0), A1 = opnd(0, 4), A2 = opnd(2, 0), A3 = opnd(2, 4);
         // the window: group i's record is unpacked, its registers take group i + D
         if (i + D < NG) wv[i % D] = ld_stream(qp + (size_t)(i + D) * 64);
-        const bf16x8_v B01 = __builtin_bit_cast(bf16x8_v, b01), B23 = __builtin_bit_cast(bf16x8_v, b23);
         f32x4_v dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B01, c0, 0, 0, 0);
         f32x4_v dh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B01, c0, 0, 0, 0);
         dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A2, B23, dl, 0, 0, 0);
@@ -142,20 +164,18 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
             acc_lo[e] = fmaf(s_lo, dl[e], acc_lo[e]);
             acc_hi[e] = fmaf(s_hi, dh[e], acc_hi[e]);
         }
-        // the accumulators are consumed here (an empty asm), so the FMAs are not sunk to the end of the kernel
-        // (the compiler would keep every group's D live)
-        asm volatile("" : "+v"(acc_lo), "+v"(acc_hi));
     }
 
-    // 4. the lane's entry is register c % 4; add the quad (t) and the two chunks (h, lanes c and c + 8)
-    const int rr = c & 3;
-    float vlo = rr == 0 ? acc_lo[0] : rr == 1 ? acc_lo[1] : rr == 2 ? acc_lo[2] : acc_lo[3];
-    float vhi = rr == 0 ? acc_hi[0] : rr == 1 ? acc_hi[1] : rr == 2 ? acc_hi[2] : acc_hi[3];
+    // 4. the lane's entry is register c % 4 (selected without branches: a branchy select lets the compiler sink
+    //    every group's FMAs into the branches and keep all D results live); add the quad (t) and the two chunks
+    //    (h, lanes c and c + 8)
+    const uint64_t m1 = __builtin_amdgcn_ballot_w64((c & 1) != 0), m2 = __builtin_amdgcn_ballot_w64((c & 2) != 0);
+    constexpr int kDppRowRor8 = 0x128;  // row_ror:8 (lane c <- lane (c + 8) % 16 of the row)
+    float vlo = pick4(acc_lo, m1, m2), vhi = pick4(acc_hi, m1, m2);
     vlo = dpp_add<kDppXor1>(vlo);
     vhi = dpp_add<kDppXor1>(vhi);
     vlo = dpp_add<kDppXor2>(vlo);
     vhi = dpp_add<kDppXor2>(vhi);
-    constexpr int kDppRowRor8 = 0x128;  // row_ror:8 (lane c <- lane (c + 8) % 16 of the row)
     vlo = dpp_add<kDppRowRor8>(vlo);
     vhi = dpp_add<kDppRowRor8>(vhi);
     if ((c & 11) == 0) {  // c = 0: rows q, q + 8; c = 4: rows 4 + q, 12 + q
@@ -183,16 +203,17 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     }
 }
 
-// K slicing of the m = 1 kernel: groups per wave NG in {10, 8, 5, 4, 2} dividing K / 128 with at most 8 waves
-// per block, the largest NG whose grid still gives ~12 waves per CU (the window keeps the loads in flight, so
-// fewer, longer waves pay less per-wave staging); 0 when none divides
+// K slicing of the m = 1 kernel: groups per wave NG in {2, 4, 5, 8, 10} dividing K / 128 with at most 8 waves
+// per block; the smallest NG whose grid stays within ~34 waves per CU (about what can be resident at 8 waves per
+// SIMD): more, shorter waves hide the per-group latencies best, as long as they need not wait for a second round
+// of wave slots. 0 when none divides.
 int gemv1_groups(int n, int k) {
     const int tiles = n / 16, G = k / 128;
     int pick = 0;
     for (int ng : {10, 8, 5, 4, 2}) {
         if (G % ng || G / ng > kMaxWaves) continue;
+        if (pick != 0 && (long)tiles * (G / ng) > 34L * qe_num_cus()) break;
         pick = ng;
-        if ((long)tiles * (G / ng) >= 12L * qe_num_cus()) break;
     }
     return pick;
 }
@@ -207,9 +228,10 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
     if (ng == 0 || ((uintptr_t)x & 15) != 0) return false;
     const int S = w.k / 128 / ng;
     const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
-#define QE_GEMV1(NG_, SDT_)                                                                                  \
-    gemv1_kernel<NG_, (NG_ < 3 ? NG_ : 3), SDT_><<<grid, block, ((size_t)S * wave_dwords<NG_>() + (size_t)S * 16) * 4, \
-                                                    st>>>(w.q, w.s, w.n, w.k, x, y, out)
+    // all of a slice's records in flight for slices of up to 5 groups, else a window of 3
+#define QE_GEMV1(NG_, SDT_)                                                                                   \
+    gemv1_kernel<NG_, (NG_ <= 5 ? NG_ : 3), SDT_><<<grid, block, ((size_t)S * wave_dwords<NG_>() + (size_t)S * 16) * 4, \
+                                                     st>>>(w.q, w.s, w.n, w.k, x, y, out)
 #define QE_GEMV1_NG(SDT_)                        \
     do {                                         \
         if (ng == 10) QE_GEMV1(10, SDT_);        \
