@@ -37,13 +37,14 @@ struct Cfg {
 
 // global_load_lds_dwordx4: lane i's 16 bytes land at LDS byte m0 + 16 i. Issued from inline asm so that the
 // compiler, which cannot tell these LDS writes from the stage the MFMAs read, does not wait for them before every
-// LDS read; the kernel waits for them itself (vmcnt) before the barrier that publishes the stage.
+// LDS read; the kernel waits for them itself (vmcnt) before the barrier that publishes the stage. An LDS DMA that
+// reads m0 needs one wait state after the scalar write of m0 (GFX9): the s_nop.
 // lds_dst: LDS byte address, wave-uniform
 __device__ __forceinline__ void dma16(const void* src, unsigned lds_dst) {
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
 }
 __device__ __forceinline__ void dma4(const void* src, unsigned lds_dst) {  // 4 bytes per lane
-    asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
 }
 
 template <int FMT, int SDT, int WMT, int WNT>
@@ -123,7 +124,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const uint32_t wd = rw[64 * t];
-            const uint32_t u = h ? (wd >> 4) & 0x0F0F0F0Fu : wd & 0x0F0F0F0Fu;  // bytes: k0, k0+8, k0+1, k0+9
+            const uint32_t u = (h ? wd >> 4 : wd) & nib_mask();  // bytes: k0, k0+8, k0+1, k0+9
             lo[t] = pack_bf16x2(fmaf(cvt_ubyte<0>(u), scl, bias), fmaf(cvt_ubyte<2>(u), scl, bias));
             hi[t] = pack_bf16x2(fmaf(cvt_ubyte<1>(u), scl, bias), fmaf(cvt_ubyte<3>(u), scl, bias));
         }

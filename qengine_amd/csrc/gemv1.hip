@@ -25,13 +25,10 @@
 namespace qe_gemv1 {
 using namespace qe_gemv;
 
-// register r of a (r = 2 b2 + b1, b1 / b2: the lane's bit in m1 / m2) with v_cndmask_b32
-__device__ __forceinline__ float pick4(f32x4_v a, uint64_t m1, uint64_t m2) {
-    float lo, hi, r;
-    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(lo) : "v"(a[0]), "v"(a[1]), "s"(m1));
-    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(hi) : "v"(a[2]), "v"(a[3]), "s"(m1));
-    asm("v_cndmask_b32 %0, %1, %2, %3" : "=v"(r) : "v"(lo), "v"(hi), "s"(m2));
-    return r;
+// register r of a (r = 2 b2 + b1): selects (v_cndmask_b32), no branch
+__device__ __forceinline__ float pick4(f32x4_v a, bool b1, bool b2) {
+    const float lo = b1 ? a[1] : a[0], hi = b1 ? a[3] : a[2];
+    return b2 ? hi : lo;
 }
 
 // Staging works on 8-dword pieces of the wave's activation slice, 64 pieces (one per lane) per round; the arrays
@@ -134,7 +131,6 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     const int bstep = diag ? 64 : 8;
     const float* cb = &xsum[4 * (c >> 3)];  // class sums of classes 4 (c / 8) .. + 3 (register r <-> t = r)
     const int grow = 4 * ((c >> 2) & 1) + qb;  // row (low nibbles) of the lane's useful D entry
-    const uint32_t kMask = 0x000F000Fu, kMagic = 0x43004300u;
     f32x4_v acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NG; i++) {
@@ -146,13 +142,18 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
         const float s_lo = scale_to_f32<SDT>((uint16_t)(sp & 0xffffu));
         const float s_hi = scale_to_f32<SDT>((uint16_t)(sp >> 16));
         const u32x4_v r = wv[i % D];
-        // the eight values of row g (sh = 0) or g + 8 (sh = 4) in words j, j + 1
-        auto opnd = [&](int j, int sh) {
-            const u32x4_v a = {and_or(r[j] >> sh, kMask, kMagic), and_or(r[j] >> (sh + 8), kMask, kMagic),
-                               and_or(r[j + 1] >> sh, kMask, kMagic), and_or(r[j + 1] >> (sh + 8), kMask, kMagic)};
+        // the eight values of row g (t0: low nibbles) or g + 8 (t1: high nibbles) in words j, j + 1
+        u32x4_v t0, t1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            t0[j] = r[j] & kNib;
+            t1[j] = (r[j] >> 4) & kNib;
+        }
+        auto opnd = [&](const u32x4_v& t, int j) {
+            const u32x4_v a = {bf16x2_b02(t[j]), bf16x2_b13(t[j]), bf16x2_b02(t[j + 1]), bf16x2_b13(t[j + 1])};
             return __builtin_bit_cast(bf16x8_v, a);
         };
-        const bf16x8_v A0 = opnd(0, 0), A1 = opnd(0, 4), A2 = opnd(2, 0), A3 = opnd(2, 4);
+        const bf16x8_v A0 = opnd(t0, 0), A1 = opnd(t1, 0), A2 = opnd(t0, 2), A3 = opnd(t1, 2);
         // the window: group i's record is unpacked, its registers take group i + D
         if (i + D < NG) wv[i % D] = ld_stream(qp + (size_t)(i + D) * 64);
         f32x4_v dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B01, c0, 0, 0, 0);
@@ -169,9 +170,8 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     // 4. the lane's entry is register c % 4 (selected without branches: a branchy select lets the compiler sink
     //    every group's FMAs into the branches and keep all D results live); add the quad (t) and the two chunks
     //    (h, lanes c and c + 8)
-    const uint64_t m1 = __builtin_amdgcn_ballot_w64((c & 1) != 0), m2 = __builtin_amdgcn_ballot_w64((c & 2) != 0);
     constexpr int kDppRowRor8 = 0x128;  // row_ror:8 (lane c <- lane (c + 8) % 16 of the row)
-    float vlo = pick4(acc_lo, m1, m2), vhi = pick4(acc_hi, m1, m2);
+    float vlo = pick4(acc_lo, (c & 1) != 0, (c & 2) != 0), vhi = pick4(acc_hi, (c & 1) != 0, (c & 2) != 0);
     vlo = dpp_add<kDppXor1>(vlo);
     vhi = dpp_add<kDppXor1>(vhi);
     vlo = dpp_add<kDppXor2>(vlo);

@@ -8,7 +8,7 @@
 //   * activation staging: lane L of a wave loads dword `slot` (L % 8) of lane class c = L / 8 of each group
 //     and stores it at LDS position L, so a class's 8 dwords are contiguous (two ds_read_b128 per lane and
 //     group, broadcast across the 8 lanes of a row pair) and the class sum is a 3-step DPP reduction.
-//   * nibbles become bf16 by OR-ing them into the mantissa of 128.0 (0x4300 -> 128 + u exactly, v_and_or_b32),
+//   * nibbles become bf16 by placing them in the mantissa of 128.0 (0x4300 -> 128 + u exactly, v_perm_b32),
 //     v_dot2_f32_bf16 accumulates (128 + u) * x in fp32; per group the bias is removed with the staged class
 //     sum and the group scale applied: acc += s * (a - 136 X). INT8 bytes (XOR 0x80 -> u = w + 128) go through
 //     v_cvt_f32_ubyte + v_cvt_pk_bf16 (exact), bias 128.
@@ -36,12 +36,13 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
 __device__ __forceinline__ u32x4_v ld_stream(const uint4* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p));
 }
-// (a & m) | c in one VALU op (the compiler splits it into two when m and c are literals)
-__device__ __forceinline__ uint32_t and_or(uint32_t a, uint32_t m, uint32_t c) {
-    uint32_t r;
-    asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "s"(m), "v"(c));
-    return r;
-}
+// Nibbles to bf16: t holds one nibble in the low half of each byte (t & 0xF0F0F0F0 == 0); v_perm_b32 with 0x43 as
+// the high byte of each half gives the bf16 pairs 128 + u exactly: bytes (0, 2) and bytes (1, 3) of t. No inline
+// asm for VALU work anywhere in these kernels: the compiler's MFMA hazard checks (VALU writes to registers an
+// in-flight MFMA still reads) do not look into asm operands.
+__device__ __forceinline__ uint32_t bf16x2_b02(uint32_t t) { return __builtin_amdgcn_perm(0x43434343u, t, 0x04020400u); }
+__device__ __forceinline__ uint32_t bf16x2_b13(uint32_t t) { return __builtin_amdgcn_perm(0x43434343u, t, 0x04030401u); }
+constexpr uint32_t kNib = 0x0F0F0F0Fu;
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
@@ -153,8 +154,6 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     // 2. per group: stage x (class-major, class sums times the bias), then the dot products
     constexpr float bias = FMT == kFmtW4 ? 136.f : 128.f;
     const int cls = 4 * h + t;
-    const uint32_t kMask = 0x000F000Fu;
-    const uint32_t kMagic = 0x43004300u;  // bf16 (128, 128)
     float acc_lo[MT], acc_hi[MT];
 #pragma unroll
     for (int tok = 0; tok < MT; tok++) acc_lo[tok] = acc_hi[tok] = 0.f;
@@ -229,10 +228,11 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint32_t wd = wv[i][0][j];
-                p[j][0] = and_or(wd, kMask, kMagic);        // row g,     k0, k0 + 1
-                p[j][1] = and_or(wd >> 4, kMask, kMagic);   // row g + 8, k0, k0 + 1
-                p[j][2] = and_or(wd >> 8, kMask, kMagic);   // row g,     k0 + 8, k0 + 9
-                p[j][3] = and_or(wd >> 12, kMask, kMagic);  // row g + 8, k0 + 8, k0 + 9
+                const uint32_t t0 = wd & kNib, t1 = (wd >> 4) & kNib;  // row g / row g + 8: k0, k0 + 8, k0 + 1, k0 + 9
+                p[j][0] = bf16x2_b02(t0);  // row g,     k0, k0 + 1
+                p[j][1] = bf16x2_b02(t1);  // row g + 8, k0, k0 + 1
+                p[j][2] = bf16x2_b13(t0);  // row g,     k0 + 8, k0 + 9
+                p[j][3] = bf16x2_b13(t1);  // row g + 8, k0 + 8, k0 + 9
             }
 #pragma unroll
             for (int tok = 0; tok < MT; tok++) {

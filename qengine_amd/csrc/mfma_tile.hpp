@@ -16,15 +16,18 @@ typedef unsigned u32x4_v __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int swz_f(int r) { return (r & 7) ^ ((r >> 3) & 3); }
 __device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ swz_f(r)) << 4); }
 
-// v_cvt_f32_ubyte{B}: byte B of v as float (the compiler would extract a 4-bit field and convert byte 0 instead)
+// byte B of v as float: one v_cvt_f32_ubyte{B}, as long as the compiler cannot see that the high nibbles of v are
+// zero (then it extracts a 4-bit field and converts byte 0 instead): nibble masks come from nib_mask()
 template <int B>
 __device__ __forceinline__ float cvt_ubyte(uint32_t v) {
-    float r;
-    if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
-    else if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
-    else if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
-    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
-    return r;
+    return static_cast<float>((v >> (8 * B)) & 0xFFu);
+}
+// 0x0F0F0F0F in an SGPR, opaque to the compiler's known-bits analysis (a scalar move: no VALU work goes through
+// inline asm in these kernels, since the compiler's MFMA hazard checks do not look into asm operands)
+__device__ __forceinline__ uint32_t nib_mask() {
+    uint32_t m;
+    asm("s_mov_b32 %0, 0x0f0f0f0f" : "=s"(m));
+    return m;
 }
 
 template <int SDT>
@@ -36,8 +39,9 @@ __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
 // dequantize the 8 nibbles of one W4 word (rows g / g + 8, k0 + {0, 1, 8, 9}) to bf16_rn((u - 8) * s) and store them
 // as 4 bf16 pairs at (row, k0) (row, k0 + 8) (row + 8, k0) (row + 8, k0 + 8) of the tile
 __device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k0) {
-    const uint32_t ev = wd & 0x0F0F0F0Fu;         // bytes: slots 0, 2, 4, 6 (row g: k0, k0+8, k0+1, k0+9)
-    const uint32_t od = (wd >> 4) & 0x0F0F0F0Fu;  // slots 1, 3, 5, 7 (row g + 8)
+    const uint32_t nm = nib_mask();
+    const uint32_t ev = wd & nm;         // bytes: slots 0, 2, 4, 6 (row g: k0, k0+8, k0+1, k0+9)
+    const uint32_t od = (wd >> 4) & nm;  // slots 1, 3, 5, 7 (row g + 8)
     const float b_lo = -8.f * s_lo, b_hi = -8.f * s_hi;
     // (u - 8) * s = fma(u, s, -8 s): exact in fp32, then one rounding to bf16
     const uint32_t g0 = pack_bf16x2(fmaf(cvt_ubyte<0>(ev), s_lo, b_lo), fmaf(cvt_ubyte<2>(ev), s_lo, b_lo));

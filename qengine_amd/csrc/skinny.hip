@@ -9,8 +9,9 @@
 //     Lane 16 q + i of the wave loads the records (c, g = i % 8, t = q) of the group's two 64-k chunks and keeps the
 //     rows of half i / 8: k slots of lane group q are then the k of record t = q, the same for every row, which
 //     is what the B operand needs. Lanes i and i + 8 load the same two records (one 16-byte load each, merged by
-//     the cache), so each lane unpacks 32 weights of its own row: (w >> 4 h) & 0x000F000F | 0x43004300 is the
-//     bf16 pair (128 + u) of two consecutive k.
+//     the cache), so each lane unpacks 32 weights of its own row: t = (w >> 4 h) & 0x0F0F0F0F holds its nibbles
+//     for k0, k0 + 8, k0 + 1, k0 + 9, and a byte permute with 0x43 gives the bf16 pairs (128 + u) of (k0, k0 + 1)
+//     and (k0 + 8, k0 + 9).
 //   * Activations are staged per group in the wave's LDS in class-major order (class c = 4 h + t holds the 8
 //     dwords of k = 64 h + 16 j + 2 t (+8)), which is exactly the B operand: one ds_read_b128 per MFMA.
 //   * The bias 136 (u = w + 8 over the 128 of the magic) is removed by one more MFMA per k step with A = -136:
@@ -121,7 +122,6 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    const uint32_t kMask = 0x000F000Fu, kMagic = 0x43004300u;  // bf16 (128, 128)
     const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
     f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -154,8 +154,8 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
             if (MT == 16 || i < MT)
                 b = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + (i < MT ? i : 0)) * 64 + (4 * (mm >> 1) + qg) * 8 + 2 * j0]);
             const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
-            const u32x4_v a = {and_or(w0 >> sh, kMask, kMagic), and_or(w0 >> (sh + 8), kMask, kMagic),
-                               and_or(w1 >> sh, kMask, kMagic), and_or(w1 >> (sh + 8), kMask, kMagic)};
+            const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
+            const u32x4_v a = {bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
             const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c, 0, 0, 0);
             c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c, 0, 0, 0);

@@ -94,7 +94,8 @@ def setup_w4(n, k, sdt, seed, glu=False):
     return w, q, s
 
 
-@pytest.mark.parametrize("n,k", [(64, 256), (256, 1280), (1024, 5120)])
+# (8192, 1280), (16384, 5120): two to four 16-row tiles per CU, as in the BASELINE shapes
+@pytest.mark.parametrize("n,k", [(64, 256), (256, 1280), (1024, 5120), (8192, 1280), (16384, 5120)])
 @pytest.mark.parametrize("sdt", [0, 1])
 def test_gemv_w4_parity(dev, n, k, sdt):
     w, q, s = setup_w4(n, k, sdt, seed=n + k + sdt)
@@ -112,7 +113,7 @@ def test_gemv_w4_parity(dev, n, k, sdt):
                 assert ex <= 1e-4, (m, ex)
 
 
-@pytest.mark.parametrize("n,k", [(256, 1280), (5120, 5120)])
+@pytest.mark.parametrize("n,k", [(256, 1280), (5120, 5120), (16384, 2048)])
 def test_gemv_w4_batch_equals_alone(dev, n, k):
     w, _, _ = setup_w4(n, k, 1, seed=7)
     x = synth.to_dev(synth.x_host(16, k, seed=8))
@@ -136,7 +137,7 @@ def test_gemv_w4_batch_equals_alone(dev, n, k):
     assert np.array_equal(again.cpu().numpy().view(np.uint32), fb)
 
 
-@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048)])
+@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048), (8192, 1280)])
 def test_gemv_w4_glu(dev, n, k):
     w, q, s = setup_w4(n, k, 1, seed=31, glu=True)
     xh = synth.x_host(16, k, seed=32)
