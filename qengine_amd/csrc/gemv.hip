@@ -42,4 +42,19 @@ Slicing gemv_slicing(int n, int k) {
     return {0, S};
 }
 
+// K slicing of the matrix-core decode kernels (m = 1 and the skinny GEMM): groups per wave NG in {2, 4, 5, 8, 10}
+// dividing K / 128 with at most 8 waves per block; the smallest NG whose grid stays within ~34 waves per CU (about
+// what can be resident at 8 waves per SIMD): more, shorter waves hide the per-group latencies best, as long as they
+// need not wait for a second round of wave slots. 0 when none divides. Depends on (n, k) only.
+int decode_groups(int n, int k) {
+    const int tiles = n / 16, G = k / 128;
+    int pick = 0;
+    for (int ng : {10, 8, 5, 4, 2}) {
+        if (G % ng || G / ng > kMaxWaves) continue;
+        if (pick != 0 && (long)tiles * (G / ng) > 34L * qe_num_cus()) break;
+        pick = ng;
+    }
+    return pick;
+}
+
 }  // namespace qe_gemv

@@ -203,28 +203,13 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     }
 }
 
-// K slicing of the m = 1 kernel: groups per wave NG in {2, 4, 5, 8, 10} dividing K / 128 with at most 8 waves
-// per block; the smallest NG whose grid stays within ~34 waves per CU (about what can be resident at 8 waves per
-// SIMD): more, shorter waves hide the per-group latencies best, as long as they need not wait for a second round
-// of wave slots. 0 when none divides.
-int gemv1_groups(int n, int k) {
-    const int tiles = n / 16, G = k / 128;
-    int pick = 0;
-    for (int ng : {10, 8, 5, 4, 2}) {
-        if (G % ng || G / ng > kMaxWaves) continue;
-        if (pick != 0 && (long)tiles * (G / ng) > 34L * qe_num_cus()) break;
-        pick = ng;
-    }
-    return pick;
-}
-
 }  // namespace qe_gemv1
 
 // m = 1 on the matrix cores when K / 128 splits evenly into slices of 10, 8, 5, 4 or 2 groups and x is 16-byte
 // aligned; returns false otherwise (the caller takes the VALU GEMV)
 bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) {
     using namespace qe_gemv1;
-    const int ng = gemv1_groups(w.n, w.k);
+    const int ng = decode_groups(w.n, w.k);
     if (ng == 0 || ((uintptr_t)x & 15) != 0) return false;
     const int S = w.k / 128 / ng;
     const dim3 grid((unsigned)(w.n / 16)), block(64 * S);

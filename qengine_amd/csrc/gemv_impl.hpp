@@ -381,6 +381,8 @@ struct Slicing {
     int ng, S;
 };
 Slicing gemv_slicing(int n, int k);
+// slice size (groups per wave) of the matrix-core decode kernels, 0 when no even slicing fits (gemv.hip)
+int decode_groups(int n, int k);
 
 template <int FMT, int SDT>
 void launch_gemv(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,

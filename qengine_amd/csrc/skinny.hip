@@ -13,22 +13,28 @@
 //     for k0, k0 + 8, k0 + 1, k0 + 9, and a byte permute with 0x43 gives the bf16 pairs (128 + u) of (k0, k0 + 1)
 //     and (k0 + 8, k0 + 9).
 //   * Activations are staged per group in the wave's LDS in class-major order (class c = 4 h + t holds the 8
-//     dwords of k = 64 h + 16 j + 2 t (+8)), which is exactly the B operand: one ds_read_b128 per MFMA.
+//     dwords of k = 64 h + 16 j + 2 t (+8)), which is exactly the B operand: one ds_read_b128 per MFMA. They are
+//     loaded as 16-byte pieces (every wave-level load instruction costs the address unit about the same, so 4-byte
+//     loads per row made the activations, not the weights, the bound at MT >= 8).
 //   * The bias 136 (u = w + 8 over the 128 of the magic) is removed by one more MFMA per k step with A = -136:
 //     C = sum (128 + u) x - 136 sum x = sum (u - 8) x, all products exact in fp32. The group scale is applied
 //     once per group: acc += s * C.
-//   * K slices per block and the fixed-order LDS reduction are those of the GEMV (gemv_slicing): deterministic,
-//     and an activation row's result does not depend on the other rows (MFMA columns are independent).
+//   * K slices per block are those of the m = 1 matrix-core kernel (decode_groups; gemv_slicing's uneven slices
+//     where no even slicing fits) and the fixed-order LDS reduction makes the result deterministic; an activation
+//     row's result does not depend on the other rows (MFMA columns are independent, the slicing depends on (n, k)
+//     only).
 #include "gemv_impl.hpp"
 
 namespace qe_skinny {
 using namespace qe_gemv;
 
-// weight groups in flight per wave (4 keeps MT <= 4 at 6 waves per SIMD; the MT rows of activations of each group
-// in the window take registers too for larger MT)
+// weight groups in flight per wave (with the activations of each group in the window for MT >= 8). Measured on the
+// BASELINE shapes with 5-group slices: 3 for every MT but 8, where 2 keeps the kernel at 6 waves per SIMD (deeper
+// windows cost more in occupancy than they gain in latency)
 template <int MT, int NG>
 constexpr int skinny_d() {
-    return MT <= 4 ? 4 : 3;
+    constexpr int d = MT == 8 ? 2 : 3;
+    return NG > 0 && NG < d ? NG : d;
 }
 
 // UPX (MT <= 4 with even slices): every group's activations are loaded before the weights and staged in LDS
@@ -65,10 +71,33 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
     const int qg = L >> 4, i = L & 15;  // operand lane group, row / column within the tile
     const int g = i & 7, sh = 4 * (i >> 3);
 
-    // activation staging: lane L holds dword (class L / 8, slot L % 8) of each row's group
-    const uint32_t* xb = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64 + x_dword<kFmtW4>(L >> 3, L & 7);
-    const size_t xs = (size_t)(ldx >> 1);
-    auto ldxg = [&](int tok, int ii) { return tok < m ? xb[tok * xs + ii * 64] : 0u; };
+    // Activation rows tok >= m (up to MT) load row m - 1 instead: no load sits under a branch, and those MFMA
+    // columns are never stored (columns are independent).
+    const size_t xs = (size_t)(ldx >> 1);  // dwords per activation row
+    // !UPX: a group's activations are MT rows x 16 pieces of 16 bytes; lane L loads pieces L + 64 e, i.e. piece
+    // L % 16 of row L / 16 + 4 e, and stages its 4 dwords at their class-major positions (MT < 4: lanes of rows
+    // past MT load a duplicate and stage nothing)
+    constexpr int XP = MT >= 4 ? MT / 4 : 1;
+    const u32x4_v* xq[XP];
+#pragma unroll
+    for (int e = 0; e < XP; e++) {
+        const int tp = (L >> 4) + 4 * e;
+        xq[e] = reinterpret_cast<const u32x4_v*>(reinterpret_cast<const uint32_t*>(x) + (size_t)(tp < m ? tp : m - 1) * xs +
+                                                 (size_t)gb * 64) + (L & 15);
+    }
+    auto ldxg = [&](u32x4_v* dst, int ii) {
+#pragma unroll
+        for (int e = 0; e < XP; e++) dst[e] = xq[e][ii * 16];
+    };
+    auto stxg = [&](const u32x4_v* src, int buf) {
+#pragma unroll
+        for (int e = 0; e < XP; e++)
+            if (MT >= 4 || (L >> 4) < MT) {
+#pragma unroll
+                for (int c = 0; c < 4; c++)
+                    xl[(buf * MT + (L >> 4) + 4 * e) * 64 + x_slot<kFmtW4>(4 * (L & 15) + c)] = src[e][c];
+            }
+    };
 
     // 1. loads in consumption order: the slice's scales (one dword per lane); UPX: every group's activations, then
     //    the first D groups of weight records; else (x_j, w_j) pairs for the first D groups
@@ -76,7 +105,7 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
         const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)tile * G + gb) * 16);
         if (L < ng * 8) reinterpret_cast<uint32_t*>(sl16)[L] = sp[L];
     }
-    uint32_t xr[UPX ? 1 : D][MT];  // activation register slots (per-group staging)
+    u32x4_v xr[UPX ? 1 : D][XP];  // activation register slots (per-group staging)
     const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + 4 * g + qg;
     u32x4_v wv[D][2];
     auto ldw = [&](int slot, int ii) {
@@ -89,12 +118,12 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
         constexpr int XL = NGM * 8;
         u32x4_v xv[MT][2];
         const uint32_t* xs0 = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64;
+        const int lc = L < XL ? L : XL - 1;  // lanes past the slice reload its last piece (not staged)
 #pragma unroll
         for (int tok = 0; tok < MT; tok++) {
-            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xs0 + tok * xs) + 2 * L;
-            const bool ok = tok < m && L < XL;
-            xv[tok][0] = ok ? src[0] : u32x4_v{0u, 0u, 0u, 0u};
-            xv[tok][1] = ok ? src[1] : u32x4_v{0u, 0u, 0u, 0u};
+            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xs0 + (tok < m ? tok : m - 1) * xs) + 2 * lc;
+            xv[tok][0] = src[0];
+            xv[tok][1] = src[1];
         }
 #pragma unroll
         for (int ii = 0; ii < D; ii++)
@@ -110,13 +139,11 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
 #pragma unroll
         for (int ii = 0; ii < D; ii++) {
             if (ii < ng) {
-#pragma unroll
-                for (int tok = 0; tok < MT; tok++) xr[ii][tok] = ldxg(tok, ii);
+                ldxg(xr[ii], ii);
                 ldw(ii, ii);
             }
         }
-#pragma unroll
-        for (int tok = 0; tok < MT; tok++) xl[tok * 64 + L] = xr[0][tok];  // group 0 -> buffer 0
+        stxg(xr[0], 0);  // group 0 -> buffer 0
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -131,18 +158,12 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
         if constexpr (!UPX) {
             // stage the next group's activations into the other buffer (read two groups ago, LDS operations of
             // a wave complete in order)
-            if (ii + 1 < ng) {
-#pragma unroll
-                for (int tok = 0; tok < MT; tok++) xl[(((ii + 1) & 1) * MT + tok) * 64 + L] = xr[(ii + 1) % D][tok];
-            }
+            if (ii + 1 < ng) stxg(xr[(ii + 1) % D], (ii + 1) & 1);
         }
         const u32x4_v r0 = wv[ii % D][0], r1 = wv[ii % D][1];
         // refill the window: group ii + D goes where group ii was
         if (ii + D < ng) {
-            if constexpr (!UPX) {
-#pragma unroll
-                for (int tok = 0; tok < MT; tok++) xr[ii % D][tok] = ldxg(tok, ii + D);
-            }
+            if constexpr (!UPX) ldxg(xr[ii % D], ii + D);
             ldw(ii % D, ii + D);
         }
         f32x4_v c = {0.f, 0.f, 0.f, 0.f};
@@ -201,7 +222,9 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
 template <int SDT>
 void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
             int out, int sdt, hipStream_t st) {
-    const Slicing sc = gemv_slicing(n, k);
+    // even slices of the matrix-core decode kernels where they divide K, else the generic uneven slices
+    const int dg = decode_groups(n, k);
+    const Slicing sc = dg > 0 ? Slicing{dg, (k >> 7) / dg} : gemv_slicing(n, k);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
     const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);
 #define QE_SK_K(MT_, NG_)                                                                                         \
@@ -209,10 +232,13 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
         q, s, n, k, x, ldx, y, ldy, m, out, sdt)
 #define QE_SK_NG(MT_)                             \
     do {                                          \
-        if (sc.ng == 8) QE_SK_K(MT_, 8);          \
+        if (sc.ng == 10) QE_SK_K(MT_, 10);        \
+        else if (sc.ng == 8) QE_SK_K(MT_, 8);     \
+        else if (sc.ng == 5) QE_SK_K(MT_, 5);     \
         else if (sc.ng == 4) QE_SK_K(MT_, 4);     \
         else if (sc.ng == 2) QE_SK_K(MT_, 2);     \
-        else QE_SK_K(MT_, 0);                     \
+        else if (sc.ng == 0) QE_SK_K(MT_, 0);     \
+        else CHECK(false, "skinny: slice of %d groups", sc.ng); \
     } while (0)
     if (mt == 1) QE_SK_NG(1);
     else if (mt == 2) QE_SK_NG(2);
