@@ -47,35 +47,77 @@ __device__ __forceinline__ void dma4(const void* src, unsigned lds_dst) {  // 4 
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
 }
 
-template <int FMT, int SDT, int WMT, int WNT>
+// MODE 0: the dense GEMM. MODE 1 / 2: the MoE grouped gate_up / down GEMMs (MoePfArgs), INT4 only: block
+// (job, n tile) with the job's rows gathered (gate_up: x rows of the slots' tokens, down: act rows of the slots),
+// the W tile from the job's expert records (gate_up: the 256 GLU rows of record n tile, K = H; down: H rows, K = I,
+// 128 k per record), and the epilogue into the slot rows.
+template <int FMT, int SDT, int WMT, int WNT, int MODE = 0>
 __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                    int N, int K, const uint16_t* __restrict__ x, int ldx, int T,
-                                                   void* __restrict__ c, int ldc, int out, int sdt, int nbn, int nbt) {
+                                                   void* __restrict__ c, int ldc, int out, int sdt, int nbn, int nbt,
+                                                   MoePfArgs ma) {
     using C = Cfg<WMT, WNT>;
     constexpr int BM = C::BM, BN = C::BN;
     constexpr bool W4 = FMT == kFmtW4;
+    static_assert(MODE == 0 || (W4 && BN == 256), "MoE modes: INT4, 256-row tiles (one gate_up record)");
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const unsigned lds32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds);  // LDS byte address of lds[]
     // XCD-aware tile order: block b runs on XCD b % 8; XCD j takes tiles [j * per, (j + 1) * per) of the
     // n-major tile sequence (consecutive tiles share the X tile, a band of them shares W tiles)
-    const int ntiles = nbn * nbt, per = (ntiles + 7) >> 3;
-    const int b = blockIdx.x, tile = (b & 7) * per + (b >> 3);
-    if (tile >= ntiles) return;
-    const int n0 = (tile % nbn) * BN, t0 = (tile / nbn) * BM;
+    int n0, t0;
+    int e = 0, slot0 = 0, nt = 0;
+    if constexpr (MODE == 0) {
+        const int ntiles = nbn * nbt, per = (ntiles + 7) >> 3;
+        const int b = blockIdx.x, tile = (b & 7) * per + (b >> 3);
+        if (tile >= ntiles) return;
+        n0 = (tile % nbn) * BN;
+        t0 = (tile / nbn) * BM;
+    } else {
+        // block b runs on XCD b % 8: the n tiles of a job run there one after another (they share its gathered
+        // rows in that L2) and the jobs, job % 8 = XCD, spread over all XCDs whatever the job count
+        const int b = blockIdx.x, r = b >> 3;
+        nt = r % nbn;
+        const int job = (r / nbn) * 8 + (b & 7);
+        if (job >= *ma.njobs) return;
+        e = ma.jobs[2 * job];
+        slot0 = ma.off[e] + ma.jobs[2 * job + 1];
+        T = min(BM, ma.off[e + 1] - slot0);  // rows of the job
+        n0 = MODE == 1 ? 0 : nt * BN;
+        t0 = 0;
+        if constexpr (MODE == 1) {  // the record's GLU rows: a 256 x H W4 matrix
+            const char* rp = ma.recs + ((size_t)e * ma.ngrp + nt) * ma.rec;
+            q = reinterpret_cast<const uint4*>(rp);
+            s = reinterpret_cast<const uint16_t*>(rp + ma.gg_q);
+        }
+    }
     const int G = K >> 7, KT = K / BK;
 
     // ---- X, INT4 path: LDS DMA (global_load_lds_dwordx4), 1 KB = 8 rows per wave instruction. Lane i lands at
     //      LDS slot i of the 8-row block, so it loads the chunk that the swizzle puts there. Rows past T re-read
     //      row T - 1 (their outputs are not stored).
+    // (MoE: the gathered row of each of this lane's DMA rows, fixed for the block)
+    const uint16_t* xrow[MODE == 0 ? 1 : C::XDMA];
+    if constexpr (MODE != 0) {
+#pragma unroll
+        for (int i = 0; i < C::XDMA; i++) {
+            const int row = (wave * C::XDMA + i) * 8 + (lane >> 3);
+            const int sl = slot0 + (row < T ? row : T - 1);
+            xrow[i] = ma.a + (MODE == 1 ? (size_t)ma.slot_tok[sl] * ma.H : (size_t)sl * ma.I);
+        }
+    }
     auto dma_x = [&](int kt, unsigned xt) {  // xt: LDS offset of the X tile from lds[]
 #pragma unroll
         for (int i = 0; i < C::XDMA; i++) {
             const int r0 = (wave * C::XDMA + i) * 8, row = r0 + (lane >> 3);
             const int ch = (lane & 7) ^ swz_f(row);
-            const int tok = t0 + row < T ? t0 + row : T - 1;
-            dma16(x + (size_t)tok * ldx + kt * BK + ch * 8, lds32 + xt + r0 * 128);
+            if constexpr (MODE == 0) {
+                const int tok = t0 + row < T ? t0 + row : T - 1;
+                dma16(x + (size_t)tok * ldx + kt * BK + ch * 8, lds32 + xt + r0 * 128);
+            } else {
+                dma16(xrow[i] + kt * BK + ch * 8, lds32 + xt + r0 * 128);
+            }
         }
     };
     // ---- X, INT8 path: XLD x 16 B per thread through registers (row = idx / 8, chunk = idx % 8)
@@ -102,16 +144,34 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     const bool jactive = tid < NJOB;
     const int jj = tid & 3, jg = (tid >> 2) & 7, jtr = tid >> 5;
     const int ntile_last = (N >> 4) - 1;
+    // record (tile tl, 64-k step kt) and scales (tile tl, group grp); MoE down: 128 k per record, in the record's
+    // [H / 16][2][32][4] down layout with [H / 16][16] scales
+    auto w_rec = [&](int tl, int kt) -> const uint4* {
+        if constexpr (MODE == 2) {
+            const char* rp = ma.recs + ((size_t)e * ma.ngrp + (kt >> 1)) * ma.rec + ma.gg_q + ma.gg_s;
+            return reinterpret_cast<const uint4*>(rp) + ((size_t)tl * 2 + (kt & 1)) * 32;
+        } else {
+            return q + ((size_t)tl * (K >> 6) + kt) * 32;
+        }
+    };
+    auto w_sc = [&](int tl, int grp) -> const uint16_t* {
+        if constexpr (MODE == 2) {
+            const char* rp = ma.recs + ((size_t)e * ma.ngrp + grp) * ma.rec + ma.gg_q + ma.gg_s + ma.gd_q;
+            return reinterpret_cast<const uint16_t*>(rp) + (size_t)tl * 16;
+        } else {
+            return s + ((size_t)tl * G + grp) * 16;
+        }
+    };
     auto dma_w4 = [&](int kt, unsigned raw) {  // raw: LDS offset of the raw record buffer
         if (wave < BN / 32) {
             const int tl = min((n0 >> 4) + 2 * wave + ((lane >> 3) & 1), ntile_last);
-            dma16(q + ((size_t)tl * (K >> 6) + kt) * 32 + 4 * (lane & 7) + (lane >> 4), lds32 + raw + wave * 1024);
+            dma16(w_rec(tl, kt) + 4 * (lane & 7) + (lane >> 4), lds32 + raw + wave * 1024);
         }
     };
     auto dma_sc = [&](int grp, unsigned sc) {  // [BN / 16 tiles][16] scales of group grp; lane i: dword i % 8 of tile i / 8
         if (wave < BN / 128) {
             const int tl = min((n0 >> 4) + 8 * wave + (lane >> 3), ntile_last);
-            dma4(s + ((size_t)tl * G + grp) * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
+            dma4(w_sc(tl, grp) + 2 * (lane & 7), lds32 + sc + wave * 256);
         }
     };
     // dequantize half h (0: row g, 1: row g + 8) of this thread's job from the raw records into the W tile
@@ -295,6 +355,19 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             for (int r = 0; r < 16; r++) {
                 const int tok = t0 + wm * 32 * WMT + a * 32 + 8 * (r >> 2) + ci + (r & 3);
                 const float v = acc[a][bb][r];
+                if constexpr (MODE == 1) {
+                    // GLU (gate row g, up row g + 8 of the 16-row tile) times the slot's routing weight; the record's
+                    // 256 rows are act columns 128 nt .. + 128
+                    const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
+                        0, __builtin_bit_cast(int, v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
+                    if ((cj & 15) < 8 && tok < T)
+                        ma.out[(size_t)(slot0 + tok) * ma.I + nt * 128 + (n >> 4) * 8 + (cj & 7)] =
+                            f32_to_bf16(silu_f32(v) * up * ma.slot_w[slot0 + tok]);
+                    continue;
+                } else if constexpr (MODE == 2) {
+                    if (tok < T && n < N) ma.out[(size_t)(slot0 + tok) * ma.H + n] = f32_to_bf16(v);
+                    continue;
+                }
                 if (out == kOutGLU) {
                     // gate = row g, up = row g + 8 of the 16-row tile: lanes j and j + 8
                     const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
@@ -317,7 +390,7 @@ void launch_cfg(const uint4* q, const uint16_t* s, int n, int k, const uint16_t*
     const int nbn = (n + C::BN - 1) / C::BN, nbt = (t + C::BM - 1) / C::BM;
     const int ntiles = nbn * nbt, per = (ntiles + 7) / 8;
     gemm_kernel<FMT, SDT, WMT, WNT><<<dim3((unsigned)(8 * per)), dim3(NTH), FMT == kFmtW4 ? C::kLdsW4 : 2 * C::kStage, st>>>(
-        q, s, n, k, x, ldx, t, c, ldc, out, sdt, nbn, nbt);
+        q, s, n, k, x, ldx, t, c, ldc, out, sdt, nbn, nbt, MoePfArgs{});
     HIP_CHECK(hipGetLastError());
 }
 
@@ -341,6 +414,23 @@ void gemm_check(int n, int k, const void* x, int ldx, int ldc, int t, bool glu) 
 }
 
 }  // namespace
+
+// MoE grouped prefill GEMMs: 128 rows (a job) x 256 weight rows (gate_up: one record) per block, 8 waves of
+// 64 x 64; grid = 8 XCD lanes x ceil(max_jobs / 8) job groups x n tiles (blocks past the job count exit)
+void moe_pf_gemm(int mode, const MoePfArgs& a, hipStream_t st) {
+    using C = Cfg<2, 2>;
+    static_assert(C::BM == kMoePfRows && C::BN == 256, "MoE prefill tile");
+    CHECK(a.H % 256 == 0 && a.I % 128 == 0 && a.max_jobs >= 1, "moe_pf H %d I %d", a.H, a.I);
+    const int nbn = mode == 1 ? a.ngrp : a.H / C::BN;
+    const unsigned grid = 8u * (unsigned)((a.max_jobs + 7) / 8) * (unsigned)nbn;
+    if (mode == 1)
+        gemm_kernel<kFmtW4, kScaleF16, 2, 2, 1><<<dim3(grid), dim3(NTH), C::kLdsW4, st>>>(
+            nullptr, nullptr, 256, a.H, nullptr, 0, 0, nullptr, 0, kOutGLU, kScaleF16, nbn, 0, a);
+    else
+        gemm_kernel<kFmtW4, kScaleF16, 2, 2, 2><<<dim3(grid), dim3(NTH), C::kLdsW4, st>>>(
+            nullptr, nullptr, a.H, a.I, nullptr, 0, 0, nullptr, 0, kOutBF16, kScaleF16, nbn, 0, a);
+    HIP_CHECK(hipGetLastError());
+}
 
 void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st) {
     gemm_check(w.n, w.k, x, ldx, ldc, t, w.glu);

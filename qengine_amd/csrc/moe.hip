@@ -15,9 +15,9 @@
 // :6436-6482), so the layer is deterministic.
 //
 // Decode (T <= 32): the grouped GEMVs reuse the decode GEMV tile (gemv_impl.hpp) with gathered activation rows,
-// jobs = (expert, chunk of <= 2 rows). Prefill: grouped MFMA GEMMs over (expert, 64-row tile) jobs.
+// jobs = (expert, chunk of <= 2 rows). Prefill: grouped MFMA GEMMs over (expert, 128-row tile) jobs, one block per
+// (job, 256 weight rows): every expert's weights are read once per 128 of its rows.
 #include "gemv_impl.hpp"
-#include "mfma_tile.hpp"
 #include "../../include/qe_kernels.h"
 
 #include <vector>
@@ -261,123 +261,8 @@ __global__ void __launch_bounds__(64 * kMaxWavesGeneric) moe_dec_down_kernel(
     }
 }
 
-// ------------------------------------------------------------------ prefill grouped GEMMs (MFMA)
-constexpr int PBM = 64, PBN = 128, PBK = 64, PNTH = 256;
-constexpr int kPStage = (PBM + PBN) * PBK * 2;  // 24 KB
-
-// MODE 0: gate_up, block (job, record g * 2 + half): rows 128 half .. +128 of gq, K = H, A = x[token(slot)]
-// MODE 1: down, block (job, 128-row tile of H): K = I over the NGRP records, A = act[slot]
-template <int MODE>
-__global__ void __launch_bounds__(PNTH) moe_pf_kernel(const char* __restrict__ recs, MoeShape sh,
-                                                      const uint16_t* __restrict__ a_src,
-                                                      const int32_t* __restrict__ off,
-                                                      const int32_t* __restrict__ slot_tok,
-                                                      const float* __restrict__ slot_w,
-                                                      const int32_t* __restrict__ jobs,
-                                                      const int32_t* __restrict__ njobs, uint16_t* __restrict__ out) {
-    using namespace qe_tile;
-    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
-    char* plds = reinterpret_cast<char*>(lds);
-    const int job = blockIdx.x;
-    if (job >= *njobs) return;
-    const int e = jobs[2 * job], r0 = jobs[2 * job + 1];
-    const int slot0 = off[e] + r0, rows = min(PBM, off[e + 1] - slot0);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int K = MODE == 0 ? sh.H : sh.I, KT = K / PBK, lda = K;
-
-    // A rows: 64 x 64 bf16 per step, 2 x 16 B per thread
-    const uint16_t* arow[2];
-    int ach[2], arr[2];
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int idx = tid + i * PNTH;
-        arr[i] = idx >> 3;
-        ach[i] = idx & 7;
-        const int sl = slot0 + (arr[i] < rows ? arr[i] : 0);
-        arow[i] = a_src + (size_t)(MODE == 0 ? slot_tok[sl] : sl) * lda;
-    }
-    // W: 8 tiles of 16 rows, one 16 B record per thread
-    const int tr = tid >> 5, wl = tid & 31, wg = wl >> 2, wt4 = wl & 3, wrow = tr * 16 + wg;
-    const int G = sh.H >> 7;
-    u32x4_v ar[2], wr;
-    uint16_t sr_lo, sr_hi;
-    auto load = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-            ar[i] = arr[i] < rows ? *reinterpret_cast<const u32x4_v*>(arow[i] + kt * PBK + ach[i] * 8)
-                                  : u32x4_v{0u, 0u, 0u, 0u};
-        const uint4* qp;
-        const uint16_t* sp;
-        if constexpr (MODE == 0) {
-            const char* rp = rec_ptr(recs, sh, e, blockIdx.y >> 1);
-            const int tile = (blockIdx.y & 1) * 8 + tr;
-            qp = reinterpret_cast<const uint4*>(rp) + ((size_t)tile * (sh.H >> 6) + kt) * 32 + wl;
-            sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q) + ((size_t)tile * G + (kt >> 1)) * 16;
-        } else {
-            const char* rp = rec_ptr(recs, sh, e, kt >> 1);
-            const int tile = blockIdx.y * 8 + tr;
-            qp = reinterpret_cast<const uint4*>(rp + sh.gg_q + sh.gg_s) + ((size_t)tile * 2 + (kt & 1)) * 32 + wl;
-            sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q) + (size_t)tile * 16;
-        }
-        wr = __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(qp));
-        sr_lo = sp[wg];
-        sr_hi = sp[wg + 8];
-    };
-    auto store = [&](char* at, char* wt) {
-#pragma unroll
-        for (int i = 0; i < 2; i++) *reinterpret_cast<u32x4_v*>(at + swz(arr[i], ach[i])) = ar[i];
-        const float s_lo = scale_to_f32<kScaleF16>(sr_lo), s_hi = scale_to_f32<kScaleF16>(sr_hi);
-#pragma unroll
-        for (int j = 0; j < 4; j++) dq_w4_word(wr[j], s_lo, s_hi, wt, wrow, 16 * j + 2 * wt4);
-    };
-
-    // waves 2 x 2: rows wm * 32 .. +32, weight rows wn * 64 .. +64 (two 32 x 32 tiles)
-    const int wm = wave >> 1, wn = wave & 1;
-    f32x16_v acc[2];
-#pragma unroll
-    for (int b = 0; b < 2; b++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[b][r] = 0.f;
-    load(0);
-    for (int kt = 0; kt < KT; kt++) {
-        char* at = plds + (kt & 1) * kPStage;
-        char* wt = at + PBM * PBK * 2;
-        store(at, wt);
-        __syncthreads();
-        if (kt + 1 < KT) load(kt + 1);
-#pragma unroll
-        for (int ks = 0; ks < PBK / 16; ks++) {
-            const int fr = lane & 31, fc = 2 * ks + (lane >> 5);
-            const bf16x8_v af = *reinterpret_cast<const bf16x8_v*>(at + swz(wm * 32 + fr, fc));
-#pragma unroll
-            for (int b = 0; b < 2; b++) {
-                const bf16x8_v bf = *reinterpret_cast<const bf16x8_v*>(wt + swz(wn * 64 + b * 32 + fr, fc));
-                acc[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc[b], 0, 0, 0);
-            }
-        }
-    }
-    const int cj = lane & 31;
-#pragma unroll
-    for (int b = 0; b < 2; b++) {
-        const int nl = wn * 64 + b * 32 + cj;  // weight row within the block's 128
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-            const int row = wm * 32 + c_row(lane, r);
-            const float v = acc[b][r];
-            if constexpr (MODE == 0) {
-                const float up = __builtin_bit_cast(
-                    float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x128 /* row_ror:8 */, 0xF, 0xF,
-                                                       false));
-                if ((cj & 15) < 8 && row < rows) {
-                    const int col = (blockIdx.y >> 1) * 128 + (blockIdx.y & 1) * 64 + (nl >> 4) * 8 + (cj & 7);
-                    out[(size_t)(slot0 + row) * sh.I + col] = f32_to_bf16(silu_f32(v) * up * slot_w[slot0 + row]);
-                }
-            } else if (row < rows) {
-                out[(size_t)(slot0 + row) * sh.H + blockIdx.y * PBN + nl] = f32_to_bf16(v);
-            }
-        }
-    }
-}
+// ------------------------------------------------------------------ prefill grouped GEMMs
+// (expert, 128-row) jobs on the prefill GEMM's W4 pipeline: moe_pf_gemm in gemm.hip
 
 // ------------------------------------------------------------------ combine: out[t] = sum_k slot_out[inv[t, k]]
 __global__ void moe_combine_kernel(const uint16_t* __restrict__ slot_out, const int32_t* __restrict__ inv, int topk,
@@ -428,7 +313,7 @@ MoeWs moe_ws(void* base, int T, int E, int topk, int H, int I) {
         return r;
     };
     const size_t P = (size_t)T * topk;
-    const int mj = max_jobs(T, E, topk, T <= 32 ? kDecRows : PBM);
+    const int mj = max_jobs(T, E, topk, T <= 32 ? kDecRows : kMoePfRows);
     ws.sel = reinterpret_cast<int32_t*>(take(P * 4));
     ws.w = reinterpret_cast<float*>(take(P * 4));
     ws.off = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
@@ -489,7 +374,7 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)workspace & 255) == 0, "moe x 16-byte / workspace 256-byte alignment");
     const char* recs = reinterpret_cast<const char*>(records);
     const bool decode = T <= 32;
-    const int chunk = decode ? kDecRows : PBM;
+    const int chunk = decode ? kDecRows : kMoePfRows;
     const int mj = max_jobs(T, E, topk, chunk);
 
     moe_route_kernel<<<(T + 3) / 4, kRouteThreads, 0, st>>>(logits, T, E, topk, ws.sel, ws.w);
@@ -513,12 +398,27 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
             recs, sh, ws.act, ws.off, ws.jobs, ws.njobs, ws.slot_out);
         HIP_CHECK(hipGetLastError());
     } else {
-        moe_pf_kernel<0><<<dim3(mj, sh.ngrp * 2), PNTH, 2 * kPStage, st>>>(recs, sh, x, ws.off, ws.slot_tok, ws.slot_w,
-                                                                         ws.jobs, ws.njobs, ws.act);
-        HIP_CHECK(hipGetLastError());
-        moe_pf_kernel<1><<<dim3(mj, H / PBN), PNTH, 2 * kPStage, st>>>(recs, sh, ws.act, ws.off, ws.slot_tok,
-                                                                     ws.slot_w, ws.jobs, ws.njobs, ws.slot_out);
-        HIP_CHECK(hipGetLastError());
+        MoePfArgs pa;
+        pa.recs = recs;
+        pa.rec = sh.rec;
+        pa.gg_q = sh.gg_q;
+        pa.gg_s = sh.gg_s;
+        pa.gd_q = sh.gd_q;
+        pa.ngrp = sh.ngrp;
+        pa.H = H;
+        pa.I = I;
+        pa.off = ws.off;
+        pa.slot_tok = ws.slot_tok;
+        pa.slot_w = ws.slot_w;
+        pa.jobs = ws.jobs;
+        pa.njobs = ws.njobs;
+        pa.max_jobs = mj;
+        pa.a = x;
+        pa.out = ws.act;
+        moe_pf_gemm(1, pa, st);
+        pa.a = ws.act;
+        pa.out = ws.slot_out;
+        moe_pf_gemm(2, pa, st);
     }
     moe_combine_kernel<<<T, 256, 0, st>>>(ws.slot_out, ws.inv, topk, H, out, (flags & QE_OUT_BF16) ? 1 : 0);
     HIP_CHECK(hipGetLastError());

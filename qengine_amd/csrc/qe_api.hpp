@@ -68,3 +68,23 @@ bool gemm_out_bf16();
 void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 
 int qe_num_cus();
+
+// ---- grouped prefill GEMMs of the MoE layer on the prefill GEMM's W4 pipeline (gemm.hip) ----
+// Jobs are (expert, first row) pairs over the expert-sorted slots, kMoePfRows rows each (moe.hip's segmentation).
+// mode 1, gate_up: act[slot][I] = bf16(silu(gate) * up * slot_w[slot]) from the records' GLU rows over x[token];
+// mode 2, down: slot_out[slot][H] = bf16(act[slot] . down) over the records' down columns.
+constexpr int kMoePfRows = 128;
+struct MoePfArgs {
+    const char* recs = nullptr;      // expert-major group records
+    size_t rec = 0, gg_q = 0, gg_s = 0, gd_q = 0;  // record bytes and part offsets
+    int ngrp = 0, H = 0, I = 0;
+    const uint16_t* a = nullptr;     // mode 1: x [T][H]; mode 2: act [slots][I]
+    const int32_t* off = nullptr;    // [E + 1] first slot of each expert
+    const int32_t* slot_tok = nullptr;
+    const float* slot_w = nullptr;
+    const int32_t* jobs = nullptr;   // [max_jobs][2]
+    const int32_t* njobs = nullptr;
+    uint16_t* out = nullptr;         // mode 1: act; mode 2: slot_out
+    int max_jobs = 0;
+};
+void moe_pf_gemm(int mode, const MoePfArgs& a, hipStream_t st);
