@@ -54,23 +54,37 @@ __device__ __forceinline__ const char* rec_ptr(const char* recs, const MoeShape&
 constexpr int kRouteThreads = 256;  // 4 tokens per block
 constexpr int kMaxExperts = 1024;
 
-// Lane l holds the logits of experts l + 64 i. Each of the topk rounds takes the lane's best untaken expert (value
-// desc; its experts ascend with i, so the first maximum is the lowest index) and reduces over the wave with the
-// tie rule (value desc, index asc): shuffles only, no barriers.
+// one argmax step over a DPP pattern with the tie rule (value desc, index asc)
+template <int CTRL>
+__device__ __forceinline__ void route_step(float& bv, int& bi) {
+    const float v2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, bv), CTRL, 0xF,
+                                                                           0xF, false));
+    const int i2 = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xF, 0xF, false);
+    const bool b2 = (v2 > bv) | ((v2 == bv) & (i2 < bi));
+    bv = b2 ? v2 : bv;
+    bi = b2 ? i2 : bi;
+}
+
+// Lane l holds the logits of experts l + 64 i (i < PER = ceil(E / 64)). Each of the topk rounds takes the lane's best
+// untaken expert (value desc; its experts ascend with i, so the first maximum is the lowest index; selects, no
+// branches), reduces each 16-lane row by DPP (quad swaps, then row rotations by 4 and 8) and the four row results by
+// readlane, with the tie rule (value desc, index asc): no LDS traffic, no barriers.
+template <int PER>
 __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
                                                                   int topk, int32_t* __restrict__ sel,
                                                                   float* __restrict__ w) {
     const int lane = threadIdx.x & 63, t = blockIdx.x * (kRouteThreads / 64) + (threadIdx.x >> 6);
     if (t >= T) return;
-    constexpr int PER = kMaxExperts / 64;
     float v[PER];
     const float* l = logits + (size_t)t * E;
 #pragma unroll
     for (int i = 0; i < PER; i++) {
         const int e = lane + 64 * i;
-        v[i] = e < E ? l[e] : -INFINITY;
+        v[i] = l[e < E ? e : E - 1];
     }
-    unsigned taken = 0;
+    unsigned avail = 0;  // bit i: expert lane + 64 i exists and is not taken
+#pragma unroll
+    for (int i = 0; i < PER; i++) avail |= (lane + 64 * i < E ? 1u : 0u) << i;
     float myv = 0.f;  // lane k keeps round k's value and index
     int myi = 0;
     float v0 = 0.f;
@@ -79,95 +93,90 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
         int bii = 0x7fffffff;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const int e = lane + 64 * i;
-            if (e < E && !(taken >> i & 1u) && (v[i] > bvv || bii == 0x7fffffff)) {
-                bvv = v[i];
-                bii = e;
-            }
+            const bool better = (((avail >> i) & 1u) != 0) & ((v[i] > bvv) | (bii == 0x7fffffff));  // no short circuit
+            bvv = better ? v[i] : bvv;
+            bii = better ? lane + 64 * i : bii;
         }
+        route_step<0xB1>(bvv, bii);   // quad_perm [1,0,3,2]
+        route_step<0x4E>(bvv, bii);   // quad_perm [2,3,0,1]
+        route_step<0x124>(bvv, bii);  // row_ror:4
+        route_step<0x128>(bvv, bii);  // row_ror:8
+        float fv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bvv), 0));
+        int fi = __builtin_amdgcn_readlane(bii, 0);
 #pragma unroll
-        for (int o = 32; o > 0; o >>= 1) {
-            const float v2 = __shfl_xor(bvv, o);
-            const int i2 = __shfl_xor(bii, o);
-            if (v2 > bvv || (v2 == bvv && i2 < bii)) {
-                bvv = v2;
-                bii = i2;
-            }
+        for (int r = 1; r < 4; r++) {
+            const float v2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bvv), 16 * r));
+            const int i2 = __builtin_amdgcn_readlane(bii, 16 * r);
+            const bool b2 = (v2 > fv) | ((v2 == fv) & (i2 < fi));
+            fv = b2 ? v2 : fv;
+            fi = b2 ? i2 : fi;
         }
-        if ((bii & 63) == lane) taken |= 1u << (bii >> 6);
-        if (lane == k) {
-            myv = bvv;
-            myi = bii;
-        }
-        if (k == 0) v0 = bvv;
+        avail &= (fi & 63) == lane ? ~(1u << (fi >> 6)) : ~0u;
+        myv = lane == k ? fv : myv;
+        myi = lane == k ? fi : myi;
+        v0 = k == 0 ? fv : v0;
     }
     // weights exp(l_k - l_max) / sum, the sum in k order
+    const float ex = expf(myv - v0);
     float tot = 0.f;
-    for (int k = 0; k < topk; k++) tot += expf(__shfl(myv, k) - v0);
+    for (int k = 0; k < topk; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
     if (lane < topk) {
         sel[(size_t)t * topk + lane] = myi;
-        w[(size_t)t * topk + lane] = expf(myv - v0) / tot;
+        w[(size_t)t * topk + lane] = ex / tot;
     }
 }
 
-// ------------------------------------------------------------------ sort & segment: one block
+void launch_route(const float* logits, int T, int E, int topk, int32_t* sel, float* w, hipStream_t st) {
+    const dim3 grid((T + 3) / 4), block(kRouteThreads);
+    const int per = (E + 63) / 64;
+    if (per <= 1) moe_route_kernel<1><<<grid, block, 0, st>>>(logits, T, E, topk, sel, w);
+    else if (per <= 2) moe_route_kernel<2><<<grid, block, 0, st>>>(logits, T, E, topk, sel, w);
+    else if (per <= 4) moe_route_kernel<4><<<grid, block, 0, st>>>(logits, T, E, topk, sel, w);
+    else if (per <= 8) moe_route_kernel<8><<<grid, block, 0, st>>>(logits, T, E, topk, sel, w);
+    else moe_route_kernel<16><<<grid, block, 0, st>>>(logits, T, E, topk, sel, w);
+    HIP_CHECK(hipGetLastError());
+}
+
+// ------------------------------------------------------------------ sort & segment
 constexpr int kSegThreads = 1024;
 constexpr int kSegChunk = 64;  // tokens per chunk (64-bit masks)
 
-// out: off [E+1]; per slot: pair (t * topk + k), token, weight; inv [pair] = slot; jobs (expert, first row) of
-// `chunk` rows each, njobs
-__global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t* __restrict__ sel,
-                                                                  const float* __restrict__ w, int T, int E, int topk,
-                                                                  int chunk, int32_t* __restrict__ off,
-                                                                  int32_t* __restrict__ slot_pair,
-                                                                  int32_t* __restrict__ slot_tok,
-                                                                  float* __restrict__ slot_w, int32_t* __restrict__ inv,
-                                                                  int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
-    __shared__ int cnt[kMaxExperts], pre[kMaxExperts + 1], jpre[kMaxExperts + 1], fill[kMaxExperts];
-    __shared__ unsigned long long mark[kMaxExperts];
-    const int tid = threadIdx.x;
-    const int P = T * topk;
-    for (int e = tid; e < E; e += kSegThreads) {
-        cnt[e] = 0;
-        fill[e] = 0;
+// exclusive scans of the expert counts cnt[] (slot offsets pre[], written to off[]) and of their job counts (jobs
+// (expert, first row) of `chunk` rows each, njobs), E <= 1024: thread e, wave scans by shuffles, then the 16 wave
+// totals. Block of kSegThreads; ends with a barrier.
+__device__ void seg_scan_jobs(const int* cnt, int* pre, int E, int chunk, int32_t* __restrict__ off,
+                              int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
+    __shared__ int wa[kSegThreads / 64], wb[kSegThreads / 64], jpre[kMaxExperts + 1];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int c0 = tid < E ? cnt[tid] : 0;
+    const int j0 = (c0 + chunk - 1) / chunk;
+    int a = c0, bsum = j0;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int a2 = __shfl_up(a, o), b2 = __shfl_up(bsum, o);
+        if (lane >= o) {
+            a += a2;
+            bsum += b2;
+        }
+    }
+    if (lane == 63) {
+        wa[wv] = a;
+        wb[wv] = bsum;
     }
     __syncthreads();
-    for (int i = tid; i < P; i += kSegThreads) atomicAdd(&cnt[sel[i]], 1);
-    __syncthreads();
-    {  // exclusive scans of the counts and the job counts over the E <= 1024 experts: thread e, wave scans by
-       // shuffles, then the 16 wave totals
-        __shared__ int wa[kSegThreads / 64], wb[kSegThreads / 64];
-        const int lane = tid & 63, wv = tid >> 6;
-        const int c0 = tid < E ? cnt[tid] : 0;
-        const int j0 = (c0 + chunk - 1) / chunk;
-        int a = c0, bsum = j0;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int a2 = __shfl_up(a, o), b2 = __shfl_up(bsum, o);
-            if (lane >= o) {
-                a += a2;
-                bsum += b2;
-            }
-        }
-        if (lane == 63) {
-            wa[wv] = a;
-            wb[wv] = bsum;
-        }
-        __syncthreads();
-        int ao = 0, bo = 0;
-        for (int q = 0; q < wv; q++) {
-            ao += wa[q];
-            bo += wb[q];
-        }
-        if (tid < E) {
-            pre[tid] = ao + a - c0;
-            jpre[tid] = bo + bsum - j0;
-        }
-        if (tid == E - 1) {
-            pre[E] = ao + a;
-            jpre[E] = bo + bsum;
-            *njobs = bo + bsum;
-        }
+    int ao = 0, bo = 0;
+    for (int q = 0; q < wv; q++) {
+        ao += wa[q];
+        bo += wb[q];
+    }
+    if (tid < E) {
+        pre[tid] = ao + a - c0;
+        jpre[tid] = bo + bsum - j0;
+    }
+    if (tid == E - 1) {
+        pre[E] = ao + a;
+        jpre[E] = bo + bsum;
+        *njobs = bo + bsum;
     }
     __syncthreads();
     for (int e = tid; e <= E; e += kSegThreads) off[e] = pre[e];
@@ -178,29 +187,121 @@ __global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t*
             jobs[2 * (jpre[e] + j) + 1] = j * chunk;
         }
     }
+    __syncthreads();
+}
+
+// place the pairs of the 64-token chunk starting at token t0: a pair's slot is base[e] (the expert's first slot
+// for this chunk) + the number of earlier tokens of the chunk on the same expert (a 64-bit token mask per expert:
+// ascending (token, k) inside an expert, as a pair's experts are distinct). mark[E] in LDS; ends with a barrier.
+__device__ void seg_place_chunk(const int32_t* __restrict__ sel, const float* __restrict__ w, int T, int E, int topk,
+                                int t0, const int* base, unsigned long long* mark, int32_t* __restrict__ slot_pair,
+                                int32_t* __restrict__ slot_tok, float* __restrict__ slot_w, int32_t* __restrict__ inv) {
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += kSegThreads) mark[e] = 0ull;
+    __syncthreads();
+    const int tl = tid / topk;  // token of this thread within the chunk (topk <= 16)
+    const int p = t0 * topk + tid;
+    const bool act = tl < kSegChunk && t0 + tl < T;
+    int e = 0;
+    if (act) {
+        e = sel[p];
+        atomicOr(&mark[e], 1ull << tl);
+    }
+    __syncthreads();
+    if (act) {
+        const int slot = base[e] + __popcll(mark[e] & ((1ull << tl) - 1ull));
+        slot_pair[slot] = p;
+        slot_tok[slot] = t0 + tl;
+        slot_w[slot] = w[p];
+        inv[p] = slot;
+    }
+    __syncthreads();
+}
+
+// One block (small T, and the qe_moe_segment entry point). out: off [E+1]; per slot: pair (t * topk + k), token,
+// weight; inv [pair] = slot; jobs (expert, first row) of `chunk` rows each, njobs
+__global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t* __restrict__ sel,
+                                                                  const float* __restrict__ w, int T, int E, int topk,
+                                                                  int chunk, int32_t* __restrict__ off,
+                                                                  int32_t* __restrict__ slot_pair,
+                                                                  int32_t* __restrict__ slot_tok,
+                                                                  float* __restrict__ slot_w, int32_t* __restrict__ inv,
+                                                                  int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
+    __shared__ int cnt[kMaxExperts], pre[kMaxExperts + 1], fill[kMaxExperts];
+    __shared__ unsigned long long mark[kMaxExperts];
+    const int tid = threadIdx.x;
+    const int P = T * topk;
+    for (int e = tid; e < E; e += kSegThreads) cnt[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < P; i += kSegThreads) atomicAdd(&cnt[sel[i]], 1);
+    __syncthreads();
+    seg_scan_jobs(cnt, pre, E, chunk, off, jobs, njobs);
+    for (int e = tid; e < E; e += kSegThreads) fill[e] = pre[e];  // first free slot of each expert
+    __syncthreads();
     for (int t0 = 0; t0 < T; t0 += kSegChunk) {
-        for (int e = tid; e < E; e += kSegThreads) mark[e] = 0ull;
-        __syncthreads();
-        const int tl = tid / topk;  // token of this thread within the chunk (topk <= 16)
-        const int p = t0 * topk + tid;
-        const bool act = tl < kSegChunk && t0 + tl < T;
-        int e = 0;
-        if (act) {
-            e = sel[p];
-            atomicOr(&mark[e], 1ull << tl);
-        }
-        __syncthreads();
-        if (act) {
-            const int slot = pre[e] + fill[e] + __popcll(mark[e] & ((1ull << tl) - 1ull));
-            slot_pair[slot] = p;
-            slot_tok[slot] = t0 + tl;
-            slot_w[slot] = w[p];
-            inv[p] = slot;
-        }
-        __syncthreads();
+        seg_place_chunk(sel, w, T, E, topk, t0, fill, mark, slot_pair, slot_tok, slot_w, inv);
         for (int e2 = tid; e2 < E; e2 += kSegThreads) fill[e2] += __popcll(mark[e2]);
         __syncthreads();
     }
+}
+
+// above this many tokens the layer segments with the three-kernel path below (one block walks the chunks in turn)
+constexpr int kSegOneBlockTokens = 256;
+
+// Many tokens: the chunks in parallel. (1) counts per (chunk, expert) -> cntb [B][E]; (2) one block: per expert the
+// exclusive scan over the chunks (cntb becomes each chunk's offset inside the expert), the expert offsets and the
+// jobs; (3) per chunk: the pairs placed at off[e] + cntb[b][e] + rank. Same slots as the one-block kernel.
+__global__ void __launch_bounds__(kSegThreads) moe_seg_count_kernel(const int32_t* __restrict__ sel, int T, int E,
+                                                                    int topk, int32_t* __restrict__ cntb) {
+    __shared__ int cnt[kMaxExperts];
+    const int tid = threadIdx.x, b = blockIdx.x;
+    for (int e = tid; e < E; e += kSegThreads) cnt[e] = 0;
+    __syncthreads();
+    const int p0 = b * kSegChunk * topk, p1 = min(T, (b + 1) * kSegChunk) * topk;
+    for (int p = p0 + tid; p < p1; p += kSegThreads) atomicAdd(&cnt[sel[p]], 1);
+    __syncthreads();
+    for (int e = tid; e < E; e += kSegThreads) cntb[(size_t)b * E + e] = cnt[e];
+}
+
+__global__ void __launch_bounds__(kSegThreads) moe_seg_scan_kernel(int nchunk, int E, int chunk,
+                                                                   int32_t* __restrict__ cntb,
+                                                                   int32_t* __restrict__ off,
+                                                                   int32_t* __restrict__ jobs,
+                                                                   int32_t* __restrict__ njobs) {
+    __shared__ int cnt[kMaxExperts], pre[kMaxExperts + 1];
+    const int tid = threadIdx.x;
+    for (int e = tid; e < E; e += kSegThreads) {
+        int run = 0;
+        for (int b0 = 0; b0 < nchunk; b0 += 16) {  // 16 loads in flight, then the running sums
+            int v[16];
+#pragma unroll
+            for (int j = 0; j < 16; j++) v[j] = b0 + j < nchunk ? cntb[(size_t)(b0 + j) * E + e] : 0;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                if (b0 + j < nchunk) cntb[(size_t)(b0 + j) * E + e] = run;
+                run += v[j];
+            }
+        }
+        cnt[e] = run;
+    }
+    __syncthreads();
+    seg_scan_jobs(cnt, pre, E, chunk, off, jobs, njobs);
+}
+
+__global__ void __launch_bounds__(kSegThreads) moe_seg_place_kernel(const int32_t* __restrict__ sel,
+                                                                    const float* __restrict__ w, int T, int E,
+                                                                    int topk, const int32_t* __restrict__ off,
+                                                                    const int32_t* __restrict__ cntb,
+                                                                    int32_t* __restrict__ slot_pair,
+                                                                    int32_t* __restrict__ slot_tok,
+                                                                    float* __restrict__ slot_w,
+                                                                    int32_t* __restrict__ inv) {
+    __shared__ int base[kMaxExperts];
+    __shared__ unsigned long long mark[kMaxExperts];
+    const int tid = threadIdx.x, b = blockIdx.x;
+    for (int e = tid; e < E; e += kSegThreads) base[e] = off[e] + cntb[(size_t)b * E + e];
+    __syncthreads();
+    seg_place_chunk(sel, w, T, E, topk, b * kSegChunk, base, mark, slot_pair, slot_tok, slot_w, inv);
 }
 
 // ------------------------------------------------------------------ decode grouped GEMVs (gemv_tile)
@@ -265,35 +366,44 @@ __global__ void __launch_bounds__(64 * kMaxWavesGeneric) moe_dec_down_kernel(
 // (expert, 128-row) jobs on the prefill GEMM's W4 pipeline: moe_pf_gemm in gemm.hip
 
 // ------------------------------------------------------------------ combine: out[t] = sum_k slot_out[inv[t, k]]
+// block t, H / 8 threads: each thread's 8 columns of every slot of the token are one 16-byte load, all issued
+// before the sums (in k order, fp32)
 __global__ void moe_combine_kernel(const uint16_t* __restrict__ slot_out, const int32_t* __restrict__ inv, int topk,
                                    int H, void* __restrict__ out, int out_bf16) {
-    const int t = blockIdx.x;
-    // the token's slots, loaded once (topk <= 16), so the slot loads of all columns issue together
+    const int t = blockIdx.x, c = threadIdx.x * 8;
     int sl[16];
 #pragma unroll
     for (int k = 0; k < 16; k++) sl[k] = k < topk ? inv[t * topk + k] : 0;
-    for (int c = threadIdx.x * 2; c < H; c += blockDim.x * 2) {
-        float a0 = 0.f, a1 = 0.f;
+    u32x4_v v[16];
 #pragma unroll
-        for (int k = 0; k < 16; k++) {
-            if (k >= topk) break;
-            const uint32_t v = *reinterpret_cast<const uint32_t*>(slot_out + (size_t)sl[k] * H + c);
-            a0 += bf16_to_f32((uint16_t)v);
-            a1 += bf16_to_f32((uint16_t)(v >> 16));
+    for (int k = 0; k < 16; k++)
+        if (k < topk) v[k] = *reinterpret_cast<const u32x4_v*>(slot_out + (size_t)sl[k] * H + c);
+    float a[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) a[j] = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+        if (k < topk) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                a[2 * j] += bf16_to_f32((uint16_t)v[k][j]);
+                a[2 * j + 1] += bf16_to_f32((uint16_t)(v[k][j] >> 16));
+            }
         }
-        if (out_bf16) {
-            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + (size_t)t * H + c) = pack_bf16x2(a0, a1);
-        } else {
-            float* o = reinterpret_cast<float*>(out) + (size_t)t * H + c;
-            o[0] = a0;
-            o[1] = a1;
-        }
+    }
+    if (out_bf16) {
+        *reinterpret_cast<u32x4_v*>(reinterpret_cast<uint16_t*>(out) + (size_t)t * H + c) =
+            u32x4_v{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(a[4], a[5]), pack_bf16x2(a[6], a[7])};
+    } else {
+        f32x4_v* o = reinterpret_cast<f32x4_v*>(reinterpret_cast<float*>(out) + (size_t)t * H + c);
+        o[0] = f32x4_v{a[0], a[1], a[2], a[3]};
+        o[1] = f32x4_v{a[4], a[5], a[6], a[7]};
     }
 }
 
 // ------------------------------------------------------------------ workspace layout
 struct MoeWs {
-    int32_t *sel, *off, *slot_pair, *slot_tok, *inv, *jobs, *njobs;
+    int32_t *sel, *off, *slot_pair, *slot_tok, *inv, *jobs, *njobs, *cntb;
     float *w, *slot_w;
     uint16_t *act, *slot_out;
     size_t bytes;
@@ -323,6 +433,7 @@ MoeWs moe_ws(void* base, int T, int E, int topk, int H, int I) {
     ws.inv = reinterpret_cast<int32_t*>(take(P * 4));
     ws.jobs = reinterpret_cast<int32_t*>(take((size_t)mj * 8));
     ws.njobs = reinterpret_cast<int32_t*>(take(4));
+    ws.cntb = reinterpret_cast<int32_t*>(take((size_t)((T + kSegChunk - 1) / kSegChunk) * E * 4));
     ws.act = reinterpret_cast<uint16_t*>(take(P * I * 2));
     ws.slot_out = reinterpret_cast<uint16_t*>(take(P * H * 2));
     ws.bytes = o;
@@ -343,9 +454,7 @@ extern "C" {
 void qe_moe_route(const float* logits, int T, int E, int topk, int32_t* sel, float* w, void* stream) {
     CHECK(T >= 1 && E >= 1 && E <= kMaxExperts && topk >= 1 && topk <= 32 && topk <= E, "moe_route T %d E %d topk %d",
           T, E, topk);
-    moe_route_kernel<<<(T + 3) / 4, kRouteThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(logits, T, E, topk, sel,
-                                                                                              w);
-    HIP_CHECK(hipGetLastError());
+    launch_route(logits, T, E, topk, sel, w, reinterpret_cast<hipStream_t>(stream));
 }
 
 void qe_moe_segment(const int32_t* sel, const float* w, int T, int E, int topk, int chunk, int32_t* off,
@@ -371,16 +480,26 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     const MoeShape sh = moe_shape(E, topk, H, I);
     const MoeWs ws = moe_ws(workspace, T, E, topk, H, I);
     CHECK(workspace && ws_bytes >= ws.bytes, "moe workspace %zu < %zu bytes", ws_bytes, ws.bytes);
-    CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)workspace & 255) == 0, "moe x 16-byte / workspace 256-byte alignment");
+    CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)workspace & 255) == 0,
+          "moe x / out 16-byte, workspace 256-byte alignment");
     const char* recs = reinterpret_cast<const char*>(records);
     const bool decode = T <= 32;
     const int chunk = decode ? kDecRows : kMoePfRows;
     const int mj = max_jobs(T, E, topk, chunk);
 
-    moe_route_kernel<<<(T + 3) / 4, kRouteThreads, 0, st>>>(logits, T, E, topk, ws.sel, ws.w);
-    HIP_CHECK(hipGetLastError());
-    moe_segment_kernel<<<1, kSegThreads, 0, st>>>(ws.sel, ws.w, T, E, topk, chunk, ws.off, ws.slot_pair, ws.slot_tok,
-                                                  ws.slot_w, ws.inv, ws.jobs, ws.njobs);
+    launch_route(logits, T, E, topk, ws.sel, ws.w, st);
+    if (T > kSegOneBlockTokens) {
+        const int nchunk = (T + kSegChunk - 1) / kSegChunk;
+        moe_seg_count_kernel<<<nchunk, kSegThreads, 0, st>>>(ws.sel, T, E, topk, ws.cntb);
+        HIP_CHECK(hipGetLastError());
+        moe_seg_scan_kernel<<<1, kSegThreads, 0, st>>>(nchunk, E, chunk, ws.cntb, ws.off, ws.jobs, ws.njobs);
+        HIP_CHECK(hipGetLastError());
+        moe_seg_place_kernel<<<nchunk, kSegThreads, 0, st>>>(ws.sel, ws.w, T, E, topk, ws.off, ws.cntb, ws.slot_pair,
+                                                             ws.slot_tok, ws.slot_w, ws.inv);
+    } else {
+        moe_segment_kernel<<<1, kSegThreads, 0, st>>>(ws.sel, ws.w, T, E, topk, chunk, ws.off, ws.slot_pair,
+                                                      ws.slot_tok, ws.slot_w, ws.inv, ws.jobs, ws.njobs);
+    }
     HIP_CHECK(hipGetLastError());
     if (decode) {
         const int G = H / 128;
@@ -420,7 +539,7 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
         pa.out = ws.slot_out;
         moe_pf_gemm(2, pa, st);
     }
-    moe_combine_kernel<<<T, 256, 0, st>>>(ws.slot_out, ws.inv, topk, H, out, (flags & QE_OUT_BF16) ? 1 : 0);
+    moe_combine_kernel<<<T, H / 8, 0, st>>>(ws.slot_out, ws.inv, topk, H, out, (flags & QE_OUT_BF16) ? 1 : 0);
     HIP_CHECK(hipGetLastError());
 }
 
