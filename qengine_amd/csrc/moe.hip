@@ -69,12 +69,11 @@ __device__ __forceinline__ void route_step(float& bv, int& bi) {
 // untaken expert (value desc; its experts ascend with i, so the first maximum is the lowest index; selects, no
 // branches), reduces each 16-lane row by DPP (quad swaps, then row rotations by 4 and 8) and the four row results by
 // readlane, with the tie rule (value desc, index asc): no LDS traffic, no barriers.
+// one token t by the calling wave; sel / w: the token's topk outputs (global or LDS)
 template <int PER>
-__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
-                                                                  int topk, int32_t* __restrict__ sel,
-                                                                  float* __restrict__ w) {
-    const int lane = threadIdx.x & 63, t = blockIdx.x * (kRouteThreads / 64) + (threadIdx.x >> 6);
-    if (t >= T) return;
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, int t, int E, int topk, int32_t* sel,
+                                            float* w) {
+    const int lane = threadIdx.x & 63;
     float v[PER];
     const float* l = logits + (size_t)t * E;
 #pragma unroll
@@ -121,9 +120,18 @@ __global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* _
     float tot = 0.f;
     for (int k = 0; k < topk; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
     if (lane < topk) {
-        sel[(size_t)t * topk + lane] = myi;
-        w[(size_t)t * topk + lane] = ex / tot;
+        sel[lane] = myi;
+        w[lane] = ex / tot;
     }
+}
+
+template <int PER>
+__global__ void __launch_bounds__(kRouteThreads) moe_route_kernel(const float* __restrict__ logits, int T, int E,
+                                                                  int topk, int32_t* __restrict__ sel,
+                                                                  float* __restrict__ w) {
+    const int t = blockIdx.x * (kRouteThreads / 64) + (threadIdx.x >> 6);
+    if (t >= T) return;
+    route_token<PER>(logits, t, E, topk, sel + (size_t)t * topk, w + (size_t)t * topk);
 }
 
 void launch_route(const float* logits, int T, int E, int topk, int32_t* sel, float* w, hipStream_t st) {
@@ -243,6 +251,48 @@ __global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t*
         for (int e2 = tid; e2 < E; e2 += kSegThreads) fill[e2] += __popcll(mark[e2]);
         __syncthreads();
     }
+}
+
+// Decode batches (T <= kDecTokens): route and segment in one block. The 16 waves route tokens w, w + 16 into LDS, then
+// the block segments them as moe_segment_kernel does (same slots, jobs and offsets).
+constexpr int kDecTokens = 32;
+template <int PER>
+__global__ void __launch_bounds__(kSegThreads) moe_route_segment_kernel(const float* __restrict__ logits, int T, int E,
+                                                                        int topk, int chunk, int32_t* __restrict__ off,
+                                                                        int32_t* __restrict__ slot_pair,
+                                                                        int32_t* __restrict__ slot_tok,
+                                                                        float* __restrict__ slot_w,
+                                                                        int32_t* __restrict__ inv,
+                                                                        int32_t* __restrict__ jobs,
+                                                                        int32_t* __restrict__ njobs) {
+    __shared__ int32_t ssel[kDecTokens * 16];
+    __shared__ float sw[kDecTokens * 16];
+    __shared__ int cnt[kMaxExperts], pre[kMaxExperts + 1];
+    __shared__ unsigned long long mark[kMaxExperts];
+    const int tid = threadIdx.x, wv = tid >> 6;
+    for (int t = wv; t < T; t += kSegThreads / 64) route_token<PER>(logits, t, E, topk, ssel + t * topk, sw + t * topk);
+    for (int e = tid; e < E; e += kSegThreads) cnt[e] = 0;
+    __syncthreads();
+    for (int i = tid; i < T * topk; i += kSegThreads) atomicAdd(&cnt[ssel[i]], 1);
+    __syncthreads();
+    seg_scan_jobs(cnt, pre, E, chunk, off, jobs, njobs);
+    seg_place_chunk(ssel, sw, T, E, topk, 0, pre, mark, slot_pair, slot_tok, slot_w, inv);  // one chunk: T <= 64
+}
+
+void launch_route_segment(const float* logits, int T, int E, int topk, int chunk, int32_t* off, int32_t* slot_pair,
+                          int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs, int32_t* njobs,
+                          hipStream_t st) {
+    const int per = (E + 63) / 64;
+#define QE_RS(PER_)                                                                                              \
+    moe_route_segment_kernel<PER_><<<1, kSegThreads, 0, st>>>(logits, T, E, topk, chunk, off, slot_pair, slot_tok, \
+                                                             slot_w, inv, jobs, njobs)
+    if (per <= 1) QE_RS(1);
+    else if (per <= 2) QE_RS(2);
+    else if (per <= 4) QE_RS(4);
+    else if (per <= 8) QE_RS(8);
+    else QE_RS(16);
+#undef QE_RS
+    HIP_CHECK(hipGetLastError());
 }
 
 // above this many tokens the layer segments with the three-kernel path below (one block walks the chunks in turn)
@@ -423,7 +473,7 @@ MoeWs moe_ws(void* base, int T, int E, int topk, int H, int I) {
         return r;
     };
     const size_t P = (size_t)T * topk;
-    const int mj = max_jobs(T, E, topk, T <= 32 ? kDecRows : kMoePfRows);
+    const int mj = max_jobs(T, E, topk, T <= kDecTokens ? kDecRows : kMoePfRows);
     ws.sel = reinterpret_cast<int32_t*>(take(P * 4));
     ws.w = reinterpret_cast<float*>(take(P * 4));
     ws.off = reinterpret_cast<int32_t*>(take((size_t)(E + 1) * 4));
@@ -483,12 +533,15 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)workspace & 255) == 0,
           "moe x / out 16-byte, workspace 256-byte alignment");
     const char* recs = reinterpret_cast<const char*>(records);
-    const bool decode = T <= 32;
+    const bool decode = T <= kDecTokens;
     const int chunk = decode ? kDecRows : kMoePfRows;
     const int mj = max_jobs(T, E, topk, chunk);
 
-    launch_route(logits, T, E, topk, ws.sel, ws.w, st);
-    if (T > kSegOneBlockTokens) {
+    if (T > kDecTokens) launch_route(logits, T, E, topk, ws.sel, ws.w, st);
+    if (T <= kDecTokens) {
+        launch_route_segment(logits, T, E, topk, chunk, ws.off, ws.slot_pair, ws.slot_tok, ws.slot_w, ws.inv, ws.jobs,
+                             ws.njobs, st);
+    } else if (T > kSegOneBlockTokens) {
         const int nchunk = (T + kSegChunk - 1) / kSegChunk;
         moe_seg_count_kernel<<<nchunk, kSegThreads, 0, st>>>(ws.sel, T, E, topk, ws.cntb);
         HIP_CHECK(hipGetLastError());
