@@ -45,10 +45,14 @@ template <int MT, int NG>
 constexpr bool skinny_upx() {
     return MT <= 4 && NG > 0;
 }
+// staged activation rows (one row = one activation row's 64 dwords of a group) are kXStride dwords apart: the B
+// operand reads of 8 consecutive lanes (8 rows, same offset in the row) then hit 8 disjoint groups of 4 banks; with
+// 64 they all hit the same banks (an 8-way conflict per read at MT >= 8)
+constexpr int kXStride = 68;
 template <int MT, int NG>
-constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][64], scales [NGM][16] half
+constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][kXStride], scales [NGM][16] half
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
-    return (skinny_upx<MT, NG>() ? NGM : 2) * MT * 64 + NGM * 8;
+    return (skinny_upx<MT, NG>() ? NGM : 2) * MT * kXStride + NGM * 8;
 }
 
 template <int MT, int SDT, int NG, int D>
@@ -95,7 +99,7 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
             if (MT >= 4 || (L >> 4) < MT) {
 #pragma unroll
                 for (int c = 0; c < 4; c++)
-                    xl[(buf * MT + (L >> 4) + 4 * e) * 64 + x_slot<kFmtW4>(4 * (L & 15) + c)] = src[e][c];
+                    xl[(buf * MT + (L >> 4) + 4 * e) * kXStride + x_slot<kFmtW4>(4 * (L & 15) + c)] = src[e][c];
             }
     };
 
@@ -133,7 +137,7 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
             for (int tok = 0; tok < MT; tok++)
 #pragma unroll
                 for (int e = 0; e < 8; e++)
-                    xl[((L >> 3) * MT + tok) * 64 + x_slot<kFmtW4>(8 * (L & 7) + e)] = xv[tok][e >> 2][e & 3];
+                    xl[((L >> 3) * MT + tok) * kXStride + x_slot<kFmtW4>(8 * (L & 7) + e)] = xv[tok][e >> 2][e & 3];
         }
     } else {
 #pragma unroll
@@ -173,7 +177,7 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
             const u32x4_v rec = mm < 2 ? r0 : r1;
             u32x4_v b = {0u, 0u, 0u, 0u};
             if (MT == 16 || i < MT)
-                b = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + (i < MT ? i : 0)) * 64 + (4 * (mm >> 1) + qg) * 8 + 2 * j0]);
+                b = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + (i < MT ? i : 0)) * kXStride + (4 * (mm >> 1) + qg) * 8 + 2 * j0]);
             const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
             const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
             const u32x4_v a = {bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
