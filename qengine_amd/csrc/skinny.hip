@@ -78,14 +78,16 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
     // Activation rows tok >= m (up to MT) load row m - 1 instead: no load sits under a branch, and those MFMA
     // columns are never stored (columns are independent).
     const size_t xs = (size_t)(ldx >> 1);  // dwords per activation row
-    // !UPX: a group's activations are MT rows x 16 pieces of 16 bytes; lane L loads pieces L + 64 e, i.e. piece
-    // L % 16 of row L / 16 + 4 e, and stages its 4 dwords at their class-major positions (MT < 4: lanes of rows
-    // past MT load a duplicate and stage nothing)
+    // !UPX: a group's activations are MT rows x 16 pieces of 16 bytes; lane L loads piece L % 16 of row xrow_of(e)
+    // and stages its 4 dwords at their class-major positions (MT < 4: lanes of rows past MT load a duplicate and
+    // stage nothing). A staging store covers 4 rows of 8 consecutive dwords (+32): MT >= 8 takes rows 2 apart
+    // (2 x kXStride = 8 banks mod 64, so the 4 rows' spans are disjoint); rows 1 apart would overlap by 4 banks.
     constexpr int XP = MT >= 4 ? MT / 4 : 1;
+    auto xrow_of = [&](int e) { return MT >= 8 ? (e & 1) + 2 * (L >> 4) + 8 * (e >> 1) : (L >> 4) + 4 * e; };
     const u32x4_v* xq[XP];
 #pragma unroll
     for (int e = 0; e < XP; e++) {
-        const int tp = (L >> 4) + 4 * e;
+        const int tp = xrow_of(e);
         xq[e] = reinterpret_cast<const u32x4_v*>(reinterpret_cast<const uint32_t*>(x) + (size_t)(tp < m ? tp : m - 1) * xs +
                                                  (size_t)gb * 64) + (L & 15);
     }
@@ -99,7 +101,7 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
             if (MT >= 4 || (L >> 4) < MT) {
 #pragma unroll
                 for (int c = 0; c < 4; c++)
-                    xl[(buf * MT + (L >> 4) + 4 * e) * kXStride + x_slot<kFmtW4>(4 * (L & 15) + c)] = src[e][c];
+                    xl[(buf * MT + xrow_of(e)) * kXStride + x_slot<kFmtW4>(4 * (L & 15) + c)] = src[e][c];
             }
     };
 
