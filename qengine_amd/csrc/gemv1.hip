@@ -39,12 +39,14 @@ template <int NG>
 constexpr int stage_groups() {
     return (NG * 8 + 63) / 64 * 8;
 }
-// LDS per wave (dwords): xl [GP][64] activations class-major, zero [GP][8] (the B operand of lanes off the
-// diagonal), xsum [GP][8] (-136 x class sums), scales [GP][8] pairs (s[g], s[g + 8]) of 16-bit values, GP =
-// stage_groups; then red [S][16] floats for the block
+// LDS per wave (dwords): xl [GP][kGStride] activations class-major (64 dwords of a group, kGStride apart: with 64
+// the 8 groups a staging store covers hit the same banks, an 8-way conflict; with 68 they are 4 banks apart),
+// zero [GP][8] (the B operand of lanes off the diagonal), xsum [GP][8] (-136 x class sums), scales [GP][8] pairs
+// (s[g], s[g + 8]) of 16-bit values, GP = stage_groups; then red [S][16] floats for the block
+constexpr int kGStride = 68;
 template <int NG>
 constexpr int wave_dwords() {
-    return stage_groups<NG>() * (64 + 8 + 8 + 8);
+    return stage_groups<NG>() * (kGStride + 8 + 8 + 8);
 }
 
 // NG groups per wave (K slice), D weight records in flight per lane (D < NG: a sliding window, the load of group
@@ -61,8 +63,8 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
     const int tile = blockIdx.x, G = K >> 7, gb = w * NG;
-    uint32_t* xl = lds + (size_t)w * WSZ;                          // [GP][64]
-    uint32_t* zr = xl + GP * 64;                                     // [GP][8] zeros
+    uint32_t* xl = lds + (size_t)w * WSZ;                          // [GP][kGStride]
+    uint32_t* zr = xl + GP * kGStride;                               // [GP][8] zeros
     float* xsum = reinterpret_cast<float*>(zr + GP * 8);             // [GP][8]
     uint16_t* sl16 = reinterpret_cast<uint16_t*>(xsum + GP * 8);     // [GP][8][2]: (s[g], s[g + 8])
     float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][16]
@@ -100,7 +102,7 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
             sl16[(gi * 8 + (row & 7)) * 2 + (row >> 3)] = (uint16_t)(sraw[r] >> (16 * e));
         }
 #pragma unroll
-        for (int e = 0; e < 8; e++) xl[gi * 64 + x_slot<kFmtW4>(8 * l8 + e)] = e < 4 ? xv[r][0][e] : xv[r][1][e - 4];
+        for (int e = 0; e < 8; e++) xl[gi * kGStride + x_slot<kFmtW4>(8 * l8 + e)] = e < 4 ? xv[r][0][e] : xv[r][1][e - 4];
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -108,7 +110,7 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
 #pragma unroll
     for (int r = 0; r < NR; r++) {
         const int p = L + 64 * r;
-        const u32x4_v* cl = reinterpret_cast<const u32x4_v*>(&xl[(p >> 3) * 64 + (p & 7) * 8]);
+        const u32x4_v* cl = reinterpret_cast<const u32x4_v*>(&xl[(p >> 3) * kGStride + (p & 7) * 8]);
         const u32x4_v a0 = cl[0], a1 = cl[1];
         float sm = 0.f;
 #pragma unroll
@@ -125,10 +127,10 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     const int qb = L >> 4, c = L & 15;
     const bool diag = (c >> 2) == qb;
     // B operand: class 4 (q / 2) + c % 4 of the staged activations on the diagonal, else 8 zeros; group i is
-    // 64 dwords further for the diagonal lanes, 8 for the others (no branch in the loop: a branch per group would
+    // kGStride dwords further for the diagonal lanes, 8 for the others (no branch in the loop: a branch per group would
     // let the compiler sink every group's FMAs to the end and keep all D results live)
     const uint32_t* bb = diag ? &xl[(4 * (qb >> 1) + (c & 3)) * 8] : zr;
-    const int bstep = diag ? 64 : 8;
+    const int bstep = diag ? kGStride : 8;
     const float* cb = &xsum[4 * (c >> 3)];  // class sums of classes 4 (c / 8) .. + 3 (register r <-> t = r)
     const int grow = 4 * ((c >> 2) & 1) + qb;  // row (low nibbles) of the lane's useful D entry
     f32x4_v acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
