@@ -91,9 +91,12 @@ __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
 // !PF: loaded when the group is reached (large m).
 // LDS (`lds`): per wave xl [XG][MT][64] u32 + xsum [XG][MT][8] + the slice's scales [NGM][16] half, then red
 // (XG = NG groups when PF with even slices, else 1).
+// qgs / sgs: uint4 / scale dwords from one group of the slice to the next (default: the W4 / W8 layouts, groups
+// adjacent; the MoE down GEMV passes the record size, its K groups are in consecutive records).
 template <int MT, int FMT, int SDT, int NG, bool PF>
 __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restrict__ qp, const uint16_t* __restrict__ sp,
-                                            const uint32_t* const* xw, int m, int ng, int sdt) {
+                                            const uint32_t* const* xw, int m, int ng, int sdt, size_t qgs = 64 * (FMT == kFmtW4 ? 1 : 2),
+                                            size_t sgs = 8) {
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
     constexpr int LPG = FMT == kFmtW4 ? 1 : 2;  // wave-loads per group
     // UP: every group's activations are loaded before the weights and staged while the weights are in flight,
@@ -137,12 +140,13 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
             xv[tok][1] = src[1];
         }
     }
-    const uint32_t sraw = reinterpret_cast<const uint32_t*>(sp)[L < ndw ? L : ndw - 1];
+    const int ls = L < ndw ? L : ndw - 1;
+    const uint32_t sraw = reinterpret_cast<const uint32_t*>(sp)[(size_t)(ls >> 3) * sgs + (ls & 7)];
 #pragma unroll
     for (int i = 0; i < NGM; i++) {
         if (NG == 0 && i >= ng) break;
 #pragma unroll
-        for (int e = 0; e < LPG; e++) wv[i][e] = ld_stream(qp + (size_t)(i * LPG + e) * 64);
+        for (int e = 0; e < LPG; e++) wv[i][e] = ld_stream(qp + (size_t)i * qgs + (size_t)e * 64);
         if constexpr (PF && !UP) {
 #pragma unroll
             for (int tok = 0; tok < MT; tok++) xr[tok][i] = xw[tok][i * 64 + xoff];

@@ -386,9 +386,10 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
     }
 }
 
-// down: block (job, 16-row tile of H); wave g = record g (K = 128 each)
-template <int MT>
-__global__ void __launch_bounds__(64 * kMaxWavesGeneric) moe_dec_down_kernel(
+// down: block = one wave = (job, 16-row tile of H), all NGRP records of the expert (K = I = 128 per record): the
+// wave streams NGRP KB and no K slice is reduced across waves
+template <int MT, int NGRP>
+__global__ void __launch_bounds__(64) moe_dec_down_kernel(
     const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ act, const int32_t* __restrict__ off,
     const int32_t* __restrict__ jobs, const int32_t* __restrict__ njobs, uint16_t* __restrict__ slot_out) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
@@ -397,18 +398,18 @@ __global__ void __launch_bounds__(64 * kMaxWavesGeneric) moe_dec_down_kernel(
     const int e = jobs[2 * job], r0 = jobs[2 * job + 1];
     const int slot0 = off[e] + r0, m = min(MT, off[e + 1] - slot0);
     const int tile = blockIdx.y;
-    const int S = blockDim.x >> 6, g = threadIdx.x >> 6;
-    const char* rp = rec_ptr(recs, sh, e, g);
+    const char* rp = rec_ptr(recs, sh, e, 0);
     const uint4* qp = reinterpret_cast<const uint4*>(rp + sh.gg_q + sh.gg_s) + (size_t)tile * 2 * 32;
     const uint16_t* sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q) + (size_t)tile * 16;
     const uint32_t* xw[MT];
 #pragma unroll
     for (int r = 0; r < MT; r++)
-        xw[r] = reinterpret_cast<const uint32_t*>(act + (size_t)(slot0 + (r < m ? r : 0)) * sh.I) + g * 64;
-    const float* red = gemv_tile<MT, kFmtW4, kScaleF16, 1, true>(lds, qp, sp, xw, m, 1, kScaleF16);
+        xw[r] = reinterpret_cast<const uint32_t*>(act + (size_t)(slot0 + (r < m ? r : 0)) * sh.I);
+    const float* red = gemv_tile<MT, kFmtW4, kScaleF16, NGRP, true>(lds, qp, sp, xw, m, NGRP, kScaleF16, sh.rec / 16,
+                                                                    sh.rec / 4);
     for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
         const int r = idx >> 4, rr = idx & 15;
-        slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_bf16(rsum<MT>(red, S, r, rr));
+        slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_bf16(rsum<MT>(red, 1, r, rr));
     }
 }
 
@@ -493,8 +494,8 @@ MoeWs moe_ws(void* base, int T, int E, int topk, int H, int I) {
 void moe_check(int T, int E, int topk, int H, int I) {
     CHECK(T >= 1 && E >= 1 && E <= kMaxExperts && topk >= 1 && topk <= 16 && topk <= E, "moe T %d E %d topk %d", T, E,
           topk);
-    CHECK(H % 512 == 0 && H / 128 <= 4 * kMaxWaves && I % 128 == 0 && I / 128 <= kMaxWavesGeneric, "moe H %d I %d", H,
-          I);
+    CHECK(H % 512 == 0 && H / 128 <= 4 * kMaxWaves && I % 128 == 0 && (I / 128 <= 8 || I / 128 == 16), "moe H %d I %d",
+          H, I);
 }
 
 }  // namespace
@@ -566,8 +567,22 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
             moe_dec_gate_up_kernel<kDecRows, 8><<<dim3(mj, sh.ngrp * 16), 64 * (G / 8), lds_gu, st>>>(
                 recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
         HIP_CHECK(hipGetLastError());
-        moe_dec_down_kernel<kDecRows><<<dim3(mj, H / 16), 64 * sh.ngrp, gemv_lds_bytes<kDecRows, 1, true>(sh.ngrp), st>>>(
-            recs, sh, ws.act, ws.off, ws.jobs, ws.njobs, ws.slot_out);
+#define QE_DOWN(NGRP_)                                                                                         \
+    moe_dec_down_kernel<kDecRows, NGRP_><<<dim3(mj, H / 16), 64, gemv_lds_bytes<kDecRows, NGRP_, true>(1), st>>>( \
+        recs, sh, ws.act, ws.off, ws.jobs, ws.njobs, ws.slot_out)
+        switch (sh.ngrp) {
+            case 1: QE_DOWN(1); break;
+            case 2: QE_DOWN(2); break;
+            case 3: QE_DOWN(3); break;
+            case 4: QE_DOWN(4); break;
+            case 5: QE_DOWN(5); break;
+            case 6: QE_DOWN(6); break;
+            case 7: QE_DOWN(7); break;
+            case 8: QE_DOWN(8); break;
+            case 16: QE_DOWN(16); break;
+            default: CHECK(false, "moe decode: I = %d (I / 128 in 1..8 or 16)", I);
+        }
+#undef QE_DOWN
         HIP_CHECK(hipGetLastError());
     } else {
         MoePfArgs pa;
