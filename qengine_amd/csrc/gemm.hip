@@ -248,6 +248,13 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[a][bb][r] = 0.f;
 
+    // MoE jobs: 32-row MFMA tiles of this wave that hold a row of the job (bit a); the others skip their fragment
+    // reads and MFMAs (their outputs are not stored). Wave-uniform.
+    const unsigned alive = __builtin_amdgcn_readfirstlane(MODE == 0 ? ~0u : [&] {
+        unsigned mk = 0;
+        for (int a = 0; a < WMT; a++) mk |= (wm * 32 * WMT + a * 32 < T ? 1u : 0u) << a;
+        return mk;
+    }());
     // one k step: MFMAs on stage kt % 2 while the next step's tiles go into the other stage
     int lane_off[BK / 16];  // swz(l % 32, 2 ks + l / 32) of this lane
 #pragma unroll
@@ -264,7 +271,8 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             const char* wl = wt + lane_off[ks];
 #pragma unroll
             for (int a = 0; a < WMT; a++)
-                af[buf][a] = *reinterpret_cast<const bf16x8_v*>(xl + (wm * 32 * WMT + a * 32) * 128);
+                if (MODE == 0 || (alive >> a) & 1)
+                    af[buf][a] = *reinterpret_cast<const bf16x8_v*>(xl + (wm * 32 * WMT + a * 32) * 128);
 #pragma unroll
             for (int bb = 0; bb < WNT; bb++)
                 bfr[buf][bb] = *reinterpret_cast<const bf16x8_v*>(wl + (wn * 32 * WNT + bb * 32) * 128);
@@ -277,7 +285,8 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             for (int a = 0; a < WMT; a++)
 #pragma unroll
                 for (int bb = 0; bb < WNT; bb++)
-                    acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][a], bfr[ks & 1][bb], acc[a][bb], 0, 0, 0);
+                    if (MODE == 0 || (alive >> a) & 1)
+                        acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][a], bfr[ks & 1][bb], acc[a][bb], 0, 0, 0);
             store_part(ks);
         }
     };
