@@ -7,10 +7,12 @@
 //          block tile BM = 64 WMT tokens x BN = 128 WNT rows, BK = 64 (one W4 chunk)
 //   LDS: two stages of X [BM][64] and W [BN][64] bf16, rows of 128 B with the 16-byte chunks XOR-swizzled by
 //        (row % 8) so the MFMA fragment reads (32 rows x 16 B per half-wave) spread over the banks
-//   pipeline, per k step: the MFMAs of step k read stage k % 2 while the same waves dequantize and store step k + 1
-//        (loaded during step k - 1) into the other stage; then the global loads of step k + 2 are issued and one
-//        barrier closes the step. The VALU dequantization overlaps the matrix pipe; the global loads get a step
-//        of MFMA time to arrive.
+//   pipeline, per k step: the MFMAs of step k read stage k % 2 while the same waves dequantize step k + 1 into the
+//        other stage; the activations of step k + 1 arrive there by LDS DMA issued at the top of step k. INT4: the
+//        raw records of step k + 2 are DMA'd to LDS at the top of step k and dequantized from LDS a step later.
+//        INT8: the records go through two register sets, loaded at the top of step k for step k + 2. Every step
+//        ends with vmcnt(0), lgkmcnt(0) and one barrier: each load gets a step of MFMA time to arrive, and the VALU
+//        dequantization overlaps the matrix pipe.
 //   grid: one block per output tile, tiles ordered so that the 8 XCDs (blockIdx % 8) each sweep a contiguous band
 //        of tiles (their L2 keeps the shared X / W tiles).
 #include "mfma_tile.hpp"
@@ -27,7 +29,6 @@ template <int WMT, int WNT>
 struct Cfg {
     static constexpr int BM = 64 * WMT, BN = 128 * WNT;
     static constexpr int kStage = (BM + BN) * BK * 2;
-    static constexpr int XLD = BM * 8 / NTH;     // 16-byte X loads per thread and step (INT8 path)
     static constexpr int XDMA = BM / 64;         // 1 KB X DMA loads per wave and step (INT4 path)
     // INT4 path: raw W records of one k step (BN / 16 tiles x 512 B) and the scales of one group (BN / 16 x 32 B),
     // both double-buffered after the two stages
@@ -94,7 +95,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     }
     const int G = K >> 7, KT = K / BK;
 
-    // ---- X, INT4 path: LDS DMA (global_load_lds_dwordx4), 1 KB = 8 rows per wave instruction. Lane i lands at
+    // ---- X (every format): LDS DMA (global_load_lds_dwordx4), 1 KB = 8 rows per wave instruction. Lane i lands at
     //      LDS slot i of the 8-row block, so it loads the chunk that the swizzle puts there. Rows past T re-read
     //      row T - 1 (their outputs are not stored).
     // (MoE: the gathered row of each of this lane's DMA rows, fixed for the block)
@@ -120,22 +121,6 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             }
         }
     };
-    // ---- X, INT8 path: XLD x 16 B per thread through registers (row = idx / 8, chunk = idx % 8)
-    u32x4_v xr[W4 ? 1 : C::XLD];
-    auto load_x = [&](int kt) {
-#pragma unroll
-        for (int i = 0; i < C::XLD; i++) {
-            const int idx = tid + i * NTH, r = idx >> 3, ch = idx & 7;
-            const int tok = t0 + r;
-            xr[i] = tok < T ? *reinterpret_cast<const u32x4_v*>(x + (size_t)tok * ldx + kt * BK + ch * 8)
-                            : u32x4_v{0u, 0u, 0u, 0u};
-        }
-    };
-    auto store_x = [&](char* xt, int i) {
-        const int idx = tid + i * NTH, r = idx >> 3, ch = idx & 7;
-        *reinterpret_cast<u32x4_v*>(xt + swz(r, ch)) = xr[i];
-    };
-
     // ---- W, INT4 path. Raw records go to LDS by DMA: a 1 KB wave load covers two 16-row tiles; lane i holds record
     //      (tile 2 u + (i / 8) % 2, g = i % 8, t = i / 16), so that a job's reads below hit 64 distinct banks. A job =
     //      k step j (16 k) of the row pair (g, g + 8) of a tile: word j of the tile's 4 records (g, t = 0..3) ->
@@ -197,13 +182,16 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     constexpr int NREC = (BN / 16) * 64;
     constexpr int WREC = NREC >= NTH ? NREC / NTH : 1;
     const bool wactive = tid < NREC;
-    u32x4_v wr[W4 ? 1 : WREC];
-    uint16_t sr_lo[W4 ? 1 : WREC], sr_hi[W4 ? 1 : WREC];
+    struct WSet {
+        u32x4_v wr[W4 ? 1 : WREC];
+        uint16_t sr_lo[W4 ? 1 : WREC], sr_hi[W4 ? 1 : WREC];
+    };
+    WSet wsA, wsB;
     auto rec_of = [&](int e, int& tr, int& slab, int& wl) {
         const int r = tid + e * NTH;
         tr = r >> 6, slab = (r >> 5) & 1, wl = r & 31;
     };
-    auto load_w8 = [&](int kt) {
+    auto load_w8 = [&](WSet& ws, int kt) {
 #pragma unroll
         for (int e = 0; e < WREC; e++) {
             int tr, slab, wl;
@@ -211,30 +199,30 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             const size_t tl = (size_t)(n0 >> 4) + tr;
             const bool v = wactive && n0 + tr * 16 < N;
             const uint4* p = q + (tl * (K >> 5) + 2 * kt + slab) * 32 + wl;
-            wr[e] = v ? __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p)) : u32x4_v{0u, 0u, 0u, 0u};
+            ws.wr[e] = v ? __builtin_nontemporal_load(reinterpret_cast<const u32x4_v*>(p)) : u32x4_v{0u, 0u, 0u, 0u};
             const int wg = wl >> 2;
             if (FMT == kFmtW8C) {
-                sr_lo[e] = v ? s[n0 + tr * 16 + wg] : 0;
-                sr_hi[e] = v ? s[n0 + tr * 16 + wg + 8] : 0;
+                ws.sr_lo[e] = v ? s[n0 + tr * 16 + wg] : 0;
+                ws.sr_hi[e] = v ? s[n0 + tr * 16 + wg + 8] : 0;
             } else {
                 const uint16_t* sp = s + (tl * G + (kt >> 1)) * 16;
-                sr_lo[e] = v ? sp[wg] : 0;
-                sr_hi[e] = v ? sp[wg + 8] : 0;
+                ws.sr_lo[e] = v ? sp[wg] : 0;
+                ws.sr_hi[e] = v ? sp[wg + 8] : 0;
             }
         }
     };
-    auto store_w8 = [&](char* wtile, int d) {  // dword d (0..3) of every record of this thread
+    auto store_w8 = [&](const WSet& ws, char* wtile, int d) {  // dword d (0..3) of every record of this thread
         if (!wactive) return;
 #pragma unroll
         for (int e = 0; e < WREC; e++) {
             int tr, slab, wl;
             rec_of(e, tr, slab, wl);
             const int wrow = tr * 16 + (wl >> 2), wt4 = wl & 3;
-            const float s_lo = scale_rt<SDT>(sr_lo[e], sdt), s_hi = scale_rt<SDT>(sr_hi[e], sdt);
+            const float s_lo = scale_rt<SDT>(ws.sr_lo[e], sdt), s_hi = scale_rt<SDT>(ws.sr_hi[e], sdt);
             if constexpr (FMT == kFmtQ8)  // word d = 2 s + hi: row + 8 hi, k 32 slab + 16 s + 2 t (+1, +8, +9)
-                dq_q8_word(wr[e][d], (d & 1) ? s_hi : s_lo, wtile, wrow + 8 * (d & 1), 32 * slab + 16 * (d >> 1) + 2 * wt4);
+                dq_q8_word(ws.wr[e][d], (d & 1) ? s_hi : s_lo, wtile, wrow + 8 * (d & 1), 32 * slab + 16 * (d >> 1) + 2 * wt4);
             else  // slab covers k 32 slab .. + 31; dword d: k step d / 2, half d % 2
-                dq_w8_dword(wr[e][d], s_lo, s_hi, wtile, wrow, 32 * slab + 16 * (d >> 1) + 8 * (d & 1) + 2 * wt4);
+                dq_w8_dword(ws.wr[e][d], s_lo, s_hi, wtile, wrow, 32 * slab + 16 * (d >> 1) + 8 * (d & 1) + 2 * wt4);
         }
     };
 
@@ -324,32 +312,29 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         }
     } else {
-        load_x(0);
-        load_w8(0);
+        // X by LDS DMA (as the INT4 path), INT8 records through two register sets: step kt issues the DMA of X
+        // (kt + 1) and the record loads of kt + 2 at its top, dequantizes the records of kt + 1 (loaded one step
+        // earlier) into the other stage during its MFMAs, and ends with vmcnt(0) + the barrier.
+        dma_x(0, 0);
+        load_w8(wsA, 0);
+        if (KT > 1) load_w8(wsB, 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int i = 0; i < C::XLD; i++) store_x(lds, i);
-#pragma unroll
-        for (int d = 0; d < 4; d++) store_w8(lds + BM * BK * 2, d);
-        if (KT > 1) {
-            load_x(1);
-            load_w8(1);
-        }
-        __syncthreads();
-        for (int kt = 0; kt < KT; kt++) {
+        for (int d = 0; d < 4; d++) store_w8(wsA, lds + BM * BK * 2, d);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        auto step = [&](int kt, const WSet& cur, WSet& nxt_regs) {
             char* nxt = lds + ((kt + 1) & 1) * C::kStage;
+            if (kt + 1 < KT) dma_x(kt + 1, ((kt + 1) & 1) * C::kStage);
             const bool more = kt + 1 < KT;
             mfma_step(kt, [&](int ks) {
-                if (!more) return;
-                store_w8(nxt + BM * BK * 2, ks);
-#pragma unroll
-                for (int i = 0; i < C::XLD; i++)
-                    if ((i & 3) == ks) store_x(nxt, i);
+                if (more) store_w8(cur, nxt + BM * BK * 2, ks);
+                if (ks == 0 && kt + 2 < KT) load_w8(nxt_regs, kt + 2);  // after the first stores free no registers
             });
-            if (kt + 2 < KT) {
-                load_x(kt + 2);
-                load_w8(kt + 2);
-            }
-            __syncthreads();
+            asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        };
+        for (int kt = 0; kt < KT; kt += 2) {
+            step(kt, wsB, wsA);
+            if (kt + 1 < KT) step(kt + 1, wsA, wsB);
         }
     }
 
