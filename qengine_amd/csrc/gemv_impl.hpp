@@ -140,8 +140,14 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
             xv[tok][1] = src[1];
         }
     }
-    const int ls = L < ndw ? L : ndw - 1;
-    const uint32_t sraw = reinterpret_cast<const uint32_t*>(sp)[(size_t)(ls >> 3) * sgs + (ls & 7)];
+    // scale dword p = L + 64 r (slices of more than 8 groups take two rounds)
+    constexpr int SPR = FMT == kFmtW8C ? 1 : (NGM * 8 + 63) / 64;
+    uint32_t sraw[SPR];
+#pragma unroll
+    for (int r = 0; r < SPR; r++) {
+        const int ls = L + 64 * r < ndw ? L + 64 * r : ndw - 1;
+        sraw[r] = reinterpret_cast<const uint32_t*>(sp)[(size_t)(ls >> 3) * sgs + (ls & 7)];
+    }
 #pragma unroll
     for (int i = 0; i < NGM; i++) {
         if (NG == 0 && i >= ng) break;
@@ -153,7 +159,9 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
         }
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (L < ndw) reinterpret_cast<uint32_t*>(sl16)[L] = sraw;
+#pragma unroll
+    for (int r = 0; r < SPR; r++)
+        if (L + 64 * r < ndw) reinterpret_cast<uint32_t*>(sl16)[L + 64 * r] = sraw[r];
 
     // 2. per group: stage x (class-major, class sums times the bias), then the dot products
     constexpr float bias = FMT == kFmtW4 ? 136.f : 128.f;

@@ -19,22 +19,35 @@
 //   * The bias 136 (u = w + 8 over the 128 of the magic) is removed by one more MFMA per k step with A = -136:
 //     C = sum (128 + u) x - 136 sum x = sum (u - 8) x, all products exact in fp32. The group scale is applied
 //     once per group: acc += s * C.
+//   * A wave computes RT = 2 tiles (16-row tiles 2 b, 2 b + 1 of block b) where that pays: one activation load,
+//     staging and B operand read serve both tiles' MFMAs.
 //   * K slices per block are those of the m = 1 matrix-core kernel (decode_groups; gemv_slicing's uneven slices
 //     where no even slicing fits) and the fixed-order LDS reduction makes the result deterministic; an activation
 //     row's result does not depend on the other rows (MFMA columns are independent, the slicing depends on (n, k)
-//     only).
+//     only, the tiles per wave do not change any tile's sums).
 #include "gemv_impl.hpp"
 
 namespace qe_skinny {
 using namespace qe_gemv;
 
-// weight groups in flight per wave (with the activations of each group in the window for MT >= 8). Measured on the
-// BASELINE shapes with 5-group slices: 3 for every MT but 8, where 2 keeps the kernel at 6 waves per SIMD (deeper
-// windows cost more in occupancy than they gain in latency)
+// Tiles per wave RT: the weight tiles of RT consecutive 16-row tiles share one wave's staged activations and B
+// operand reads (the activation traffic per tile halves at RT = 2). Even slices can take RT = 2 (the host picks it
+// in launch()); uneven slices (NG = 0) take RT = 1. Weight groups in flight per wave D and the occupancy hint
+// WPE, measured on the BASELINE shapes (K = 5120, 5-group slices; N = 5120 and 17408):
+//   RT = 2: D = 2 on slices of <= 5 groups (WPE 4: <= 128 VGPRs), else D = 3 (MT = 8: 2)
+//   RT = 1: D = 3 (MT = 8: 2, 6 waves per SIMD), WPE 6 at MT <= 4 on even slices of <= 5 groups
 template <int MT, int NG>
+constexpr int skinny_rt() {
+    return NG == 0 ? 1 : 2;
+}
+template <int MT, int NG, int RT>
 constexpr int skinny_d() {
-    constexpr int d = MT == 8 ? 2 : 3;
+    constexpr int d = MT == 8 || (RT == 2 && NG > 0 && NG <= 5) ? 2 : 3;
     return NG > 0 && NG < d ? NG : d;
+}
+template <int MT, int NG, int RT>
+constexpr int skinny_wpe() {  // minimum waves per SIMD asked of the register allocator
+    return RT == 2 ? (NG <= 5 ? 4 : 1) : (MT <= 4 && NG > 0 && NG <= 5 ? 6 : 1);
 }
 
 // UPX (MT <= 4 with even slices): every group's activations are loaded before the weights and staged in LDS
@@ -43,34 +56,34 @@ constexpr int skinny_d() {
 // through a window of D groups.
 template <int MT, int NG>
 constexpr bool skinny_upx() {
-    return MT <= 4 && NG > 0;
+    return MT <= 4 && NG > 0 && NG <= 8;
 }
 // staged activation rows (one row = one activation row's 64 dwords of a group) are kXStride dwords apart: the B
 // operand reads of 8 consecutive lanes (8 rows, same offset in the row) then hit 8 disjoint groups of 4 banks; with
 // 64 they all hit the same banks (an 8-way conflict per read at MT >= 8)
 constexpr int kXStride = 68;
-template <int MT, int NG>
-constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][kXStride], scales [NGM][16] half
+template <int MT, int NG, int RT>
+constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][kXStride], scales [RT][NGM][16] half
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
-    return (skinny_upx<MT, NG>() ? NGM : 2) * MT * kXStride + NGM * 8;
+    return (skinny_upx<MT, NG>() ? NGM : 2) * MT * kXStride + RT * NGM * 8;
 }
 
-template <int MT, int SDT, int NG, int D>
+template <int MT, int SDT, int NG, int RT, int D = skinny_d<MT, NG, RT>(), int WPE = skinny_wpe<MT, NG, RT>()>
 __global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
-__attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
+__attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K, const uint16_t* __restrict__ x,
     int ldx, void* __restrict__ y, int ldy, int m, int out, int sdt) {
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
     constexpr bool UPX = skinny_upx<MT, NG>();
-    constexpr int WSZ = skinny_wsz<MT, NG>();
+    constexpr int WSZ = skinny_wsz<MT, NG, RT>();
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
-    const int tile = blockIdx.x, G = K >> 7;
+    const int tile0 = blockIdx.x * RT, G = K >> 7;
     const int gb = NG > 0 ? w * NG : w * G / S;
     const int ng = NG > 0 ? NG : (w + 1) * G / S - gb;
     uint32_t* xl = lds + (size_t)w * WSZ;
-    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + (WSZ - NGM * 8));
-    float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][16 tok][16 rows]
+    uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + (WSZ - RT * NGM * 8));
+    float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][RT][16 tok][16 rows]
 
     const int qg = L >> 4, i = L & 15;  // operand lane group, row / column within the tile
     const int g = i & 7, sh = 4 * (i >> 3);
@@ -105,41 +118,56 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
             }
     };
 
-    // 1. loads in consumption order: the slice's scales (one dword per lane); UPX: every group's activations, then
-    //    the first D groups of weight records; else (x_j, w_j) pairs for the first D groups
-    {
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)tile * G + gb) * 16);
-        if (L < ng * 8) reinterpret_cast<uint32_t*>(sl16)[L] = sp[L];
+    // 1. loads in consumption order: the slice's scales (8 dwords per group, dword p on lane p % 64); UPX: every
+    //    group's activations, then the first D groups of weight records; else (x_j, w_j) pairs for the first D groups
+    constexpr int PR = (NGM * 8 + 63) / 64;  // rounds of 64 scale dwords / activation pieces (slices of > 8 groups)
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)(tile0 + r) * G + gb) * 16);
+#pragma unroll
+        for (int pr = 0; pr < PR; pr++)
+            if (L + 64 * pr < ng * 8) reinterpret_cast<uint32_t*>(sl16)[r * NGM * 8 + L + 64 * pr] = sp[L + 64 * pr];
     }
     u32x4_v xr[UPX ? 1 : D][XP];  // activation register slots (per-group staging)
-    const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + 4 * g + qg;
-    u32x4_v wv[D][2];
+    const uint4* qp = q + ((size_t)tile0 * (K >> 6) + 2 * gb) * 32 + 4 * g + qg;
+    const size_t qts = (size_t)(K >> 6) * 32;  // records per tile
+    u32x4_v wv[D][RT][2];
     auto ldw = [&](int slot, int ii) {
-        wv[slot][0] = ld_stream(qp + (size_t)ii * 64);
-        wv[slot][1] = ld_stream(qp + (size_t)ii * 64 + 32);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            wv[slot][r][0] = ld_stream(qp + r * qts + (size_t)ii * 64);
+            wv[slot][r][1] = ld_stream(qp + r * qts + (size_t)ii * 64 + 32);
+        }
     };
     if constexpr (UPX) {
-        // lane L loads dwords [8 L, 8 L + 8) of each row's slice (16-byte pieces; x and ldx are 16-byte aligned)
-        // and stores dword 8 (L % 8) + e of group L / 8 at its class-major position
+        // piece p = L + 64 pr: lane L loads dwords [8 p, 8 p + 8) of each row's slice (16-byte pieces; x and ldx
+        // are 16-byte aligned) and stores dword 8 (p % 8) + e of group p / 8 at its class-major position
         constexpr int XL = NGM * 8;
-        u32x4_v xv[MT][2];
+        u32x4_v xv[PR][MT][2];
         const uint32_t* xs0 = reinterpret_cast<const uint32_t*>(x) + (size_t)gb * 64;
-        const int lc = L < XL ? L : XL - 1;  // lanes past the slice reload its last piece (not staged)
 #pragma unroll
-        for (int tok = 0; tok < MT; tok++) {
-            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xs0 + (tok < m ? tok : m - 1) * xs) + 2 * lc;
-            xv[tok][0] = src[0];
-            xv[tok][1] = src[1];
+        for (int pr = 0; pr < PR; pr++) {
+            const int lc = L + 64 * pr < XL ? L + 64 * pr : XL - 1;  // lanes past the slice reload its last piece
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) {
+                const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xs0 + (tok < m ? tok : m - 1) * xs) + 2 * lc;
+                xv[pr][tok][0] = src[0];
+                xv[pr][tok][1] = src[1];
+            }
         }
 #pragma unroll
         for (int ii = 0; ii < D; ii++)
             if (ii < ng) ldw(ii, ii);
-        if (L < XL) {
 #pragma unroll
-            for (int tok = 0; tok < MT; tok++)
+        for (int pr = 0; pr < PR; pr++) {
+            const int pc = L + 64 * pr;
+            if (pc < XL) {
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                    xl[((L >> 3) * MT + tok) * kXStride + x_slot<kFmtW4>(8 * (L & 7) + e)] = xv[tok][e >> 2][e & 3];
+                for (int tok = 0; tok < MT; tok++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        xl[((pc >> 3) * MT + tok) * kXStride + x_slot<kFmtW4>(8 * (pc & 7) + e)] = xv[pr][tok][e >> 2][e & 3];
+            }
         }
     } else {
 #pragma unroll
@@ -156,71 +184,94 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
-    f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4_v acc[RT];
 #pragma unroll
-    for (int ii = 0; ii < NGM; ii++) {
-        if (NG == 0 && ii >= ng) break;
+    for (int r = 0; r < RT; r++) acc[r] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+    // groups in rounds of D (register slot d = group % D, a compile-time index). MT = 8 on slices of more than 5
+    // groups keeps the rounds rolled: fully unrolled, the compiler hoists operand reads across the whole slice and
+    // needs 200+ registers (2 waves per SIMD); the other shapes run faster fully unrolled
+    constexpr int OUTER_UNROLL = MT == 8 && NG > 5 ? 1 : (NGM + D - 1) / D;
+#pragma unroll OUTER_UNROLL
+    for (int i0 = 0; i0 < NGM; i0 += D) {
+#pragma unroll
+    for (int d = 0; d < D; d++) {
+        const int ii = i0 + d;
+        if (ii >= ng) break;
         const int xrow = UPX ? ii * MT : (ii & 1) * MT;  // first staged row of this group
         if constexpr (!UPX) {
             // stage the next group's activations into the other buffer (read two groups ago, LDS operations of
             // a wave complete in order)
-            if (ii + 1 < ng) stxg(xr[(ii + 1) % D], (ii + 1) & 1);
+            if (ii + 1 < ng) stxg(xr[(d + 1) % D], (ii + 1) & 1);
         }
-        const u32x4_v r0 = wv[ii % D][0], r1 = wv[ii % D][1];
+        u32x4_v rc[RT][2];
+#pragma unroll
+        for (int r = 0; r < RT; r++) rc[r][0] = wv[d][r][0], rc[r][1] = wv[d][r][1];
         // refill the window: group ii + D goes where group ii was
         if (ii + D < ng) {
-            if constexpr (!UPX) ldxg(xr[ii % D], ii + D);
-            ldw(ii % D, ii + D);
+            if constexpr (!UPX) ldxg(xr[d], ii + D);
+            ldw(d, ii + D);
         }
-        f32x4_v c = {0.f, 0.f, 0.f, 0.f};
+        // per k step: one B operand read (the group's activations) serves the weight MFMA and the bias MFMA
+        // (A = -136) of each tile: c = sum (128 + u) x - 136 sum x = sum (u - 8) x
+        f32x4_v c[RT];
+#pragma unroll
+        for (int r = 0; r < RT; r++) c[r] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
-            const int j0 = 2 * (mm & 1);
-            const u32x4_v rec = mm < 2 ? r0 : r1;
             u32x4_v b = {0u, 0u, 0u, 0u};
             if (MT == 16 || i < MT)
-                b = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + (i < MT ? i : 0)) * kXStride + (4 * (mm >> 1) + qg) * 8 + 2 * j0]);
-            const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
-            const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
-            const u32x4_v a = {bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
+                b = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + (i < MT ? i : 0)) * kXStride + (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
             const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c, 0, 0, 0);
+            const int j0 = 2 * (mm & 1);
+#pragma unroll
+            for (int r = 0; r < RT; r++) {
+                const u32x4_v rec = rc[r][mm >> 1];
+                const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
+                const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
+                const u32x4_v a = {bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
+                c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c[r], 0, 0, 0);
+                c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c[r], 0, 0, 0);
+            }
         }
-        // rows 4 qg .. 4 qg + 3 of the group's scales
-        const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[ii * 16 + 4 * qg]);
-        acc[0] = fmaf(scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt), c[0], acc[0]);
-        acc[1] = fmaf(scale_rt<SDT>((uint16_t)(sv.x >> 16), sdt), c[1], acc[1]);
-        acc[2] = fmaf(scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt), c[2], acc[2]);
-        acc[3] = fmaf(scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt), c[3], acc[3]);
+#pragma unroll
+        for (int r = 0; r < RT; r++) {
+            // rows 4 qg .. 4 qg + 3 of the group's scales
+            const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[(r * NGM + ii) * 16 + 4 * qg]);
+            acc[r][0] = fmaf(scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt), c[r][0], acc[r][0]);
+            acc[r][1] = fmaf(scale_rt<SDT>((uint16_t)(sv.x >> 16), sdt), c[r][1], acc[r][1]);
+            acc[r][2] = fmaf(scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt), c[r][2], acc[r][2]);
+            acc[r][3] = fmaf(scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt), c[r][3], acc[r][3]);
+        }
         if constexpr (!UPX) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
     }
+    }
 
-    // 2. slices through LDS in a fixed order: red[w][tok][row], lane (qg, i) holds rows 4 qg .. + 3 of column i
-    *reinterpret_cast<f32x4_v*>(&red[(w * 16 + i) * 16 + 4 * qg]) = acc;
+    // 2. slices through LDS in a fixed order: red[w][r][tok][row], lane (qg, i) holds rows 4 qg .. + 3 of column i
+#pragma unroll
+    for (int r = 0; r < RT; r++) *reinterpret_cast<f32x4_v*>(&red[((w * RT + r) * 16 + i) * 16 + 4 * qg]) = acc[r];
     __syncthreads();
-    auto rsum = [&](int tok, int rr) {
+    auto rsum = [&](int r, int tok, int rr) {
         float v = 0.f;
-        for (int ws = 0; ws < S; ws++) v += red[(ws * 16 + tok) * 16 + rr];
+        for (int ws = 0; ws < S; ws++) v += red[((ws * RT + r) * 16 + tok) * 16 + rr];
         return v;
     };
-    const int row0 = 16 * tile;
     if (out == kOutGLU) {
-        for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
-            const int tok = idx >> 3, gg = idx & 7;
-            reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 / 2 + gg] =
-                f32_to_bf16(silu_f32(rsum(tok, gg)) * rsum(tok, gg + 8));
+        for (int idx = threadIdx.x; idx < RT * m * 8; idx += blockDim.x) {
+            const int r = idx / (m * 8), tok = (idx >> 3) - r * m, gg = idx & 7;
+            reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + 8 * (tile0 + r) + gg] =
+                f32_to_bf16(silu_f32(rsum(r, tok, gg)) * rsum(r, tok, gg + 8));
         }
     } else {
-        for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
-            const int tok = idx >> 4, rr = idx & 15;
-            const float v = rsum(tok, rr);
-            if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + row0 + rr] = f32_to_bf16(v);
-            else reinterpret_cast<float*>(y)[(size_t)tok * ldy + row0 + rr] = v;
+        for (int idx = threadIdx.x; idx < RT * m * 16; idx += blockDim.x) {
+            const int r = idx / (m * 16), tok = (idx >> 4) - r * m, rr = idx & 15;
+            const float v = rsum(r, tok, rr);
+            const size_t o = (size_t)tok * ldy + 16 * (tile0 + r) + rr;
+            if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[o] = f32_to_bf16(v);
+            else reinterpret_cast<float*>(y)[o] = v;
         }
     }
 }
@@ -228,14 +279,27 @@ __attribute__((amdgpu_waves_per_eu(MT <= 4 ? 6 : 1))) skinny_kernel(
 template <int SDT>
 void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
             int out, int sdt, hipStream_t st) {
-    // even slices of the matrix-core decode kernels where they divide K, else the generic uneven slices
+    // the K slices of the m = 1 matrix-core kernel where they divide K, else the generic uneven slices; they depend
+    // on (n, k) only, so every m in 2..16 sums a row in the same order (the rows of a batch equal the rows alone)
     const int dg = decode_groups(n, k);
     const Slicing sc = dg > 0 ? Slicing{dg, (k >> 7) / dg} : gemv_slicing(n, k);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
-    const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);
-#define QE_SK_K(MT_, NG_)                                                                                         \
-    skinny_kernel<MT_, SDT, NG_, skinny_d<MT_, NG_>()><<<grid, block, (size_t)sc.S * (skinny_wsz<MT_, NG_>() + 256) * 4, st>>>( \
-        q, s, n, k, x, ldx, y, ldy, m, out, sdt)
+    const dim3 block(64 * sc.S);
+    // two tiles per wave (where n / 16 is even) at m in 5..8, and for the other m on grids of fewer than 16 waves
+    // per CU at one tile per wave. Measured (K = 5120): RT = 2 is 3 % (m = 16, 4, 2) slower on N = 17408 (8704
+    // waves), 3 % faster at m = 8, and 6 to 16 % faster on N = 5120 (2560 waves)
+    const bool rt2 = n % 32 == 0 && (mt == 8 || (long)(n / 16) * sc.S < 16L * qe_num_cus());
+#define QE_SK_K(MT_, NG_)                                                                                           \
+    do {                                                                                                            \
+        constexpr int RT_ = skinny_rt<MT_, NG_>();                                                                  \
+        if (RT_ == 2 && rt2)                                                                                        \
+            skinny_kernel<MT_, SDT, NG_, RT_><<<dim3((unsigned)(n / (16 * RT_))), block,                            \
+                                         (size_t)sc.S * (skinny_wsz<MT_, NG_, RT_>() + 256 * RT_) * 4, st>>>(       \
+                q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                           \
+        else                                                                                                        \
+            skinny_kernel<MT_, SDT, NG_, 1><<<dim3((unsigned)(n / 16)), block, (size_t)sc.S * (skinny_wsz<MT_, NG_, 1>() + 256) * 4, st>>>(     \
+                    q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                       \
+    } while (0)
 #define QE_SK_NG(MT_)                             \
     do {                                          \
         if (sc.ng == 10) QE_SK_K(MT_, 10);        \

@@ -196,6 +196,28 @@ def test_gemv_w4_baseline_shapes(dev, n, k, m):
     assert_bf16_close(y, oracle.matmul_bf16(xh, oracle.dequant_w4(q, s, n, k, 1)))
 
 
+@pytest.mark.parametrize("n,k", [(20480, 5120), (20480, 8064)])
+def test_gemv_long_slices(dev, n, k):
+    """K slices of more than 8 groups, whose scale dwords (and up-front activation pieces) outnumber a wave's 64
+    lanes: (20480, 5120) takes 10-group slices in the m = 1 and skinny matrix-core kernels; (20480, 8064) has no even
+    slicing (K / 128 = 63) and takes 4 uneven slices of 15-16 groups in the VALU GEMV (m = 1, W4 and W8) and the
+    skinny kernel (m >= 2)"""
+    w, q, s = setup_w4(n, k, 1, seed=n + k)
+    xh = synth.x_host(16, k, seed=k + 1)
+    x = synth.to_dev(xh)
+    ref = oracle_ref(xh, q, s, n, k, 1)
+    for m in (1, 2, 4, 16):
+        y = out_f32(ops.gemv_w4(w, x[:m], out_bf16=True))
+        assert_bf16_close(y, ref[:m])
+    del w, ref
+    q8, s8 = synth.w8_host(n, k, seed=53, per_channel=False)
+    s8 = s8.reshape(n, k // 128)
+    w8 = ops.tile_w8(synth.to_dev(q8), synth.to_dev(s8, torch.float16), False)
+    ref8 = oracle_ref_w8(xh[:2], q8, s8, n, k, False)
+    for m in (1, 2):
+        assert_bf16_close(out_f32(ops.gemv_w8(w8, x[:m], out_bf16=True)), ref8[:m])
+
+
 @pytest.mark.parametrize("per_channel", [True, False])
 @pytest.mark.parametrize("n,k", [(64, 256), (8192, 2048)])
 def test_gemv_w8_parity(dev, per_channel, n, k):
