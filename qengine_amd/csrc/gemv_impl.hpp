@@ -127,18 +127,23 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
     const int ndw = FMT == kFmtW8C ? 8 : ng * 8;  // scale dwords of the slice
     u32x4_v wv[NGM][LPG];
     uint32_t xr[PF && !UP ? MT : 1][PF && !UP ? NGM : 1];
-    // UP: lane L loads dwords [8 L, 8 L + 8) of each row's slice (NG groups x 64 dwords) with two 16-byte loads
-    // (the slice starts 16-byte aligned: launch_gemv checks x and ldx)
-    constexpr int XL = UP ? NGM * 8 : 1;  // lanes holding activations
-    u32x4_v xv[UP ? MT : 1][2];
+    // UP: piece p = L + 64 r (slices of more than 8 groups take two rounds): lane L loads dwords [8 p, 8 p + 8) of
+    // each row's slice (NG groups x 64 dwords) with two 16-byte loads (the slice starts 16-byte aligned:
+    // launch_gemv checks x and ldx)
+    constexpr int XL = UP ? NGM * 8 : 1;  // activation pieces of the slice
+    constexpr int XR = (XL + 63) / 64;
+    u32x4_v xv[UP ? XR : 1][UP ? MT : 1][2];
     qp += L;
     if constexpr (UP) {
 #pragma unroll
-        for (int tok = 0; tok < MT; tok++) {
-            const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xw[tok]) + 2 * (L < XL ? L : XL - 1);
-            xv[tok][0] = src[0];
-            xv[tok][1] = src[1];
-        }
+        for (int r = 0; r < XR; r++)
+#pragma unroll
+            for (int tok = 0; tok < MT; tok++) {
+                const int pc = L + 64 * r < XL ? L + 64 * r : XL - 1;
+                const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xw[tok]) + 2 * pc;
+                xv[r][tok][0] = src[0];
+                xv[r][tok][1] = src[1];
+            }
     }
     // scale dword p = L + 64 r (slices of more than 8 groups take two rounds)
     constexpr int SPR = FMT == kFmtW8C ? 1 : (NGM * 8 + 63) / 64;
@@ -185,20 +190,26 @@ __device__ __forceinline__ float* gemv_tile(uint32_t* lds, const uint4* __restri
         }
     };
     if constexpr (UP) {
-        // dword e of lane L is dword d = 8 (L % 8) + e of group L / 8, stored at its (class, slot) (x_slot, the
-        // inverse of x_dword); then lane L adds up class L % 8 of group L / 8 (16 values, in order)
-        const int gi = L >> 3, l8 = L & 7;
-        if (L < XL) {
+        // dword e of piece p is dword d = 8 (p % 8) + e of group p / 8, stored at its (class, slot) (x_slot, the
+        // inverse of x_dword); then the lane of piece p adds up class p % 8 of group p / 8 (16 values, in order)
 #pragma unroll
-            for (int tok = 0; tok < MT; tok++)
+        for (int r = 0; r < XR; r++) {
+            const int pc = L + 64 * r, gi = pc >> 3, l8 = pc & 7;
+            if (pc < XL) {
 #pragma unroll
-                for (int e = 0; e < 8; e++)
-                    xl[(gi * MT + tok) * 64 + x_slot<FMT>(8 * l8 + e)] = tok < m ? xv[tok][e >> 2][e & 3] : 0u;
+                for (int tok = 0; tok < MT; tok++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++)
+                        xl[(gi * MT + tok) * 64 + x_slot<FMT>(8 * l8 + e)] = tok < m ? xv[r][tok][e >> 2][e & 3] : 0u;
+            }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (L < XL) {
+#pragma unroll
+        for (int r = 0; r < XR; r++) {
+            const int pc = L + 64 * r, gi = pc >> 3, l8 = pc & 7;
+            if (pc >= XL) continue;
 #pragma unroll
             for (int tok = 0; tok < MT; tok++) {
                 const u32x4_v* cl = reinterpret_cast<const u32x4_v*>(&xl[(gi * MT + tok) * 64 + l8 * 8]);

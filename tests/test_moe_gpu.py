@@ -72,6 +72,14 @@ def test_moe_layer_small(dev, T):
     assert_bf16_close(y, ref)
 
 
+@pytest.mark.parametrize("T,I", [(4, 1024), (4, 2048), (100, 2048)])
+def test_moe_layer_wide_intermediate(dev, T, I):
+    """I = 1024 / 2048: the decode down GEMV runs K slices of 8 / 16 groups (16 groups: two rounds of activation
+    pieces per lane in its up-front staging); T = 100 takes the prefill GEMMs"""
+    y, ref, *_ = _layer(dev, T, E=8, topk=2, H=512, I=I, seed=I + T)
+    assert_bf16_close(y, ref)
+
+
 def pipeline_ref(lg, xh, gq, gs, dq, ds, topk, H, I):
     """this build's layer numerics on the oracle's bf16-dequantized experts (float64 products): act =
     bf16(silu(gate) up w_k) (gate_up epilogue), slot = bf16(down . act) (down epilogue), out = bf16 of the fp32 sum
