@@ -54,73 +54,86 @@ __device__ __forceinline__ const char* rec_ptr(const char* recs, const MoeShape&
 constexpr int kRouteThreads = 256;  // 4 tokens per block
 constexpr int kMaxExperts = 1024;
 
-// one argmax step over a DPP pattern with the tie rule (value desc, index asc)
-template <int CTRL>
-__device__ __forceinline__ void route_step(float& bv, int& bi) {
-    const float v2 = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, bv), CTRL, 0xF,
-                                                                           0xF, false));
-    const int i2 = __builtin_amdgcn_update_dpp(0, bi, CTRL, 0xF, 0xF, false);
-    const bool b2 = (v2 > bv) | ((v2 == bv) & (i2 < bi));
-    bv = b2 ? v2 : bv;
-    bi = b2 ? i2 : bi;
+// Routing key of (logit v, expert i): unsigned 64-bit order = (v desc, i asc). High word: the float bits made monotone
+// (-0 taken as +0, so equal logits compare equal as floats do), low word: ~i.
+__device__ __forceinline__ uint64_t route_key(float v, int i) {
+    uint32_t b = __builtin_bit_cast(uint32_t, v);
+    b = (b & 0x7FFFFFFFu) == 0u ? 0u : b;
+    b = (b & 0x80000000u) != 0u ? ~b : (b | 0x80000000u);
+    return ((uint64_t)b << 32) | (uint64_t)(~(uint32_t)i);
+}
+__device__ __forceinline__ float route_key_value(uint64_t k) {
+    const uint32_t b = (uint32_t)(k >> 32);
+    return __builtin_bit_cast(float, (b & 0x80000000u) != 0u ? (b & 0x7FFFFFFFu) : ~b);
 }
 
-// Lane l holds the logits of experts l + 64 i (i < PER = ceil(E / 64)). Each of the topk rounds takes the lane's best
-// untaken expert (value desc; its experts ascend with i, so the first maximum is the lowest index; selects, no
-// branches), reduces each 16-lane row by DPP (quad swaps, then row rotations by 4 and 8) and the four row results by
-// readlane, with the tie rule (value desc, index asc): no LDS traffic, no barriers.
+// one max step of the wave reduction over a DPP pattern; lanes of rows outside ROWMASK keep their key (every lane
+// is written when ROWMASK is 0xF, so no old value has to be kept)
+template <int CTRL, int ROWMASK = 0xF>
+__device__ __forceinline__ void route_step(uint64_t& k) {
+    const int hi = (int)(k >> 32), lo = (int)(uint32_t)k;
+    int h2, l2;
+    if constexpr (ROWMASK == 0xF) {
+        h2 = __builtin_amdgcn_mov_dpp(hi, CTRL, 0xF, 0xF, false);
+        l2 = __builtin_amdgcn_mov_dpp(lo, CTRL, 0xF, 0xF, false);
+    } else {
+        h2 = __builtin_amdgcn_update_dpp(hi, hi, CTRL, ROWMASK, 0xF, false);
+        l2 = __builtin_amdgcn_update_dpp(lo, lo, CTRL, ROWMASK, 0xF, false);
+    }
+    const uint64_t k2 = ((uint64_t)(uint32_t)h2 << 32) | (uint32_t)l2;
+    k = k2 > k ? k2 : k;
+}
+
+// Lane l holds the keys of experts l + 64 i (i < PER = ceil(E / 64); missing experts key 0). Each of the topk rounds
+// takes the lane's largest unselected key, reduces the lanes' candidates to the wave's largest key by DPP (quad
+// swaps, row rotations by 4 and 8, row broadcasts 15 and 31: lane 63 holds it) and the lane that held it marks that
+// key selected: no LDS traffic, no barriers, one 64-bit compare per step. Keys are distinct, so the order is total.
 // one token t by the calling wave; sel / w: the token's topk outputs (global or LDS)
 template <int PER>
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, int t, int E, int topk, int32_t* sel,
                                             float* w) {
     const int lane = threadIdx.x & 63;
+    uint64_t k[PER];
     float v[PER];
     const float* l = logits + (size_t)t * E;
 #pragma unroll
+    for (int i = 0; i < PER; i++) v[i] = l[lane + 64 * i < E ? lane + 64 * i : E - 1];  // all loads before any use
+#pragma unroll
     for (int i = 0; i < PER; i++) {
         const int e = lane + 64 * i;
-        v[i] = l[e < E ? e : E - 1];
+        k[i] = route_key(v[i], e) & (0ull - (uint64_t)(e < E));  // missing experts: key 0 (no branch)
     }
-    unsigned avail = 0;  // bit i: expert lane + 64 i exists and is not taken
-#pragma unroll
-    for (int i = 0; i < PER; i++) avail |= (lane + 64 * i < E ? 1u : 0u) << i;
-    float myv = 0.f;  // lane k keeps round k's value and index
-    int myi = 0;
-    float v0 = 0.f;
-    for (int k = 0; k < topk; k++) {
-        float bvv = -INFINITY;
-        int bii = 0x7fffffff;
+    unsigned avail = (1u << PER) - 1u;  // bit i: key i not yet selected (missing experts hold key 0, never selected)
+    uint64_t mine = 0;                   // lane r keeps round r's key
+    for (int r = 0; r < topk; r++) {
+        // the lane's largest available key (selects over the PER keys, no branches)
+        uint64_t lk = 0;
+        int li = 0;
 #pragma unroll
         for (int i = 0; i < PER; i++) {
-            const bool better = (((avail >> i) & 1u) != 0) & ((v[i] > bvv) | (bii == 0x7fffffff));  // no short circuit
-            bvv = better ? v[i] : bvv;
-            bii = better ? lane + 64 * i : bii;
+            const bool better = (((avail >> i) & 1u) != 0u) & (k[i] > lk);  // no short circuit
+            lk = better ? k[i] : lk;
+            li = better ? i : li;
         }
-        route_step<0xB1>(bvv, bii);   // quad_perm [1,0,3,2]
-        route_step<0x4E>(bvv, bii);   // quad_perm [2,3,0,1]
-        route_step<0x124>(bvv, bii);  // row_ror:4
-        route_step<0x128>(bvv, bii);  // row_ror:8
-        float fv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bvv), 0));
-        int fi = __builtin_amdgcn_readlane(bii, 0);
-#pragma unroll
-        for (int r = 1; r < 4; r++) {
-            const float v2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, bvv), 16 * r));
-            const int i2 = __builtin_amdgcn_readlane(bii, 16 * r);
-            const bool b2 = (v2 > fv) | ((v2 == fv) & (i2 < fi));
-            fv = b2 ? v2 : fv;
-            fi = b2 ? i2 : fi;
-        }
-        avail &= (fi & 63) == lane ? ~(1u << (fi >> 6)) : ~0u;
-        myv = lane == k ? fv : myv;
-        myi = lane == k ? fi : myi;
-        v0 = k == 0 ? fv : v0;
+        uint64_t bk = lk;
+        route_step<0xB1>(bk);        // quad_perm [1,0,3,2]
+        route_step<0x4E>(bk);        // quad_perm [2,3,0,1]
+        route_step<0x124>(bk);       // row_ror:4
+        route_step<0x128>(bk);       // row_ror:8: every lane of a row holds the row's largest
+        route_step<0x142, 0xA>(bk);  // row_bcast:15 into rows 1 and 3
+        route_step<0x143, 0xC>(bk);  // row_bcast:31 into rows 2 and 3: lane 63 holds the wave's largest
+        const uint64_t best = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(bk >> 32), 63) << 32) |
+                              (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bk, 63);
+        avail &= ~((lk == best ? 1u : 0u) << li);
+        mine = lane == r ? best : mine;
     }
     // weights exp(l_k - l_max) / sum, the sum in k order
-    const float ex = expf(myv - v0);
+    const float v0 = route_key_value(((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(mine >> 32), 0) << 32));
+    const float ex = expf(route_key_value(mine) - v0);
     float tot = 0.f;
-    for (int k = 0; k < topk; k++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), k));
+    for (int r = 0; r < topk; r++) tot += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, ex), r));
     if (lane < topk) {
-        sel[lane] = myi;
+        sel[lane] = (int)~(uint32_t)mine;
         w[lane] = ex / tot;
     }
 }
@@ -253,8 +266,11 @@ __global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t*
     }
 }
 
-// Decode batches (T <= kDecTokens): route and segment in one block. The 16 waves route tokens w, w + 16 into LDS, then
-// the block segments them as moe_segment_kernel does (same slots, jobs and offsets).
+// Decode batches (T <= kDecTokens): route and segment in one block of min(T, 16) waves. The waves route tokens
+// w, w + nw, ... into LDS; after the one barrier wave 0 alone segments them (its LDS operations complete in order, so
+// it needs no further barrier): per-expert counts and 32-bit token masks by LDS atomics, the exclusive scans of the
+// counts and job counts with lane l owning experts PER l .. PER l + PER - 1, then each pair's slot = the expert's
+// offset + the number of earlier tokens on that expert. Same off / slots / jobs as moe_segment_kernel.
 constexpr int kDecTokens = 32;
 template <int PER>
 __global__ void __launch_bounds__(kSegThreads) moe_route_segment_kernel(const float* __restrict__ logits, int T, int E,
@@ -267,25 +283,81 @@ __global__ void __launch_bounds__(kSegThreads) moe_route_segment_kernel(const fl
                                                                         int32_t* __restrict__ njobs) {
     __shared__ int32_t ssel[kDecTokens * 16];
     __shared__ float sw[kDecTokens * 16];
-    __shared__ int cnt[kMaxExperts], pre[kMaxExperts + 1];
-    __shared__ unsigned long long mark[kMaxExperts];
-    const int tid = threadIdx.x, wv = tid >> 6;
-    for (int t = wv; t < T; t += kSegThreads / 64) route_token<PER>(logits, t, E, topk, ssel + t * topk, sw + t * topk);
-    for (int e = tid; e < E; e += kSegThreads) cnt[e] = 0;
+    __shared__ int cnt[64 * PER], pre[64 * PER];
+    __shared__ unsigned mark[64 * PER];
+    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
+    for (int e = tid; e < E; e += blockDim.x) {
+        cnt[e] = 0;
+        mark[e] = 0u;
+    }
+    for (int t = wv; t < T; t += nw) route_token<PER>(logits, t, E, topk, ssel + t * topk, sw + t * topk);
     __syncthreads();
-    for (int i = tid; i < T * topk; i += kSegThreads) atomicAdd(&cnt[ssel[i]], 1);
-    __syncthreads();
-    seg_scan_jobs(cnt, pre, E, chunk, off, jobs, njobs);
-    seg_place_chunk(ssel, sw, T, E, topk, 0, pre, mark, slot_pair, slot_tok, slot_w, inv);  // one chunk: T <= 64
+    if (wv != 0) return;
+    const int P = T * topk;
+    for (int p = lane; p < P; p += 64) {
+        const int e = ssel[p];
+        atomicAdd(&cnt[e], 1);
+        atomicOr(&mark[e], 1u << (p / topk));
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    int c[PER], a = 0, jb = 0;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = lane * PER + j;
+        c[j] = e < E ? cnt[e] : 0;
+        a += c[j];
+        jb += (c[j] + chunk - 1) / chunk;
+    }
+    int ai = a, ji = jb;  // inclusive wave scans
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int a2 = __shfl_up(ai, o), j2 = __shfl_up(ji, o);
+        ai += lane >= o ? a2 : 0;
+        ji += lane >= o ? j2 : 0;
+    }
+    int run = ai - a, jrun = ji - jb;
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int e = lane * PER + j;
+        if (e < E) {
+            pre[e] = run;
+            off[e] = run;
+            const int nj = (c[j] + chunk - 1) / chunk;
+            for (int q = 0; q < nj; q++) {
+                jobs[2 * (jrun + q)] = e;
+                jobs[2 * (jrun + q) + 1] = q * chunk;
+            }
+            run += c[j];
+            jrun += nj;
+        }
+    }
+    if (lane == 63) {
+        off[E] = ai;
+        *njobs = ji;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int p = lane; p < P; p += 64) {
+        const int e = ssel[p], t = p / topk;
+        const int slot = pre[e] + __popc(mark[e] & ((1u << t) - 1u));
+        slot_pair[slot] = p;
+        slot_tok[slot] = t;
+        slot_w[slot] = sw[p];
+        inv[p] = slot;
+    }
 }
 
 void launch_route_segment(const float* logits, int T, int E, int topk, int chunk, int32_t* off, int32_t* slot_pair,
                           int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs, int32_t* njobs,
                           hipStream_t st) {
     const int per = (E + 63) / 64;
-#define QE_RS(PER_)                                                                                              \
-    moe_route_segment_kernel<PER_><<<1, kSegThreads, 0, st>>>(logits, T, E, topk, chunk, off, slot_pair, slot_tok, \
-                                                             slot_w, inv, jobs, njobs)
+    const unsigned threads = 64u * (unsigned)(T < 16 ? T : 16);
+#define QE_RS(PER_)                                                                                                 \
+    moe_route_segment_kernel<PER_><<<1, threads, 0, st>>>(logits, T, E, topk, chunk, off, slot_pair, slot_tok, slot_w, \
+                                                          inv, jobs, njobs)
     if (per <= 1) QE_RS(1);
     else if (per <= 2) QE_RS(2);
     else if (per <= 4) QE_RS(4);

@@ -135,3 +135,31 @@ def test_moe_layer_baseline(dev, T):
     tokens = None if T <= 16 else np.sort(np.random.default_rng(7).choice(T, 24, replace=False))
     y, ref, *_ = _layer(dev, T, E=512, topk=10, H=2048, I=512, seed=100 + T, tokens=tokens)
     assert_bf16_close(y, ref)
+
+
+@pytest.mark.parametrize("T", [1, 16, 40])
+def test_moe_layer_graph_replay(dev, T):
+    """the layer captured in a HIP graph (no host synchronization, allocation or memset inside a call) and replayed
+    with new logits and activations copied into the captured inputs: every replay equals the eager call"""
+    E, topk, H, I = 32, 4, 512, 256
+    gq, gs, dq, ds = synth.moe_host(E, H, I, seed=70 + T)
+    moe = ops.MoE.pack(synth.to_dev(gq), synth.to_dev(gs, torch.float16), synth.to_dev(dq),
+                       synth.to_dev(ds, torch.float16), topk=topk)
+    lg_in = torch.zeros(T, E, dtype=torch.float32, device=dev)
+    x_in = torch.zeros(T, H, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    moe(lg_in, x_in, out_bf16=True, out=out)  # workspace allocated outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        moe(lg_in, x_in, out_bf16=True, out=out)
+    for r in range(3):
+        lg = torch.from_numpy(synth.logits_host(T, E, seed=80 + r)).to(dev)
+        x = synth.to_dev(synth.x_host(T, H, seed=90 + r))
+        want = moe(lg, x, out_bf16=True)
+        torch.cuda.synchronize()
+        lg_in.copy_(lg)
+        x_in.copy_(x)
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), r
