@@ -1,7 +1,18 @@
 // INT8 decode GEMV / skinny GEMM instantiations (kernel: gemv_impl.hpp); the scale dtype is a run-time value.
 #include "gemv_impl.hpp"
 
+#include <cstdlib>
+
 using namespace qe_gemv;
+
+static int w8_mfma_min_m() {
+    static const int v = [] {
+        const char* e = getenv("QE_W8_MFMA_MIN_M");
+        const int x = e ? atoi(e) : 2;
+        return x >= 1 ? x : 2;
+    }();
+    return v;
+}
 
 void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
     CHECK(w.n > 0 && w.k > 0 && w.n % 16 == 0 && w.k % 128 == 0 && m >= 1 && m <= kMaxGemvRows, "gemv_w8 %d %d %d",
@@ -10,6 +21,12 @@ void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     CHECK(ldy >= (w.glu ? w.n / 2 : w.n), "gemv_w8 ldy %d", ldy);
     CHECK(!w.glu || w.q8, "gemv_w8: GLU is for Q8 matrices");
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    // W8 records with 16-byte aligned activation rows: the matrix-core kernel (QE_W8_MFMA_MIN_M, default 2, is the
+    // smallest m it takes); Q8, GLU and unaligned rows: the VALU GEMV
+    if (!w.q8 && !w.glu && m >= w8_mfma_min_m() && ((uintptr_t)x & 15) == 0 && ldx % 8 == 0) {
+        skinny_w8_mfma(w, x, ldx, y, ldy, m, out, st);
+        return;
+    }
     if (w.q8) launch_gemv<kFmtQ8, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else if (w.per_channel) launch_gemv<kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else launch_gemv<kFmtW8G, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);

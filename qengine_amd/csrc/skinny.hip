@@ -36,18 +36,18 @@ using namespace qe_gemv;
 // WPE, measured on the BASELINE shapes (K = 5120, 5-group slices; N = 5120 and 17408):
 //   RT = 2: D = 2 on slices of <= 5 groups (WPE 4: <= 128 VGPRs), else D = 3 (MT = 8: 2)
 //   RT = 1: D = 3 (MT = 8: 2, 6 waves per SIMD), WPE 6 at MT <= 4 on even slices of <= 5 groups
-template <int MT, int NG>
+template <int MT, int NG, int FMT>
 constexpr int skinny_rt() {
-    return NG == 0 ? 1 : 2;
+    return NG == 0 || FMT != kFmtW4 ? 1 : 2;
 }
-template <int MT, int NG, int RT>
+template <int MT, int NG, int RT, int FMT>
 constexpr int skinny_d() {
-    constexpr int d = MT == 8 || (RT == 2 && NG > 0 && NG <= 5) ? 2 : 3;
+    constexpr int d = MT == 8 || FMT != kFmtW4 || (RT == 2 && NG > 0 && NG <= 5) ? 2 : 3;
     return NG > 0 && NG < d ? NG : d;
 }
-template <int MT, int NG, int RT>
+template <int MT, int NG, int RT, int FMT>
 constexpr int skinny_wpe() {  // minimum waves per SIMD asked of the register allocator
-    return RT == 2 ? (NG <= 5 ? 4 : 1) : (MT <= 4 && NG > 0 && NG <= 5 ? 6 : 1);
+    return FMT != kFmtW4 ? 1 : RT == 2 ? (NG <= 5 ? 4 : 1) : (MT <= 4 && NG > 0 && NG <= 5 ? 6 : 1);
 }
 
 // UPX (MT <= 4 with even slices): every group's activations are loaded before the weights and staged in LDS
@@ -68,7 +68,8 @@ constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][
     return (skinny_upx<MT, NG>() ? NGM : 2) * MT * kXStride + RT * NGM * 8;
 }
 
-template <int MT, int SDT, int NG, int RT, int D = skinny_d<MT, NG, RT>(), int WPE = skinny_wpe<MT, NG, RT>()>
+template <int MT, int SDT, int NG, int RT, int FMT, int D = skinny_d<MT, NG, RT, FMT>(),
+          int WPE = skinny_wpe<MT, NG, RT, FMT>()>
 __global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
 __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K, const uint16_t* __restrict__ x,
@@ -86,7 +87,7 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][RT][16 tok][16 rows]
 
     const int qg = L >> 4, i = L & 15;  // operand lane group, row / column within the tile
-    const int g = i & 7, sh = 4 * (i >> 3);
+    const int g = i & 7, sh = 4 * (i >> 3);  // W4: nibble shift of row i's half (W8: byte pair 16 sh / 4)
 
     // Activation rows tok >= m (up to MT) load row m - 1 instead: no load sits under a branch, and those MFMA
     // columns are never stored (columns are independent).
@@ -123,21 +124,27 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     constexpr int PR = (NGM * 8 + 63) / 64;  // rounds of 64 scale dwords / activation pieces (slices of > 8 groups)
 #pragma unroll
     for (int r = 0; r < RT; r++) {
-        const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)(tile0 + r) * G + gb) * 16);
+        if constexpr (FMT == kFmtW8C) {  // one scale per row: the tile's 16 (8 dwords), for every group
+            const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + (size_t)(tile0 + r) * 16);
+            if (L < 8) reinterpret_cast<uint32_t*>(sl16)[r * NGM * 8 + L] = sp[L];
+        } else {
+            const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)(tile0 + r) * G + gb) * 16);
 #pragma unroll
-        for (int pr = 0; pr < PR; pr++)
-            if (L + 64 * pr < ng * 8) reinterpret_cast<uint32_t*>(sl16)[r * NGM * 8 + L + 64 * pr] = sp[L + 64 * pr];
+            for (int pr = 0; pr < PR; pr++)
+                if (L + 64 * pr < ng * 8) reinterpret_cast<uint32_t*>(sl16)[r * NGM * 8 + L + 64 * pr] = sp[L + 64 * pr];
+        }
     }
     u32x4_v xr[UPX ? 1 : D][XP];  // activation register slots (per-group staging)
-    const uint4* qp = q + ((size_t)tile0 * (K >> 6) + 2 * gb) * 32 + 4 * g + qg;
-    const size_t qts = (size_t)(K >> 6) * 32;  // records per tile
-    u32x4_v wv[D][RT][2];
+    // records of lane (g, t): W4 one per 64 k (two per group), W8 one per 32 k (four per group); 32 per record column
+    constexpr int LPG = FMT == kFmtW4 ? 2 : 4;
+    const size_t qts = (size_t)(K >> (FMT == kFmtW4 ? 6 : 5)) * 32;  // records per tile
+    const uint4* qp = q + (size_t)tile0 * qts + (size_t)(LPG * gb) * 32 + 4 * g + qg;
+    u32x4_v wv[D][RT][LPG];
     auto ldw = [&](int slot, int ii) {
 #pragma unroll
-        for (int r = 0; r < RT; r++) {
-            wv[slot][r][0] = ld_stream(qp + r * qts + (size_t)ii * 64);
-            wv[slot][r][1] = ld_stream(qp + r * qts + (size_t)ii * 64 + 32);
-        }
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int e = 0; e < LPG; e++) wv[slot][r][e] = ld_stream(qp + r * qts + (size_t)ii * (32 * LPG) + 32 * e);
     };
     if constexpr (UPX) {
         // piece p = L + 64 pr: lane L loads dwords [8 p, 8 p + 8) of each row's slice (16-byte pieces; x and ldx
@@ -183,7 +190,9 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
+    // the bias as bf16 pairs: W4 -136 (u = w + 8 over the magic's 128), W8 -128 (u = w + 128)
+    constexpr uint32_t kBias = FMT == kFmtW4 ? 0xC308C308u : 0xC300C300u;
+    const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{kBias, kBias, kBias, kBias});
     f32x4_v acc[RT];
 #pragma unroll
     for (int r = 0; r < RT; r++) acc[r] = f32x4_v{0.f, 0.f, 0.f, 0.f};
@@ -203,9 +212,11 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             // a wave complete in order)
             if (ii + 1 < ng) stxg(xr[(d + 1) % D], (ii + 1) & 1);
         }
-        u32x4_v rc[RT][2];
+        u32x4_v rc[RT][LPG];
 #pragma unroll
-        for (int r = 0; r < RT; r++) rc[r][0] = wv[d][r][0], rc[r][1] = wv[d][r][1];
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int e = 0; e < LPG; e++) rc[r][e] = wv[d][r][e];
         // refill the window: group ii + D goes where group ii was
         if (ii + D < ng) {
             if constexpr (!UPX) ldxg(xr[d], ii + D);
@@ -225,10 +236,25 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             const int j0 = 2 * (mm & 1);
 #pragma unroll
             for (int r = 0; r < RT; r++) {
-                const u32x4_v rec = rc[r][mm >> 1];
-                const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
-                const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
-                const u32x4_v a = {bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
+                u32x4_v a;
+                if constexpr (FMT == kFmtW4) {
+                    const u32x4_v rec = rc[r][mm >> 1];
+                    const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
+                    const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
+                    a = u32x4_v{bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
+                } else {
+                    // record of slab mm: dword d holds bytes (g, k) (g, k + 1) (g + 8, k) (g + 8, k + 1) at
+                    // k = 32 mm + 16 (d / 2) + 8 (d % 2) + 2 t, the B operand's k order; row i takes its byte pair,
+                    // u = w + 128 as float (exact) and the high halves are the bf16 pair
+                    const u32x4_v rec = rc[r][mm];
+#pragma unroll
+                    for (int dd = 0; dd < 4; dd++) {
+                        const uint32_t u = (rec[dd] ^ 0x80808080u) >> (4 * sh);
+                        const float f0 = static_cast<float>(u & 0xFFu), f1 = static_cast<float>((u >> 8) & 0xFFu);
+                        a[dd] = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0),
+                                                      0x07060302u);
+                    }
+                }
                 c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c[r], 0, 0, 0);
                 c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c[r], 0, 0, 0);
             }
@@ -236,7 +262,7 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
 #pragma unroll
         for (int r = 0; r < RT; r++) {
             // rows 4 qg .. 4 qg + 3 of the group's scales
-            const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[(r * NGM + ii) * 16 + 4 * qg]);
+            const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[(r * NGM + (FMT == kFmtW8C ? 0 : ii)) * 16 + 4 * qg]);
             acc[r][0] = fmaf(scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt), c[r][0], acc[r][0]);
             acc[r][1] = fmaf(scale_rt<SDT>((uint16_t)(sv.x >> 16), sdt), c[r][1], acc[r][1]);
             acc[r][2] = fmaf(scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt), c[r][2], acc[r][2]);
@@ -276,7 +302,7 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     }
 }
 
-template <int SDT>
+template <int FMT, int SDT>
 void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
             int out, int sdt, hipStream_t st) {
     // the K slices of the m = 1 matrix-core kernel where they divide K, else the generic uneven slices; they depend
@@ -291,13 +317,14 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     const bool rt2 = n % 32 == 0 && (mt == 8 || (long)(n / 16) * sc.S < 16L * qe_num_cus());
 #define QE_SK_K(MT_, NG_)                                                                                           \
     do {                                                                                                            \
-        constexpr int RT_ = skinny_rt<MT_, NG_>();                                                                  \
+        constexpr int RT_ = skinny_rt<MT_, NG_, FMT>();                                                             \
         if (RT_ == 2 && rt2)                                                                                        \
-            skinny_kernel<MT_, SDT, NG_, RT_><<<dim3((unsigned)(n / (16 * RT_))), block,                            \
+            skinny_kernel<MT_, SDT, NG_, RT_, FMT><<<dim3((unsigned)(n / (16 * RT_))), block,                       \
                                          (size_t)sc.S * (skinny_wsz<MT_, NG_, RT_>() + 256 * RT_) * 4, st>>>(       \
                 q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                           \
         else                                                                                                        \
-            skinny_kernel<MT_, SDT, NG_, 1><<<dim3((unsigned)(n / 16)), block, (size_t)sc.S * (skinny_wsz<MT_, NG_, 1>() + 256) * 4, st>>>(     \
+            skinny_kernel<MT_, SDT, NG_, 1, FMT><<<dim3((unsigned)(n / 16)), block,                                 \
+                                              (size_t)sc.S * (skinny_wsz<MT_, NG_, 1>() + 256) * 4, st>>>(         \
                     q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                       \
     } while (0)
 #define QE_SK_NG(MT_)                             \
@@ -323,6 +350,12 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
 }  // namespace qe_skinny
 
 void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
-    if (w.sdt == kScaleF16) qe_skinny::launch<kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
-    else qe_skinny::launch<kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    if (w.sdt == kScaleF16) qe_skinny::launch<qe_gemv::kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    else qe_skinny::launch<qe_gemv::kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+}
+
+// INT8 (W8 layout, per-channel or group scales; the scale dtype a run-time value), no GLU
+void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
+    if (w.per_channel) qe_skinny::launch<qe_gemv::kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    else qe_skinny::launch<qe_gemv::kFmtW8G, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }

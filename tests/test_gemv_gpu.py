@@ -219,7 +219,7 @@ def test_gemv_long_slices(dev, n, k):
 
 
 @pytest.mark.parametrize("per_channel", [True, False])
-@pytest.mark.parametrize("n,k", [(64, 256), (8192, 2048)])
+@pytest.mark.parametrize("n,k", [(64, 256), (8192, 2048), (4096, 5120)])
 def test_gemv_w8_parity(dev, per_channel, n, k):
     q, s = synth.w8_host(n, k, seed=51, per_channel=per_channel)
     if not per_channel:
@@ -232,13 +232,18 @@ def test_gemv_w8_parity(dev, per_channel, n, k):
     full = ops.gemv_w8(w, x)
     torch.cuda.synchronize()
     assert err_ratio(full.cpu().numpy(), ref_ex) <= 1e-4
-    assert err_ratio(full.cpu().numpy(), ref) <= TOL
-    for m in (1, 4):
+    # against the reference's bf16-rounded weights (K = 5120: their rounding alone reaches ~2e-2 * rms on the rows
+    # with the largest scales), the BASELINE gate with the rounding allowance of the other tests
+    assert_bf16_close(full.cpu().numpy(), ref)
+    for m in (1, 2, 4, 9):
         y = ops.gemv_w8(w, x[:m], out_bf16=True)
         assert_bf16_close(out_f32(y), ref[:m])
         y32 = ops.gemv_w8(w, x[:m])
         torch.cuda.synchronize()
-        assert np.array_equal(y32.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32)[:m])
+        if m == 1:  # the VALU GEMV (m >= 2: the matrix-core kernel, whose rows are the same for every m)
+            assert err_ratio(y32.cpu().numpy(), full.cpu().numpy()[:1]) <= 1e-5
+        else:
+            assert np.array_equal(y32.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32)[:m]), m
 
 
 def test_gemv_w8_reference_hook(dev):
