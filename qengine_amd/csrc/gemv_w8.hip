@@ -5,13 +5,16 @@
 
 using namespace qe_gemv;
 
-static int w8_mfma_min_m() {
-    static const int v = [] {
+// smallest m that the matrix-core kernel takes: QE_W8_MFMA_MIN_M if set, else 2, or 1 where the m = 1 slicing
+// has >= 4 groups per wave (measured, N = 8192: m = 1 at K = 5120 (5-group slices) 10.9 -> 8.9 us on the matrix
+// cores; at K = 2048 (2-group slices) the VALU GEMV is faster, 5.0 vs 6.0 us)
+static int w8_mfma_min_m(int n, int k) {
+    static const int env = [] {
         const char* e = getenv("QE_W8_MFMA_MIN_M");
-        const int x = e ? atoi(e) : 2;
-        return x >= 1 ? x : 2;
+        return e && atoi(e) >= 1 ? atoi(e) : 0;
     }();
-    return v;
+    if (env > 0) return env;
+    return decode_groups(n, k) >= 4 ? 1 : 2;
 }
 
 void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
@@ -21,9 +24,9 @@ void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     CHECK(ldy >= (w.glu ? w.n / 2 : w.n), "gemv_w8 ldy %d", ldy);
     CHECK(!w.glu || w.q8, "gemv_w8: GLU is for Q8 matrices");
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
-    // W8 records with 16-byte aligned activation rows: the matrix-core kernel (QE_W8_MFMA_MIN_M, default 2, is the
-    // smallest m it takes); Q8, GLU and unaligned rows: the VALU GEMV
-    if (!w.q8 && !w.glu && m >= w8_mfma_min_m() && ((uintptr_t)x & 15) == 0 && ldx % 8 == 0) {
+    // W8 records with 16-byte aligned activation rows: the matrix-core kernel from w8_mfma_min_m rows; Q8, GLU and
+    // unaligned rows: the VALU GEMV
+    if (!w.q8 && !w.glu && m >= w8_mfma_min_m(w.n, w.k) && ((uintptr_t)x & 15) == 0 && ldx % 8 == 0) {
         skinny_w8_mfma(w, x, ldx, y, ldy, m, out, st);
         return;
     }

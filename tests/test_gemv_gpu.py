@@ -240,7 +240,7 @@ def test_gemv_w8_parity(dev, per_channel, n, k):
         assert_bf16_close(out_f32(y), ref[:m])
         y32 = ops.gemv_w8(w, x[:m])
         torch.cuda.synchronize()
-        if m == 1:  # the VALU GEMV (m >= 2: the matrix-core kernel, whose rows are the same for every m)
+        if m == 1:  # the VALU GEMV at short slices (m >= 2: the matrix-core kernel, the same rows for every m)
             assert err_ratio(y32.cpu().numpy(), full.cpu().numpy()[:1]) <= 1e-5
         else:
             assert np.array_equal(y32.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32)[:m]), m
