@@ -242,6 +242,20 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                     const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
                     const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
                     a = u32x4_v{bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
+                } else if constexpr (FMT == kFmtQ8) {
+                    // record of 32-k chunk mm: word 2 s + hh holds row g + 8 hh, the signed weights w at
+                    // k0 + {0, 8, 1, 9}, k0 = 32 mm + 16 s + 2 t: bytes (0, 2) and (1, 3) of u = w + 128 are the B
+                    // operand's pairs (k0, k0 + 1) and (k0 + 8, k0 + 9)
+                    const u32x4_v rec = rc[r][mm];
+                    const bool hh = sh != 0;
+                    const uint32_t wa = (hh ? rec[1] : rec[0]) ^ 0x80808080u, wb = (hh ? rec[3] : rec[2]) ^ 0x80808080u;
+                    auto pr = [](uint32_t u, int b0) {  // bf16 pair of bytes b0, b0 + 2 (exact)
+                        const float f0 = static_cast<float>((u >> (8 * b0)) & 0xFFu);
+                        const float f1 = static_cast<float>((u >> (8 * b0 + 16)) & 0xFFu);
+                        return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0),
+                                                     0x07060302u);
+                    };
+                    a = u32x4_v{pr(wa, 0), pr(wa, 1), pr(wb, 0), pr(wb, 1)};
                 } else {
                     // record of slab mm: dword d holds bytes (g, k) (g, k + 1) (g + 8, k) (g + 8, k + 1) at
                     // k = 32 mm + 16 (d / 2) + 8 (d % 2) + 2 t, the B operand's k order; row i takes its byte pair,
@@ -354,8 +368,9 @@ void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, i
     else qe_skinny::launch<qe_gemv::kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }
 
-// INT8 (W8 layout, per-channel or group scales; the scale dtype a run-time value), no GLU
+// INT8 (W8 layout with per-channel or group scales, or the Q8 layout; the scale dtype a run-time value)
 void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
-    if (w.per_channel) qe_skinny::launch<qe_gemv::kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    if (w.q8) qe_skinny::launch<qe_gemv::kFmtQ8, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    else if (w.per_channel) qe_skinny::launch<qe_gemv::kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else qe_skinny::launch<qe_gemv::kFmtW8G, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }

@@ -47,7 +47,7 @@ def test_glu_rows8_bit_exact(dev):
     assert np.array_equal(dq.cpu().numpy(), rq) and np.array_equal(synth.bits(ds), rs)
 
 
-@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048)])
+@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048), (2048, 5120)])
 def test_gemv_q8_parity(dev, n, k):
     q, s, w = q8_host(n, k, n + k)
     wq = ops.repack_q8(synth.to_dev(q), synth.to_dev(s))
