@@ -266,33 +266,18 @@ __global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t*
     }
 }
 
-// Decode batches (T <= kDecTokens): route and segment in one block of min(T, 16) waves. The waves route tokens
-// w, w + nw, ... into LDS; after the one barrier wave 0 alone segments them (its LDS operations complete in order, so
-// it needs no further barrier): per-expert counts and 32-bit token masks by LDS atomics, the exclusive scans of the
-// counts and job counts with lane l owning experts PER l .. PER l + PER - 1, then each pair's slot = the expert's
-// offset + the number of earlier tokens on that expert. Same off / slots / jobs as moe_segment_kernel.
+// Decode batches (T <= kDecTokens), one wave segments the routed pairs (ssel / sw: T * topk, LDS or global): its
+// LDS operations complete in order, so it needs no barrier. Per-expert counts and 32-bit token masks by LDS atomics,
+// the exclusive scans of the counts and job counts with lane l owning experts PER l .. PER l + PER - 1, then each
+// pair's slot = the expert's offset + the number of earlier tokens on that expert. Same off / slots / jobs as
+// moe_segment_kernel. cnt / pre / mark: LDS [64 PER], cnt and mark zeroed by the caller.
 constexpr int kDecTokens = 32;
 template <int PER>
-__global__ void __launch_bounds__(kSegThreads) moe_route_segment_kernel(const float* __restrict__ logits, int T, int E,
-                                                                        int topk, int chunk, int32_t* __restrict__ off,
-                                                                        int32_t* __restrict__ slot_pair,
-                                                                        int32_t* __restrict__ slot_tok,
-                                                                        float* __restrict__ slot_w,
-                                                                        int32_t* __restrict__ inv,
-                                                                        int32_t* __restrict__ jobs,
-                                                                        int32_t* __restrict__ njobs) {
-    __shared__ int32_t ssel[kDecTokens * 16];
-    __shared__ float sw[kDecTokens * 16];
-    __shared__ int cnt[64 * PER], pre[64 * PER];
-    __shared__ unsigned mark[64 * PER];
-    const int tid = threadIdx.x, wv = tid >> 6, lane = tid & 63, nw = blockDim.x >> 6;
-    for (int e = tid; e < E; e += blockDim.x) {
-        cnt[e] = 0;
-        mark[e] = 0u;
-    }
-    for (int t = wv; t < T; t += nw) route_token<PER>(logits, t, E, topk, ssel + t * topk, sw + t * topk);
-    __syncthreads();
-    if (wv != 0) return;
+__device__ void seg_one_wave(const int32_t* ssel, const float* sw, int T, int E, int topk, int chunk, int* cnt,
+                             int* pre, unsigned* mark, int32_t* __restrict__ off, int32_t* __restrict__ slot_pair,
+                             int32_t* __restrict__ slot_tok, float* __restrict__ slot_w, int32_t* __restrict__ inv,
+                             int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
+    const int lane = threadIdx.x & 63;
     const int P = T * topk;
     for (int p = lane; p < P; p += 64) {
         const int e = ssel[p];
@@ -350,14 +335,71 @@ __global__ void __launch_bounds__(kSegThreads) moe_route_segment_kernel(const fl
     }
 }
 
-void launch_route_segment(const float* logits, int T, int E, int topk, int chunk, int32_t* off, int32_t* slot_pair,
-                          int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs, int32_t* njobs,
-                          hipStream_t st) {
+// T <= kDecRouteFused: route and segment in one block of T waves (routing into LDS, one barrier, wave 0 segments)
+constexpr int kDecRouteFused = 4;
+template <int PER>
+__global__ void __launch_bounds__(64 * kDecRouteFused) moe_route_segment_kernel(
+    const float* __restrict__ logits, int T, int E, int topk, int chunk, int32_t* __restrict__ off,
+    int32_t* __restrict__ slot_pair, int32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
+    int32_t* __restrict__ inv, int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
+    __shared__ int32_t ssel[kDecRouteFused * 16];
+    __shared__ float sw[kDecRouteFused * 16];
+    __shared__ int cnt[64 * PER], pre[64 * PER];
+    __shared__ unsigned mark[64 * PER];
+    const int tid = threadIdx.x, wv = tid >> 6;
+    for (int e = tid; e < E; e += blockDim.x) {
+        cnt[e] = 0;
+        mark[e] = 0u;
+    }
+    if (wv < T) route_token<PER>(logits, wv, E, topk, ssel + wv * topk, sw + wv * topk);
+    __syncthreads();
+    if (wv != 0) return;
+    seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs);
+}
+
+// kDecRouteFused < T <= kDecTokens: routed by moe_route_kernel (tokens over CUs: one CU routing 16+ tokens is
+// issue-bound), then this one-wave kernel segments sel / w
+template <int PER>
+__global__ void __launch_bounds__(64) moe_dec_segment_kernel(const int32_t* __restrict__ sel,
+                                                             const float* __restrict__ w, int T, int E, int topk,
+                                                             int chunk, int32_t* __restrict__ off,
+                                                             int32_t* __restrict__ slot_pair,
+                                                             int32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
+                                                             int32_t* __restrict__ inv, int32_t* __restrict__ jobs,
+                                                             int32_t* __restrict__ njobs) {
+    __shared__ int32_t ssel[kDecTokens * 16];
+    __shared__ float sw[kDecTokens * 16];
+    __shared__ int cnt[64 * PER], pre[64 * PER];
+    __shared__ unsigned mark[64 * PER];
+    const int lane = threadIdx.x;
+    for (int e = lane; e < E; e += 64) {
+        cnt[e] = 0;
+        mark[e] = 0u;
+    }
+    for (int p = lane; p < T * topk; p += 64) {
+        ssel[p] = sel[p];
+        sw[p] = w[p];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs);
+}
+
+void launch_route_segment(const float* logits, int T, int E, int topk, int chunk, int32_t* sel, float* w, int32_t* off,
+                          int32_t* slot_pair, int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs,
+                          int32_t* njobs, hipStream_t st) {
     const int per = (E + 63) / 64;
-    const unsigned threads = 64u * (unsigned)(T < 16 ? T : 16);
+    if (T > kDecRouteFused) launch_route(logits, T, E, topk, sel, w, st);
 #define QE_RS(PER_)                                                                                                 \
-    moe_route_segment_kernel<PER_><<<1, threads, 0, st>>>(logits, T, E, topk, chunk, off, slot_pair, slot_tok, slot_w, \
-                                                          inv, jobs, njobs)
+    do {                                                                                                            \
+        if (T <= kDecRouteFused)                                                                                    \
+            moe_route_segment_kernel<PER_><<<1, 64 * T, 0, st>>>(logits, T, E, topk, chunk, off, slot_pair, slot_tok, \
+                                                                 slot_w, inv, jobs, njobs);                         \
+        else                                                                                                        \
+            moe_dec_segment_kernel<PER_><<<1, 64, 0, st>>>(sel, w, T, E, topk, chunk, off, slot_pair, slot_tok,      \
+                                                           slot_w, inv, jobs, njobs);                               \
+    } while (0)
     if (per <= 1) QE_RS(1);
     else if (per <= 2) QE_RS(2);
     else if (per <= 4) QE_RS(4);
@@ -612,8 +654,8 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
 
     if (T > kDecTokens) launch_route(logits, T, E, topk, ws.sel, ws.w, st);
     if (T <= kDecTokens) {
-        launch_route_segment(logits, T, E, topk, chunk, ws.off, ws.slot_pair, ws.slot_tok, ws.slot_w, ws.inv, ws.jobs,
-                             ws.njobs, st);
+        launch_route_segment(logits, T, E, topk, chunk, ws.sel, ws.w, ws.off, ws.slot_pair, ws.slot_tok, ws.slot_w,
+                             ws.inv, ws.jobs, ws.njobs, st);
     } else if (T > kSegOneBlockTokens) {
         const int nchunk = (T + kSegChunk - 1) / kSegChunk;
         moe_seg_count_kernel<<<nchunk, kSegThreads, 0, st>>>(ws.sel, T, E, topk, ws.cntb);
