@@ -471,6 +471,97 @@ __global__ void __launch_bounds__(kSegThreads) moe_seg_place_kernel(const int32_
 // ------------------------------------------------------------------ decode grouped GEMVs (gemv_tile)
 constexpr int kDecRows = 2;  // rows per decode job
 
+// Matrix-core decode tile (W4, fp16 scales, slices of NG <= 8 groups, MT <= 4 gathered activation rows): the
+// arithmetic of the skinny GEMM kernel (skinny.hip) behind gemv_tile's interface. Lane 16 q + i holds A row i of the
+// 16-row tile (its half of the records (g = i % 8, t = q): t = (w >> 4 (i / 8)) & 0x0F0F0F0F, byte permutes with 0x43
+// give the bf16 pairs 128 + u) and B column i = activation row i (class-major staged activations, one ds_read_b128
+// per MFMA); the bias by one more MFMA with A = -136; acc += s * C per group. Activations, scales and every group's
+// records are loaded before any wait. Returns red in gemv_tile's layout [S][2][MT][16] (half 1 zero) for rsum().
+template <int MT, int NG>
+__device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __restrict__ qp,
+                                               const uint16_t* __restrict__ sp, const uint32_t* const* xw, int m,
+                                               size_t qgs, size_t sgs) {
+    static_assert(NG >= 1 && NG <= 8 && MT <= 4, "mfma_dec_tile");
+    constexpr int XS = 68;                       // staged activation rows XS dwords apart (disjoint bank groups)
+    constexpr int WSZ = NG * MT * XS + NG * 8;   // dwords per wave: xl [NG][MT][XS], scales [NG][16] half
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    uint32_t* xl = lds + (size_t)w * WSZ;
+    uint32_t* sl = xl + NG * MT * XS;
+    const uint16_t* sl16 = reinterpret_cast<const uint16_t*>(sl);
+    float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][2][MT][16]
+    const int qg = L >> 4, i = L & 15, g = i & 7, sh = 4 * (i >> 3);
+
+    // 1. loads: activation pieces p = L + 64 r (row p / (16 NG), group (p / 16) % NG, 16-byte chunk p % 16; rows
+    //    past m re-read row m - 1), the scale dword L (group L / 8), then the records of every group
+    constexpr int XL = MT * NG * 16, XR = (XL + 63) / 64;
+    u32x4_v xv[XR];
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const int p = L + 64 * r < XL ? L + 64 * r : XL - 1;
+        const int row = p / (16 * NG), gi = (p >> 4) % NG, ch = p & 15;
+        xv[r] = reinterpret_cast<const u32x4_v*>(xw[row < m ? row : m - 1] + gi * 64)[ch];
+    }
+    const int ls = L < NG * 8 ? L : NG * 8 - 1;
+    const uint32_t sraw = reinterpret_cast<const uint32_t*>(sp)[(size_t)(ls >> 3) * sgs + (ls & 7)];
+    u32x4_v wv[NG][2];
+#pragma unroll
+    for (int ii = 0; ii < NG; ii++)
+#pragma unroll
+        for (int c = 0; c < 2; c++) wv[ii][c] = ld_stream(qp + (size_t)ii * qgs + 32 * c + 4 * g + qg);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 2. staging: scales, activations class-major (x_slot)
+    if (L < NG * 8) sl[L] = sraw;
+#pragma unroll
+    for (int r = 0; r < XR; r++) {
+        const int p = L + 64 * r;
+        if (p < XL) {
+            const int row = p / (16 * NG), gi = (p >> 4) % NG, ch = p & 15;
+#pragma unroll
+            for (int c = 0; c < 4; c++) xl[(gi * MT + row) * XS + x_slot<kFmtW4>(4 * ch + c)] = xv[r][c];
+        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 3. per group: 4 k steps of a weight MFMA and a bias MFMA, then the group scale
+    const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
+    f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ii = 0; ii < NG; ii++) {
+        f32x4_v c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int mm = 0; mm < 4; mm++) {
+            u32x4_v b = *reinterpret_cast<const u32x4_v*>(
+                &xl[(ii * MT + (i < MT ? i : 0)) * XS + (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
+            b = i < MT ? b : u32x4_v{0u, 0u, 0u, 0u};
+            const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
+            const u32x4_v rec = wv[ii][mm >> 1];
+            const int j0 = 2 * (mm & 1);
+            const uint32_t t0 = (rec[j0] >> sh) & kNib, t1 = (rec[j0 + 1] >> sh) & kNib;
+            const u32x4_v a = {bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c, 0, 0, 0);
+        }
+        const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[ii * 16 + 4 * qg]);
+        acc[0] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.x & 0xffffu)), c[0], acc[0]);
+        acc[1] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.x >> 16)), c[1], acc[1]);
+        acc[2] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.y & 0xffffu)), c[2], acc[2]);
+        acc[3] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.y >> 16)), c[3], acc[3]);
+    }
+    // 4. lane (q, i < MT) holds rows 4 q .. 4 q + 3 of activation row i
+    if (i < MT) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            red[((w * 2) * MT + i) * 16 + 4 * qg + j] = acc[j];
+            red[((w * 2 + 1) * MT + i) * 16 + 4 * qg + j] = 0.f;
+        }
+    }
+    __syncthreads();
+    return red;
+}
+
 // gate_up: block (job, record g * 16 + 16-row tile); S = G / NG waves over K = H
 template <int MT, int NG>
 __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
@@ -492,7 +583,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
 #pragma unroll
     for (int r = 0; r < MT; r++)
         xw[r] = reinterpret_cast<const uint32_t*>(x + (size_t)slot_tok[slot0 + (r < m ? r : 0)] * sh.H) + gb * 64;
-    const float* red = gemv_tile<MT, kFmtW4, kScaleF16, NG, true>(lds, qp, sp, xw, m, NG, kScaleF16);
+    const float* red = mfma_dec_tile<MT, NG>(lds, qp, sp, xw, m, 64, 8);
     for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
         const int r = idx >> 3, gg = idx & 7;
         const float v = silu_f32(rsum<MT>(red, S, r, gg)) * rsum<MT>(red, S, r, gg + 8) * slot_w[slot0 + r];
@@ -519,8 +610,9 @@ __global__ void __launch_bounds__(64) moe_dec_down_kernel(
 #pragma unroll
     for (int r = 0; r < MT; r++)
         xw[r] = reinterpret_cast<const uint32_t*>(act + (size_t)(slot0 + (r < m ? r : 0)) * sh.I);
-    const float* red = gemv_tile<MT, kFmtW4, kScaleF16, NGRP, true>(lds, qp, sp, xw, m, NGRP, kScaleF16, sh.rec / 16,
-                                                                    sh.rec / 4);
+    const float* red = NGRP <= 8 ? mfma_dec_tile<MT, NGRP <= 8 ? NGRP : 8>(lds, qp, sp, xw, m, sh.rec / 16, sh.rec / 4)
+                                  : gemv_tile<MT, kFmtW4, kScaleF16, NGRP, true>(lds, qp, sp, xw, m, NGRP, kScaleF16,
+                                                                                 sh.rec / 16, sh.rec / 4);
     for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
         const int r = idx >> 4, rr = idx & 15;
         slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_bf16(rsum<MT>(red, 1, r, rr));
