@@ -763,10 +763,18 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     HIP_CHECK(hipGetLastError());
     if (decode) {
         const int G = H / 128;
-        const int ng = (G % 4 == 0 && G / 4 <= kMaxWaves) ? 4 : 8;
+        // gate_up K slices: 2-group slices (more, shorter waves) while the pairs are few (<= 64: a latency-bound
+        // launch), else 4 (measured, H = 2048: T = 1 21.0 -> 19.6 us at 2 groups, T = 16 58.4 -> 64.5 us)
+        const bool few = T * topk <= 64;
+        const int ng = (few && G % 2 == 0 && G / 2 <= kMaxWaves) ? 2 : (G % 4 == 0 && G / 4 <= kMaxWaves) ? 4 : 8;
         CHECK(G % ng == 0 && G / ng <= kMaxWaves, "moe decode H %d", H);
-        const size_t lds_gu = ng == 4 ? gemv_lds_bytes<kDecRows, 4, true>(G / 4) : gemv_lds_bytes<kDecRows, 8, true>(G / 8);
-        if (ng == 4)
+        const size_t lds_gu = ng == 2   ? gemv_lds_bytes<kDecRows, 2, true>(G / 2)
+                              : ng == 4 ? gemv_lds_bytes<kDecRows, 4, true>(G / 4)
+                                        : gemv_lds_bytes<kDecRows, 8, true>(G / 8);
+        if (ng == 2)
+            moe_dec_gate_up_kernel<kDecRows, 2><<<dim3(mj, sh.ngrp * 16), 64 * (G / 2), lds_gu, st>>>(
+                recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
+        else if (ng == 4)
             moe_dec_gate_up_kernel<kDecRows, 4><<<dim3(mj, sh.ngrp * 16), 64 * (G / 4), lds_gu, st>>>(
                 recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
         else
