@@ -274,7 +274,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
 #pragma unroll
                 for (int bb = 0; bb < WNT; bb++)
                     if (MODE == 0 || (alive >> a) & 1)
-                        acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[ks & 1][a], bfr[ks & 1][bb], acc[a][bb], 0, 0, 0);
+                        acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][bb], af[ks & 1][a], acc[a][bb], 0, 0, 0);
             store_part(ks);
         }
     };
@@ -338,40 +338,65 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         }
     }
 
-    // ---- epilogue: lane l holds column n = l % 32 of each 32 x 32 tile, rows 8 (r / 4) + 4 (l / 32) + r % 4
+    // ---- epilogue. The MFMAs take the W fragments as A and the X fragments as B, so each 32 x 32 tile holds C^T:
+    //      lane l holds token l % 32 and weight rows (output columns) 8 (r / 4) + 4 (l / 32) + r % 4, i.e. 4
+    //      consecutive output columns per r / 4 -> one 8-byte (bf16) or 16-byte (fp32) store, or scalar stores where
+    //      ldc / c are not aligned for them. GLU: gate row g and up row g + 8 of a 16-row tile are registers r and
+    //      r + 4 of the same lane.
     const int cj = lane & 31, ci = 4 * (lane >> 5);
+    const bool vec = MODE != 0 || ((ldc & 3) == 0 && ((uintptr_t)c & (out == kOutF32 ? 15u : 7u)) == 0);
+    auto st4 = [&](uint16_t* p, float v0, float v1, float v2, float v3) {  // 4 consecutive bf16
+        if (vec) {
+            *reinterpret_cast<uint2*>(p) = uint2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
+        } else {
+            p[0] = f32_to_bf16(v0);
+            p[1] = f32_to_bf16(v1);
+            p[2] = f32_to_bf16(v2);
+            p[3] = f32_to_bf16(v3);
+        }
+    };
 #pragma unroll
     for (int a = 0; a < WMT; a++)
 #pragma unroll
         for (int bb = 0; bb < WNT; bb++) {
-            const int n = n0 + wn * 32 * WNT + bb * 32 + cj;
+            const int tok = t0 + wm * 32 * WMT + a * 32 + cj;
+            if (tok >= T) continue;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int tok = t0 + wm * 32 * WMT + a * 32 + 8 * (r >> 2) + ci + (r & 3);
-                const float v = acc[a][bb][r];
-                if constexpr (MODE == 1) {
-                    // GLU (gate row g, up row g + 8 of the 16-row tile) times the slot's routing weight; the record's
-                    // 256 rows are act columns 128 nt .. + 128
-                    const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                        0, __builtin_bit_cast(int, v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
-                    if ((cj & 15) < 8 && tok < T)
-                        ma.out[(size_t)(slot0 + tok) * ma.I + nt * 128 + (n >> 4) * 8 + (cj & 7)] =
-                            f32_to_bf16(silu_f32(v) * up * ma.slot_w[slot0 + tok]);
-                    continue;
+            for (int rb = 0; rb < 4; rb++) {
+                const int n = n0 + wn * 32 * WNT + bb * 32 + 8 * rb + ci;  // first of the 4 columns
+                const f32x16_v& v = acc[a][bb];
+                const bool glu = MODE == 1 || (MODE == 0 && out == kOutGLU);
+                if (glu) {
+                    if (rb & 1) continue;  // rows 8 (rb + 1) + ..: the up rows of this gate block
+                    float g[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) g[j] = silu_f32(v[4 * rb + j]) * v[4 * rb + 4 + j];
+                    if constexpr (MODE == 1) {
+                        // the record's 256 GLU rows are act columns 128 nt .. + 128; times the slot's routing weight
+                        const float sw = ma.slot_w[slot0 + tok];
+                        st4(ma.out + (size_t)(slot0 + tok) * ma.I + nt * 128 + (n >> 4) * 8 + (n & 7), g[0] * sw,
+                            g[1] * sw, g[2] * sw, g[3] * sw);
+                    } else if (n < N) {
+                        st4(reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + (n >> 4) * 8 + (n & 7), g[0], g[1],
+                            g[2], g[3]);
+                    }
                 } else if constexpr (MODE == 2) {
-                    if (tok < T && n < N) ma.out[(size_t)(slot0 + tok) * ma.H + n] = f32_to_bf16(v);
-                    continue;
-                }
-                if (out == kOutGLU) {
-                    // gate = row g, up = row g + 8 of the 16-row tile: lanes j and j + 8
-                    const float up = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(
-                        0, __builtin_bit_cast(int, v), 0x128 /* row_ror:8 */, 0xF, 0xF, false));
-                    if ((cj & 15) < 8 && tok < T && n < N)
-                        reinterpret_cast<uint16_t*>(c)[(size_t)tok * ldc + (n >> 4) * 8 + (cj & 7)] =
-                            f32_to_bf16(silu_f32(v) * up);
-                } else if (tok < T && n < N) {
-                    if (out == kOutBF16) reinterpret_cast<uint16_t*>(c)[(size_t)tok * ldc + n] = f32_to_bf16(v);
-                    else reinterpret_cast<float*>(c)[(size_t)tok * ldc + n] = v;
+                    if (n < N)
+                        st4(ma.out + (size_t)(slot0 + tok) * ma.H + n, v[4 * rb], v[4 * rb + 1], v[4 * rb + 2],
+                            v[4 * rb + 3]);
+                } else if (n < N) {
+                    if (out == kOutBF16) {
+                        st4(reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + n, v[4 * rb], v[4 * rb + 1],
+                            v[4 * rb + 2], v[4 * rb + 3]);
+                    } else {
+                        float* p = reinterpret_cast<float*>(c) + (size_t)tok * ldc + n;
+                        if (vec) {
+                            *reinterpret_cast<f32x4_v*>(p) = f32x4_v{v[4 * rb], v[4 * rb + 1], v[4 * rb + 2], v[4 * rb + 3]};
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 4; j++) p[j] = v[4 * rb + j];
+                        }
+                    }
                 }
             }
         }

@@ -47,6 +47,25 @@ def test_gemm_w4_glu(dev):
     assert_glu_close(y, act, 1e-4)
 
 
+@pytest.mark.parametrize("glu", [False, True])
+def test_gemm_w4_strided_output(dev, glu):
+    """outputs written into a wider matrix at an odd offset and row stride (the epilogue's scalar stores) equal the
+    contiguous outputs (8- / 16-byte stores) bit for bit, for bf16, fp32 and GLU outputs"""
+    n, k, t = 512, 1024, 70
+    w, _, _ = setup(n, k, 1, seed=12, glu=glu)
+    x = synth.to_dev(synth.x_host(t, k, seed=13))
+    cols = n // 2 if glu else n
+    for out_bf16 in ((True,) if glu else (False, True)):
+        dt = torch.bfloat16 if (out_bf16 or glu) else torch.float32
+        want = ops.gemm_w4(w, x, out_bf16=out_bf16)
+        big = torch.full((t, cols + 7), float("nan"), dtype=dt, device=dev)
+        got = ops.gemm_w4(w, x, out_bf16=out_bf16, y=big[:, 1:1 + cols])
+        torch.cuda.synchronize()
+        iv = torch.int16 if dt == torch.bfloat16 else torch.int32
+        assert torch.equal(got.contiguous().view(iv), want.view(iv)), (glu, out_bf16)
+        assert torch.isnan(big[:, 0]).all() and torch.isnan(big[:, 1 + cols:]).all()
+
+
 def test_gemm_matches_gemv_rows(dev):
     """matmul dispatch: m <= 32 runs the GEMV, above the GEMM; both meet the gate on the same rows"""
     n, k = 1024, 2048
