@@ -65,7 +65,9 @@ constexpr int kXStride = 68;
 template <int MT, int NG, int RT>
 constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][kXStride], scales [RT][NGM][16] half
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
-    return (skinny_upx<MT, NG>() ? NGM : 2) * MT * kXStride + RT * NGM * 8;
+    constexpr int stage = (skinny_upx<MT, NG>() ? NGM : 2) * MT * kXStride + RT * NGM * 8;
+    // after its loop a wave writes its partial sums [RT][16][16] floats over its own (then dead) staging area
+    return stage > RT * 256 ? stage : RT * 256;
 }
 
 template <int MT, int SDT, int NG, int RT, int FMT, int D = skinny_d<MT, NG, RT, FMT>(),
@@ -84,7 +86,7 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     const int ng = NG > 0 ? NG : (w + 1) * G / S - gb;
     uint32_t* xl = lds + (size_t)w * WSZ;
     uint16_t* sl16 = reinterpret_cast<uint16_t*>(xl + (WSZ - RT * NGM * 8));
-    float* red = reinterpret_cast<float*>(lds + (size_t)S * WSZ);  // [S][RT][16 tok][16 rows]
+    float* red = reinterpret_cast<float*>(lds);  // wave w's [RT][16 tok][16 rows] at w * WSZ (its staging area)
 
     const int qg = L >> 4, i = L & 15;  // operand lane group, row / column within the tile
     const int g = i & 7, sh = 4 * (i >> 3);  // W4: nibble shift of row i's half (W8: byte pair 16 sh / 4)
@@ -290,13 +292,17 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     }
     }
 
-    // 2. slices through LDS in a fixed order: red[w][r][tok][row], lane (qg, i) holds rows 4 qg .. + 3 of column i
+    // 2. slices through LDS in a fixed order: wave w's sums over its own staging area (its last LDS reads come
+    //    first: a wave's LDS operations complete in order), lane (qg, i) holds rows 4 qg .. + 3 of column i
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int r = 0; r < RT; r++) *reinterpret_cast<f32x4_v*>(&red[((w * RT + r) * 16 + i) * 16 + 4 * qg]) = acc[r];
+    for (int r = 0; r < RT; r++) *reinterpret_cast<f32x4_v*>(&red[(size_t)w * WSZ + (r * 16 + i) * 16 + 4 * qg]) = acc[r];
     __syncthreads();
     auto rsum = [&](int r, int tok, int rr) {
         float v = 0.f;
-        for (int ws = 0; ws < S; ws++) v += red[((ws * RT + r) * 16 + tok) * 16 + rr];
+        for (int ws = 0; ws < S; ws++) v += red[(size_t)ws * WSZ + (r * 16 + tok) * 16 + rr];
         return v;
     };
     if (out == kOutGLU) {
@@ -325,20 +331,21 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     const Slicing sc = dg > 0 ? Slicing{dg, (k >> 7) / dg} : gemv_slicing(n, k);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
     const dim3 block(64 * sc.S);
-    // two tiles per wave (where n / 16 is even) at m in 5..8, and for the other m on grids of fewer than 16 waves
-    // per CU at one tile per wave. Measured (K = 5120): RT = 2 is 3 % (m = 16, 4, 2) slower on N = 17408 (8704
-    // waves), 3 % faster at m = 8, and 6 to 16 % faster on N = 5120 (2560 waves)
-    const bool rt2 = n % 32 == 0 && (mt == 8 || (long)(n / 16) * sc.S < 16L * qe_num_cus());
+    // two tiles per wave (where n / 16 is even) at m >= 5, and for m <= 4 on grids of fewer than 16 waves per CU at
+    // one tile per wave. Measured (K = 5120): RT = 2 is 3 % slower at m = 2, 4 on N = 17408 (8704 waves), 3 % faster
+    // at m = 8, 13 % faster at m = 16 (two blocks per CU since the partial sums reuse the staging LDS), and 6 to 16 %
+    // faster on N = 5120 (2560 waves)
+    const bool rt2 = n % 32 == 0 && (mt >= 8 || (long)(n / 16) * sc.S < 16L * qe_num_cus());
 #define QE_SK_K(MT_, NG_)                                                                                           \
     do {                                                                                                            \
         constexpr int RT_ = skinny_rt<MT_, NG_, FMT>();                                                             \
         if (RT_ == 2 && rt2)                                                                                        \
             skinny_kernel<MT_, SDT, NG_, RT_, FMT><<<dim3((unsigned)(n / (16 * RT_))), block,                       \
-                                         (size_t)sc.S * (skinny_wsz<MT_, NG_, RT_>() + 256 * RT_) * 4, st>>>(       \
+                                         (size_t)sc.S * skinny_wsz<MT_, NG_, RT_>() * 4, st>>>(                    \
                 q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                           \
         else                                                                                                        \
             skinny_kernel<MT_, SDT, NG_, 1, FMT><<<dim3((unsigned)(n / 16)), block,                                 \
-                                              (size_t)sc.S * (skinny_wsz<MT_, NG_, 1>() + 256) * 4, st>>>(         \
+                                              (size_t)sc.S * skinny_wsz<MT_, NG_, 1>() * 4, st>>>(                 \
                     q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                       \
     } while (0)
 #define QE_SK_NG(MT_)                             \
