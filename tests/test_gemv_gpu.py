@@ -196,6 +196,31 @@ def test_gemv_w4_baseline_shapes(dev, n, k, m):
     assert_bf16_close(y, oracle.matmul_bf16(xh, oracle.dequant_w4(q, s, n, k, 1)))
 
 
+@pytest.mark.parametrize("n,k", [(16, 128), (48, 384), (80, 640)])
+def test_gemv_small_odd_shapes(dev, n, k):
+    """one and an odd number of 16-row tiles (the skinny kernel's one-tile-per-wave fallback), one group, slices that
+    no even slicing divides (K / 128 = 3, 5), W4 and W8, every m"""
+    w, q, s = setup_w4(n, k, 1, seed=n * k)
+    xh = synth.x_host(16, k, seed=n + k)
+    x = synth.to_dev(xh)
+    ref = oracle_ref(xh, q, s, n, k, 1)
+    ref_ex = matmul_f64(xh, exact_w4(q, s, n, k, 1))
+    full = ops.gemv_w4(w, x)
+    torch.cuda.synchronize()
+    for m in range(1, 17):
+        y = ops.gemv_w4(w, x[:m])
+        torch.cuda.synchronize()
+        assert_bf16_close(out_f32(y), ref[:m])
+        assert err_ratio(y.cpu().numpy(), ref_ex[:m]) <= 1e-4, m
+        if m >= 2:
+            assert np.array_equal(y.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32)[:m]), m
+    q8, s8 = synth.w8_host(n, k, seed=n, per_channel=True)
+    w8 = ops.tile_w8(synth.to_dev(q8), synth.to_dev(s8, torch.float16), True)
+    ref8 = oracle_ref_w8(xh, q8, s8, n, k, True)
+    for m in (1, 2, 7, 16):
+        assert_bf16_close(out_f32(ops.gemv_w8(w8, x[:m], out_bf16=True)), ref8[:m])
+
+
 @pytest.mark.parametrize("n,k", [(20480, 5120), (20480, 8064)])
 def test_gemv_long_slices(dev, n, k):
     """K slices of more than 8 groups, whose scale dwords (and up-front activation pieces) outnumber a wave's 64

@@ -72,6 +72,14 @@ def test_moe_layer_small(dev, T):
     assert_bf16_close(y, ref)
 
 
+@pytest.mark.parametrize("T,E,topk", [(3, 100, 1), (7, 100, 16), (40, 1000, 16), (1, 1024, 8)])
+def test_moe_layer_expert_counts(dev, T, E, topk):
+    """expert counts that are not multiples of 64 (partial routing lanes), topk 1 and the maximum 16, up to 1024 experts,
+    the fused (T <= 4), split (T <= 32) and prefill routing paths"""
+    y, ref, *_ = _layer(dev, T, E=E, topk=topk, H=512, I=128, seed=T + E + topk)
+    assert_bf16_close(y, ref)
+
+
 @pytest.mark.parametrize("T,I", [(4, 1024), (4, 2048), (100, 2048)])
 def test_moe_layer_wide_intermediate(dev, T, I):
     """I = 1024 / 2048: the decode down GEMV runs K slices of 8 / 16 groups (16 groups: two rounds of activation
