@@ -35,14 +35,15 @@ using namespace qe_gemv;
 // in launch()); uneven slices (NG = 0) take RT = 1. Weight groups in flight per wave D and the occupancy hint
 // WPE, measured on the BASELINE shapes (K = 5120, 5-group slices; N = 5120 and 17408):
 //   RT = 2: D = 2 on slices of <= 5 groups (WPE 4: <= 128 VGPRs), else D = 3 (MT = 8: 2)
-//   RT = 1: D = 3 (MT = 8: 2, 6 waves per SIMD), WPE 6 at MT <= 4 on even slices of <= 5 groups
+//   RT = 1: D = 2 for MT <= 8 (MT = 2 / 4: 5 / 2.5 % faster than 3, 4 and 5 slower still), else 3; WPE 6 at
+//   MT <= 4 on even slices of <= 5 groups
 template <int MT, int NG, int FMT>
 constexpr int skinny_rt() {
     return NG == 0 || FMT != kFmtW4 ? 1 : 2;
 }
 template <int MT, int NG, int RT, int FMT>
 constexpr int skinny_d() {
-    constexpr int d = MT == 8 || FMT != kFmtW4 || (RT == 2 && NG > 0 && NG <= 5) ? 2 : 3;
+    constexpr int d = MT <= 8 || FMT != kFmtW4 || (RT == 2 && NG > 0 && NG <= 5) ? 2 : 3;
     return NG > 0 && NG < d ? NG : d;
 }
 template <int MT, int NG, int RT, int FMT>
