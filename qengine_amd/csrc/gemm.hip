@@ -226,6 +226,40 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         }
     };
 
+    // W8 (per-channel / group scales): lanes t = 0..3 of a quad hold the records (g, t) of one slab, dword d = k pairs
+    // 8 d + 2 t of rows g / g + 8. A 4 x 4 transpose across the quad (two rounds of DPP exchanges with lanes t ^ 2,
+    // then t ^ 1) gives lane t dword t of all four: the 8 consecutive k of chunk 4 slab + t of both rows, stored as
+    // two 16-byte chunks (instead of eight 4-byte stores). Record e is dequantized at step ks = e.
+    auto xpose4 = [&](u32x4_v v) {
+        const int t = lane & 3;
+        const bool b = (t & 2) != 0, c = (t & 1) != 0;
+        int r0 = __builtin_amdgcn_mov_dpp((int)(b ? v[0] : v[2]), 0x4E, 0xF, 0xF, false);  // quad_perm [2,3,0,1]
+        int r1 = __builtin_amdgcn_mov_dpp((int)(b ? v[1] : v[3]), 0x4E, 0xF, 0xF, false);
+        v = u32x4_v{b ? (uint32_t)r0 : v[0], b ? (uint32_t)r1 : v[1], b ? v[2] : (uint32_t)r0, b ? v[3] : (uint32_t)r1};
+        r0 = __builtin_amdgcn_mov_dpp((int)(c ? v[0] : v[1]), 0xB1, 0xF, 0xF, false);  // quad_perm [1,0,3,2]
+        r1 = __builtin_amdgcn_mov_dpp((int)(c ? v[2] : v[3]), 0xB1, 0xF, 0xF, false);
+        return u32x4_v{c ? (uint32_t)r0 : v[0], c ? v[1] : (uint32_t)r0, c ? (uint32_t)r1 : v[2], c ? v[3] : (uint32_t)r1};
+    };
+    auto store_w8x = [&](const WSet& ws, char* wtile, int e) {
+        if (!wactive || e >= WREC) return;
+        int tr, slab, wl;
+        rec_of(e, tr, slab, wl);
+        const int row = tr * 16 + (wl >> 2);
+        const float s_lo = scale_rt<SDT>(ws.sr_lo[e], sdt), s_hi = scale_rt<SDT>(ws.sr_hi[e], sdt);
+        const float b_lo = -128.f * s_lo, b_hi = -128.f * s_hi;
+        const u32x4_v tv = xpose4(ws.wr[e]);  // tv[t'] = dword (lane t) of record (g, t'): k 8 t + 2 t' (+1)
+        uint32_t lo[4], hi[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const uint32_t x = tv[u] ^ 0x80808080u;  // w + 128
+            lo[u] = pack_bf16x2(fmaf(cvt_ubyte<0>(x), s_lo, b_lo), fmaf(cvt_ubyte<1>(x), s_lo, b_lo));
+            hi[u] = pack_bf16x2(fmaf(cvt_ubyte<2>(x), s_hi, b_hi), fmaf(cvt_ubyte<3>(x), s_hi, b_hi));
+        }
+        const int ch = 4 * slab + (wl & 3);
+        *reinterpret_cast<u32x4_v*>(wtile + swz(row, ch)) = u32x4_v{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u32x4_v*>(wtile + swz(row + 8, ch)) = u32x4_v{hi[0], hi[1], hi[2], hi[3]};
+    };
+
     // ---- MFMA tiles: wave (wm, wn) owns tokens wm * 32 WMT .. , rows wn * 32 WNT ..
     const int wm = wave >> 2, wn = wave & 3;
     f32x16_v acc[WMT][WNT];
@@ -320,14 +354,20 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         if (KT > 1) load_w8(wsB, 1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int d = 0; d < 4; d++) store_w8(wsA, lds + BM * BK * 2, d);
+        for (int d = 0; d < 4; d++) {
+            if constexpr (FMT == kFmtQ8) store_w8(wsA, lds + BM * BK * 2, d);
+            else store_w8x(wsA, lds + BM * BK * 2, d);
+        }
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         auto step = [&](int kt, const WSet& cur, WSet& nxt_regs) {
             char* nxt = lds + ((kt + 1) & 1) * C::kStage;
             if (kt + 1 < KT) dma_x(kt + 1, ((kt + 1) & 1) * C::kStage);
             const bool more = kt + 1 < KT;
             mfma_step(kt, [&](int ks) {
-                if (more) store_w8(cur, nxt + BM * BK * 2, ks);
+                if (more) {
+                    if constexpr (FMT == kFmtQ8) store_w8(cur, nxt + BM * BK * 2, ks);
+                    else store_w8x(cur, nxt + BM * BK * 2, ks);
+                }
                 if (ks == 0 && kt + 2 < KT) load_w8(nxt_regs, kt + 2);  // after the first stores free no registers
             });
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
