@@ -211,25 +211,11 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             }
         }
     };
-    auto store_w8 = [&](const WSet& ws, char* wtile, int d) {  // dword d (0..3) of every record of this thread
-        if (!wactive) return;
-#pragma unroll
-        for (int e = 0; e < WREC; e++) {
-            int tr, slab, wl;
-            rec_of(e, tr, slab, wl);
-            const int wrow = tr * 16 + (wl >> 2), wt4 = wl & 3;
-            const float s_lo = scale_rt<SDT>(ws.sr_lo[e], sdt), s_hi = scale_rt<SDT>(ws.sr_hi[e], sdt);
-            if constexpr (FMT == kFmtQ8)  // word d = 2 s + hi: row + 8 hi, k 32 slab + 16 s + 2 t (+1, +8, +9)
-                dq_q8_word(ws.wr[e][d], (d & 1) ? s_hi : s_lo, wtile, wrow + 8 * (d & 1), 32 * slab + 16 * (d >> 1) + 2 * wt4);
-            else  // slab covers k 32 slab .. + 31; dword d: k step d / 2, half d % 2
-                dq_w8_dword(ws.wr[e][d], s_lo, s_hi, wtile, wrow, 32 * slab + 16 * (d >> 1) + 8 * (d & 1) + 2 * wt4);
-        }
-    };
-
-    // W8 (per-channel / group scales): lanes t = 0..3 of a quad hold the records (g, t) of one slab, dword d = k pairs
-    // 8 d + 2 t of rows g / g + 8. A 4 x 4 transpose across the quad (two rounds of DPP exchanges with lanes t ^ 2,
-    // then t ^ 1) gives lane t dword t of all four: the 8 consecutive k of chunk 4 slab + t of both rows, stored as
-    // two 16-byte chunks (instead of eight 4-byte stores). Record e is dequantized at step ks = e.
+    // Lanes t = 0..3 of a quad hold the records (g, t) of one 32-k slab. W8: dword d = the k pair 8 d + 2 t of rows
+    // g / g + 8; Q8: word d = row g + 8 (d % 2), bytes at k0 + {0, 8, 1, 9}, k0 = 16 (d / 2) + 2 t. A 4 x 4 transpose
+    // across the quad (two rounds of DPP exchanges with lanes t ^ 2, then t ^ 1) gives lane t dword / word t of all
+    // four, i.e. whole 8-k chunks, stored as 16-byte chunks (instead of eight 4-byte stores). Record e is dequantized
+    // at step ks = e.
     auto xpose4 = [&](u32x4_v v) {
         const int t = lane & 3;
         const bool b = (t & 2) != 0, c = (t & 1) != 0;
@@ -247,7 +233,24 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         const int row = tr * 16 + (wl >> 2);
         const float s_lo = scale_rt<SDT>(ws.sr_lo[e], sdt), s_hi = scale_rt<SDT>(ws.sr_hi[e], sdt);
         const float b_lo = -128.f * s_lo, b_hi = -128.f * s_hi;
-        const u32x4_v tv = xpose4(ws.wr[e]);  // tv[t'] = dword (lane t) of record (g, t'): k 8 t + 2 t' (+1)
+        const u32x4_v tv = xpose4(ws.wr[e]);  // tv[t'] = dword (lane t) of record (g, t')
+        if constexpr (FMT == kFmtQ8) {
+            // Q8 word 2 s + h: row g + 8 h, bytes at k0 + {0, 8, 1, 9}, k0 = 32 slab + 16 s + 2 t: lane t now holds
+            // word t of the quad, i.e. row g + 8 (t % 2) at chunks 4 slab + 2 (t / 2) (bytes 0, 2) and + 1 (bytes 1, 3)
+            const int t = wl & 3;
+            const float sc = (t & 1) ? s_hi : s_lo, bs = -128.f * sc;
+            uint32_t a[4], b[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const uint32_t x = tv[u] ^ 0x80808080u;  // w + 128
+                a[u] = pack_bf16x2(fmaf(cvt_ubyte<0>(x), sc, bs), fmaf(cvt_ubyte<2>(x), sc, bs));
+                b[u] = pack_bf16x2(fmaf(cvt_ubyte<1>(x), sc, bs), fmaf(cvt_ubyte<3>(x), sc, bs));
+            }
+            const int qrow = row + 8 * (t & 1), ch = 4 * slab + 2 * (t >> 1);
+            *reinterpret_cast<u32x4_v*>(wtile + swz(qrow, ch)) = u32x4_v{a[0], a[1], a[2], a[3]};
+            *reinterpret_cast<u32x4_v*>(wtile + swz(qrow, ch + 1)) = u32x4_v{b[0], b[1], b[2], b[3]};
+            return;
+        }
         uint32_t lo[4], hi[4];
 #pragma unroll
         for (int u = 0; u < 4; u++) {
@@ -354,20 +357,14 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         if (KT > 1) load_w8(wsB, 1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
-        for (int d = 0; d < 4; d++) {
-            if constexpr (FMT == kFmtQ8) store_w8(wsA, lds + BM * BK * 2, d);
-            else store_w8x(wsA, lds + BM * BK * 2, d);
-        }
+        for (int d = 0; d < 4; d++) store_w8x(wsA, lds + BM * BK * 2, d);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         auto step = [&](int kt, const WSet& cur, WSet& nxt_regs) {
             char* nxt = lds + ((kt + 1) & 1) * C::kStage;
             if (kt + 1 < KT) dma_x(kt + 1, ((kt + 1) & 1) * C::kStage);
             const bool more = kt + 1 < KT;
             mfma_step(kt, [&](int ks) {
-                if (more) {
-                    if constexpr (FMT == kFmtQ8) store_w8(cur, nxt + BM * BK * 2, ks);
-                    else store_w8x(cur, nxt + BM * BK * 2, ks);
-                }
+                if (more) store_w8x(cur, nxt + BM * BK * 2, ks);
                 if (ks == 0 && kt + 2 < KT) load_w8(nxt_regs, kt + 2);  // after the first stores free no registers
             });
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");

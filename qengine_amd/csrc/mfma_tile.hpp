@@ -56,29 +56,6 @@ __device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, 
     *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c0 + 1) + o0) = h8;
 }
 
-// one INT8 dword of the W8 layout: bytes (g, k) (g, k+1) (g+8, k) (g+8, k+1) -> bf16_rn(w * s)
-__device__ __forceinline__ void dq_w8_dword(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k) {
-    const uint32_t u = wd ^ 0x80808080u;  // w + 128
-    const float b_lo = -128.f * s_lo, b_hi = -128.f * s_hi;
-    const uint32_t g = pack_bf16x2(fmaf(cvt_ubyte<0>(u), s_lo, b_lo), fmaf(cvt_ubyte<1>(u), s_lo, b_lo));
-    const uint32_t h = pack_bf16x2(fmaf(cvt_ubyte<2>(u), s_hi, b_hi), fmaf(cvt_ubyte<3>(u), s_hi, b_hi));
-    const int c = k >> 3, o = (k & 7) * 2;
-    *reinterpret_cast<uint32_t*>(wt + swz(row, c) + o) = g;
-    *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c) + o) = h;
-}
-
-// one word of the Q8 layout: row `row` bytes (k0, k0 + 8, k0 + 1, k0 + 9) -> bf16_rn(w * s) pairs at (row, k0) and
-// (row, k0 + 8) of the tile
-__device__ __forceinline__ void dq_q8_word(uint32_t wd, float sc, char* wt, int row, int k0) {
-    const uint32_t u = wd ^ 0x80808080u;  // w + 128
-    const float b = -128.f * sc;
-    const uint32_t lo = pack_bf16x2(fmaf(cvt_ubyte<0>(u), sc, b), fmaf(cvt_ubyte<2>(u), sc, b));
-    const uint32_t hi = pack_bf16x2(fmaf(cvt_ubyte<1>(u), sc, b), fmaf(cvt_ubyte<3>(u), sc, b));
-    const int o = (k0 & 7) * 2;
-    *reinterpret_cast<uint32_t*>(wt + swz(row, k0 >> 3) + o) = lo;
-    *reinterpret_cast<uint32_t*>(wt + swz(row, (k0 >> 3) + 1) + o) = hi;
-}
-
 // 32x32 MFMA C fragment: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 for r = 0..15
 __device__ __forceinline__ int c_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 
