@@ -335,11 +335,13 @@ __device__ void seg_one_wave(const int32_t* ssel, const float* sw, int T, int E,
     }
 }
 
-// T <= kDecRouteFused: route and segment in one block of T waves (routing into LDS, one barrier, wave 0 segments)
+// T <= kDecRouteFused: route and segment in one block of T waves (routing into LDS, one barrier, wave 0 segments;
+// the routing is also stored to sel / w, which the fused decode down + combine kernel reads)
 constexpr int kDecRouteFused = 4;
 template <int PER>
 __global__ void __launch_bounds__(64 * kDecRouteFused) moe_route_segment_kernel(
-    const float* __restrict__ logits, int T, int E, int topk, int chunk, int32_t* __restrict__ off,
+    const float* __restrict__ logits, int T, int E, int topk, int chunk, int32_t* __restrict__ sel,
+    float* __restrict__ w, int32_t* __restrict__ off,
     int32_t* __restrict__ slot_pair, int32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
     int32_t* __restrict__ inv, int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
     __shared__ int32_t ssel[kDecRouteFused * 16];
@@ -353,6 +355,10 @@ __global__ void __launch_bounds__(64 * kDecRouteFused) moe_route_segment_kernel(
     }
     if (wv < T) route_token<PER>(logits, wv, E, topk, ssel + wv * topk, sw + wv * topk);
     __syncthreads();
+    for (int p = tid; p < T * topk; p += blockDim.x) {
+        sel[p] = ssel[p];
+        w[p] = sw[p];
+    }
     if (wv != 0) return;
     seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs);
 }
@@ -394,8 +400,8 @@ void launch_route_segment(const float* logits, int T, int E, int topk, int chunk
 #define QE_RS(PER_)                                                                                                 \
     do {                                                                                                            \
         if (T <= kDecRouteFused)                                                                                    \
-            moe_route_segment_kernel<PER_><<<1, 64 * T, 0, st>>>(logits, T, E, topk, chunk, off, slot_pair, slot_tok, \
-                                                                 slot_w, inv, jobs, njobs);                         \
+            moe_route_segment_kernel<PER_><<<1, 64 * T, 0, st>>>(logits, T, E, topk, chunk, sel, w, off, slot_pair,   \
+                                                                 slot_tok, slot_w, inv, jobs, njobs);               \
         else                                                                                                        \
             moe_dec_segment_kernel<PER_><<<1, 64, 0, st>>>(sel, w, T, E, topk, chunk, off, slot_pair, slot_tok,      \
                                                            slot_w, inv, jobs, njobs);                               \
@@ -619,6 +625,32 @@ __global__ void __launch_bounds__(64) moe_dec_down_kernel(
     }
 }
 
+// T * topk <= 64 (decode, few pairs), I / 128 <= 8: the down GEMV and the combine in one launch. Block (16-row tile
+// of H, token t) of topk waves; wave k multiplies expert sel[t, k]'s tile by act slot inv[t, k] over the whole K = I
+// (the tile of moe_dec_down_kernel with one activation row), and 16 lanes sum the waves' bf16-rounded slots in k
+// order in fp32: the values moe_dec_down_kernel + moe_combine_kernel produce, without the slot_out round trip.
+template <int NGRP>
+__global__ void __launch_bounds__(64 * 16) moe_dec_down_combine_kernel(
+    const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ act, const int32_t* __restrict__ sel,
+    const int32_t* __restrict__ inv, int topk, void* __restrict__ out, int out_bf16) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    const int tile = blockIdx.x, t = blockIdx.y, k = threadIdx.x >> 6;
+    const int e = sel[t * topk + k], slot = inv[t * topk + k];
+    const char* rp = rec_ptr(recs, sh, e, 0);
+    const uint4* qp = reinterpret_cast<const uint4*>(rp + sh.gg_q + sh.gg_s) + (size_t)tile * 2 * 32;
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q) + (size_t)tile * 16;
+    const uint32_t* xw[1] = {reinterpret_cast<const uint32_t*>(act + (size_t)slot * sh.I)};
+    const float* red = mfma_dec_tile<1, NGRP>(lds, qp, sp, xw, 1, sh.rec / 16, sh.rec / 4);
+    if (threadIdx.x < 16) {
+        const int rr = threadIdx.x;
+        float a = 0.f;
+        for (int kk = 0; kk < topk; kk++) a += bf16_to_f32(f32_to_bf16(rsum<1>(red + kk * 2 * 16, 1, 0, rr)));
+        const size_t o = (size_t)t * sh.H + tile * 16 + rr;
+        if (out_bf16) reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16(a);
+        else reinterpret_cast<float*>(out)[o] = a;
+    }
+}
+
 // ------------------------------------------------------------------ prefill grouped GEMMs
 // (expert, 128-row) jobs on the prefill GEMM's W4 pipeline: moe_pf_gemm in gemm.hip
 
@@ -781,6 +813,24 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
             moe_dec_gate_up_kernel<kDecRows, 8><<<dim3(mj, sh.ngrp * 16), 64 * (G / 8), lds_gu, st>>>(
                 recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
         HIP_CHECK(hipGetLastError());
+        if (few && sh.ngrp <= 8) {
+#define QE_DOWN_COMBINE(NGRP_)                                                                                 \
+    moe_dec_down_combine_kernel<NGRP_><<<dim3(H / 16, T), 64 * topk, gemv_lds_bytes<1, NGRP_, true>(topk), st>>>( \
+        recs, sh, ws.act, ws.sel, ws.inv, topk, out, (flags & QE_OUT_BF16) ? 1 : 0)
+            switch (sh.ngrp) {
+                case 1: QE_DOWN_COMBINE(1); break;
+                case 2: QE_DOWN_COMBINE(2); break;
+                case 3: QE_DOWN_COMBINE(3); break;
+                case 4: QE_DOWN_COMBINE(4); break;
+                case 5: QE_DOWN_COMBINE(5); break;
+                case 6: QE_DOWN_COMBINE(6); break;
+                case 7: QE_DOWN_COMBINE(7); break;
+                default: QE_DOWN_COMBINE(8); break;
+            }
+#undef QE_DOWN_COMBINE
+            HIP_CHECK(hipGetLastError());
+            return;
+        }
 #define QE_DOWN(NGRP_)                                                                                         \
     moe_dec_down_kernel<kDecRows, NGRP_><<<dim3(mj, H / 16), 64, gemv_lds_bytes<kDecRows, NGRP_, true>(1), st>>>( \
         recs, sh, ws.act, ws.off, ws.jobs, ws.njobs, ws.slot_out)
