@@ -88,6 +88,26 @@ def test_moe_layer_wide_intermediate(dev, T, I):
     assert_bf16_close(y, ref)
 
 
+def test_moe_decode_fused_down_combine_bit_exact(dev):
+    """T * topk <= 64 runs down + combine as one kernel, above that as two (down slots, then the k-order sum). With
+    H = 4096 both take the same gate_up K slicing, and every value is per (token, k), so the first 6 tokens of a
+    7-token call (70 pairs: two kernels) equal a 6-token call (60 pairs: fused) bit for bit, bf16 and fp32 out"""
+    E, topk, H, I = 16, 10, 4096, 256
+    gq, gs, dq, ds = synth.moe_host(E, H, I, seed=31)
+    moe = ops.MoE.pack(synth.to_dev(gq), synth.to_dev(gs, torch.float16), synth.to_dev(dq),
+                       synth.to_dev(ds, torch.float16), topk=topk)
+    lg = torch.from_numpy(synth.logits_host(7, E, seed=32)).to(dev)
+    x = synth.to_dev(synth.x_host(7, H, seed=33))
+    for out_bf16 in (True, False):
+        y7 = moe(lg, x, out_bf16=out_bf16)
+        y6 = moe(lg[:6].contiguous(), x[:6].contiguous(), out_bf16=out_bf16)
+        torch.cuda.synchronize()
+        iv = torch.int16 if out_bf16 else torch.int32
+        assert torch.equal(y6.view(iv), y7[:6].contiguous().view(iv)), out_bf16
+    y1, ref, *_ = _layer(dev, 6, E=E, topk=topk, H=H, I=I, seed=34)
+    assert_bf16_close(y1, ref)
+
+
 def pipeline_ref(lg, xh, gq, gs, dq, ds, topk, H, I):
     """this build's layer numerics on the oracle's bf16-dequantized experts (float64 products): act =
     bf16(silu(gate) up w_k) (gate_up epilogue), slot = bf16(down . act) (down epilogue), out = bf16 of the fp32 sum
