@@ -161,7 +161,8 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
 
 /* load time: compressed-tensors experts -> group records (reference loader, src/flash/flash.cu:1555-1611).
  * gate_up int32 [E][2I][H/8] (gate rows then up rows) + fp16 [E][2I][H/128]; down int32 [E][H][I/8] + fp16
- * [E][H][I/128]; records: E * qe_moe_record_bytes(H, I) bytes. Synchronizes the stream. */
+ * [E][H][I/128]; records: E * qe_moe_record_bytes(H, I) bytes. One kernel on `stream` (stream-ordered, no
+ * allocation, no synchronization). */
 void qe_moe_pack_w4(const int32_t* gu_q, const uint16_t* gu_s, const int32_t* dn_q, const uint16_t* dn_s, int E, int H,
                     int I, void* records, void* stream);
 

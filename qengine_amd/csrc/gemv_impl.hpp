@@ -413,14 +413,14 @@ void launch_gemv(const uint4* q, const uint16_t* s, int n, int k, const uint16_t
     const Slicing sc = gemv_slicing(n, k);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
     const int ngm = sc.ng > 0 ? sc.ng : kGenericNG;
-    // activation prefetch registers; the up-front staging of even slices loads 16-byte pieces of x
+    // activation prefetch registers; the up-front staging of even slices loads 16-byte pieces of x, so it needs
+    // 16-byte aligned rows. The template launched follows pf, and its LDS is sized by that same template.
     const bool aligned = ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
     const bool pf = mt * ngm <= 16 && (aligned || sc.ng == 0);
-    const int xg = pf && sc.ng > 0 ? sc.ng : 1;  // activation groups staged at once (gemv_tile's XG)
-    const size_t lds = (size_t)sc.S * (xg * mt * 72 + ngm * 8) * 4 + (size_t)sc.S * 2 * mt * 16 * 4;  // gemv_lds_bytes
     const dim3 grid((unsigned)(n / 16)), block(64 * sc.S);
-#define QE_GEMV_K(MT_, NG_, PF_) \
-    gemv_kernel<MT_, FMT, SDT, NG_, PF_><<<grid, block, lds, st>>>(q, s, n, k, x, ldx, y, ldy, m, out, sdt)
+#define QE_GEMV_K(MT_, NG_, PF_)                                                                          \
+    gemv_kernel<MT_, FMT, SDT, NG_, PF_><<<grid, block, gemv_lds_bytes<MT_, NG_, PF_>(sc.S), st>>>( \
+        q, s, n, k, x, ldx, y, ldy, m, out, sdt)
 #define QE_GEMV_NG(MT_, PF_)                         \
     do {                                             \
         if (sc.ng == 8) QE_GEMV_K(MT_, 8, PF_);      \
@@ -428,16 +428,17 @@ void launch_gemv(const uint4* q, const uint16_t* s, int n, int k, const uint16_t
         else if (sc.ng == 2) QE_GEMV_K(MT_, 2, PF_); \
         else QE_GEMV_K(MT_, 0, PF_);                 \
     } while (0)
-    if (mt == 1) QE_GEMV_NG(1, true);
-    else if (mt == 2) QE_GEMV_NG(2, true);
-    else if (mt == 4) {
-        if (pf) QE_GEMV_NG(4, true);
-        else QE_GEMV_NG(4, false);
-    } else if (mt == 8) {
-        QE_GEMV_NG(8, false);
-    } else {
-        QE_GEMV_NG(16, false);
-    }
+#define QE_GEMV_PF(MT_)                 \
+    do {                                \
+        if (pf) QE_GEMV_NG(MT_, true);  \
+        else QE_GEMV_NG(MT_, false);    \
+    } while (0)
+    if (mt == 1) QE_GEMV_PF(1);
+    else if (mt == 2) QE_GEMV_PF(2);
+    else if (mt == 4) QE_GEMV_PF(4);
+    else if (mt == 8) QE_GEMV_NG(8, false);  // mt = 8 / 16: activations loaded per group
+    else QE_GEMV_NG(16, false);
+#undef QE_GEMV_PF
 #undef QE_GEMV_NG
 #undef QE_GEMV_K
     HIP_CHECK(hipGetLastError());

@@ -20,7 +20,6 @@
 #include "gemv_impl.hpp"
 #include "../../include/qe_kernels.h"
 
-#include <vector>
 
 namespace {
 
@@ -690,6 +689,98 @@ __global__ void moe_combine_kernel(const uint16_t* __restrict__ slot_out, const 
     }
 }
 
+// ------------------------------------------------------------------ record packer (load time)
+// One thread per 32-bit word of the records (expert-major, record e * NGRP + g). A record is four parts:
+//   gq: the group's 256 gate/up rows (record row dr of 16-row tile dr / 16: rows 0..7 of the tile are gate row
+//       128 g + 8 tile + j, rows 8..15 the matching up rows I + 128 g + 8 tile + j - 8) in the W4 fragment layout
+//       (u32 idx: k-step idx % 4, lane (idx / 4) % 32, chunk idx / 128 = tile * (H / 64) + 64-k chunk; nibble slot
+//       s = rowhalf + 2 khalf + 4 odd holds (row 16 tile + lane / 4 + 8 rowhalf, k = 64 c + 16 j + 2 (lane % 4) +
+//       8 khalf + odd)), the same map as repack_w4 after the GLU interleave;
+//   gs: their fp16 scales [16][H / 128][16];
+//   dq: the expert's H down rows restricted to columns 128 g .. 128 g + 127, W4 fragment layout (K = 128);
+//   ds: their scales [H / 16][16] (one group).
+__device__ __forceinline__ uint32_t pack_nibbles(const int32_t* __restrict__ src, size_t wpr, int row, int k0) {
+    // slots: (row, k0) (row + 8, k0) (row, k0 + 8) (row + 8, k0 + 8) (row, k0 + 1) ... ; k0 even, so k0 / k0 + 1
+    // share a source word and k0 + 8 / k0 + 9 the next one
+    const int w0 = k0 >> 3, sh = 4 * (k0 & 7);
+    const uint32_t a0 = (uint32_t)src[(size_t)row * wpr + w0], a1 = (uint32_t)src[(size_t)row * wpr + w0 + 1];
+    const uint32_t b0 = (uint32_t)src[(size_t)(row + 8) * wpr + w0], b1 = (uint32_t)src[(size_t)(row + 8) * wpr + w0 + 1];
+    uint32_t word = 0;
+    const uint32_t ra[2] = {a0, a1}, rb[2] = {b0, b1};
+#pragma unroll
+    for (int sl = 0; sl < 8; sl++) {
+        const int rowhalf = sl & 1, khalf = (sl >> 1) & 1, odd = sl >> 2;
+        const uint32_t v = ((rowhalf ? rb[khalf] : ra[khalf]) >> (sh + 4 * odd)) & 15u;
+        word |= v << (4 * sl);
+    }
+    return word;
+}
+
+// the gq part with the GLU interleave: source row of record row dr (rows of the expert's [2I] gate/up matrix)
+__device__ __forceinline__ int glu_src_row(int dr, int g, int I) {
+    const int tile = dr >> 4, j = dr & 15;
+    return j < 8 ? 128 * g + 8 * tile + j : I + 128 * g + 8 * tile + (j - 8);
+}
+
+__global__ void __launch_bounds__(256) moe_pack_kernel(const int32_t* __restrict__ gu_q, const uint16_t* __restrict__ gu_s,
+                                                       const int32_t* __restrict__ dn_q,
+                                                       const uint16_t* __restrict__ dn_s, MoeShape sh,
+                                                       uint32_t* __restrict__ out) {
+    const size_t rw = sh.rec / 4;  // words per record
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)sh.E * sh.ngrp * rw) return;
+    const size_t recn = idx / rw;
+    const int e = (int)(recn / sh.ngrp), g = (int)(recn % sh.ngrp);
+    size_t wi = idx - recn * rw;  // word inside the record
+    const int H = sh.H, I = sh.I, GH = H / 128;
+    const size_t gq_w = sh.gg_q / 4, gs_w = sh.gg_s / 4, dq_w = sh.gd_q / 4;
+    uint32_t word;
+    if (wi < gq_w) {
+        const int j = (int)(wi & 3), lane = (int)((wi >> 2) & 31);
+        const size_t chunk = wi >> 7;
+        const int chunks = H >> 6;
+        const int r = (int)(chunk / chunks), c = (int)(chunk % chunks);
+        const int dr = 16 * r + (lane >> 2);  // record row (rows dr and dr + 8 of the tile)
+        const int k0 = 64 * c + 16 * j + 2 * (lane & 3);
+        // rows dr and dr + 8 of a tile map to gate row 8 tile + j and up row 8 tile + j: both read their own source
+        const int sa = glu_src_row(dr, g, I), sb = glu_src_row(dr + 8, g, I);
+        const int32_t* src = gu_q + (size_t)e * 2 * I * (H / 8);
+        const size_t wpr = H / 8;
+        const int w0 = k0 >> 3, shf = 4 * (k0 & 7);
+        const uint32_t ra[2] = {(uint32_t)src[(size_t)sa * wpr + w0], (uint32_t)src[(size_t)sa * wpr + w0 + 1]};
+        const uint32_t rb[2] = {(uint32_t)src[(size_t)sb * wpr + w0], (uint32_t)src[(size_t)sb * wpr + w0 + 1]};
+        word = 0;
+#pragma unroll
+        for (int sl = 0; sl < 8; sl++) {
+            const int rowhalf = sl & 1, khalf = (sl >> 1) & 1, odd = sl >> 2;
+            word |= (((rowhalf ? rb[khalf] : ra[khalf]) >> (shf + 4 * odd)) & 15u) << (4 * sl);
+        }
+    } else if ((wi -= gq_w) < gs_w) {
+        // two consecutive 16-bit scales [tile][gi][i], i even
+        const size_t h0 = 2 * wi;
+        const int i = (int)(h0 & 15), gi = (int)((h0 >> 4) % GH), r = (int)((h0 >> 4) / GH);
+        const uint16_t* ss = gu_s + (size_t)e * 2 * I * GH;
+        const uint32_t v0 = ss[(size_t)glu_src_row(16 * r + i, g, I) * GH + gi];
+        const uint32_t v1 = ss[(size_t)glu_src_row(16 * r + i + 1, g, I) * GH + gi];
+        word = v0 | (v1 << 16);
+    } else if ((wi -= gs_w) < dq_w) {
+        // down rows, the group's 128 columns: K = 128 (two 64-k chunks per tile)
+        const int j = (int)(wi & 3), lane = (int)((wi >> 2) & 31);
+        const size_t chunk = wi >> 7;
+        const int r = (int)(chunk >> 1), c = (int)(chunk & 1);
+        const int row = 16 * r + (lane >> 2);
+        const int k0 = 128 * g + 64 * c + 16 * j + 2 * (lane & 3);  // column of the expert's [H][I] down matrix
+        word = pack_nibbles(dn_q + (size_t)e * H * (I / 8), I / 8, row, k0);
+    } else {
+        wi -= dq_w;
+        const size_t h0 = 2 * wi;  // scale [tile][i] of rows 16 tile + i, i + 1: column group g
+        const int GI = I / 128;
+        const uint16_t* ss = dn_s + (size_t)e * H * GI;
+        word = (uint32_t)ss[h0 * GI + g] | ((uint32_t)ss[(h0 + 1) * GI + g] << 16);
+    }
+    out[idx] = word;
+}
+
 // ------------------------------------------------------------------ workspace layout
 struct MoeWs {
     int32_t *sel, *off, *slot_pair, *slot_tok, *inv, *jobs, *njobs, *cntb;
@@ -762,13 +853,15 @@ size_t qe_moe_workspace_bytes(int T, int E, int topk, int H, int I) {
 
 size_t qe_moe_record_bytes(int H, int I) { return moe_shape(1, 1, H, I).rec * (size_t)(I / 128); }
 
-void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
-               void* out, int flags, void* workspace, size_t ws_bytes, void* stream) {
-    moe_check(T, E, topk, H, I);
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+}  // extern "C"
+
+namespace {
+
+// the layer on a workspace of moe_ws(T, ...).bytes at `workspace` (checked by the callers)
+void moe_run(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
+             void* out, int flags, void* workspace, hipStream_t st) {
     const MoeShape sh = moe_shape(E, topk, H, I);
     const MoeWs ws = moe_ws(workspace, T, E, topk, H, I);
-    CHECK(workspace && ws_bytes >= ws.bytes, "moe workspace %zu < %zu bytes", ws_bytes, ws.bytes);
     CHECK(((uintptr_t)x & 15) == 0 && ((uintptr_t)out & 15) == 0 && ((uintptr_t)workspace & 255) == 0,
           "moe x / out 16-byte, workspace 256-byte alignment");
     const char* recs = reinterpret_cast<const char*>(records);
@@ -875,54 +968,33 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     HIP_CHECK(hipGetLastError());
 }
 
+}  // namespace
+
+extern "C" {
+
+void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
+               void* out, int flags, void* workspace, size_t ws_bytes, void* stream) {
+    moe_check(T, E, topk, H, I);
+    const size_t need = moe_ws(nullptr, T, E, topk, H, I).bytes;
+    CHECK(workspace && ws_bytes >= need, "moe workspace %zu < %zu bytes", ws_bytes, need);
+    moe_run(logits, x, records, T, E, topk, H, I, out, flags, workspace, reinterpret_cast<hipStream_t>(stream));
+}
+
 // compressed-tensors experts -> group records. gate_up: int32 [E][2I][H/8] (rows gate 0..I then up 0..I), fp16
 // scales [E][2I][H/128]; down: int32 [E][H][I/8], fp16 scales [E][H][I/128]. The reference's loader does the same
 // per group (flash.cu:1555-1611): gather the group's gate/up rows, GLU-interleave, repack; gather the group's down
-// columns, repack.
+// columns, repack. Here one kernel writes every 32-bit word of every record straight from the source tensors
+// (moe_pack_kernel): no staging copies, no allocation, no host synchronization (stream-ordered like any kernel).
 void qe_moe_pack_w4(const int32_t* gu_q, const uint16_t* gu_s, const int32_t* dn_q, const uint16_t* dn_s, int E, int H,
                     int I, void* records, void* stream) {
     moe_check(1, E, 1, H, I);
-    hipStream_t st = reinterpret_cast<hipStream_t>(stream);
     const MoeShape sh = moe_shape(E, 1, H, I);
-    int32_t *tq, *tq2;
-    uint16_t *ts, *ts2;
-    HIP_CHECK(hipMalloc(&tq, (size_t)256 * H / 2));
-    HIP_CHECK(hipMalloc(&tq2, (size_t)256 * H / 2));
-    HIP_CHECK(hipMalloc(&ts, (size_t)256 * (H / 128) * 2));
-    HIP_CHECK(hipMalloc(&ts2, (size_t)256 * (H / 128) * 2));
-    int32_t* dq;
-    uint16_t* dsc;
-    HIP_CHECK(hipMalloc(&dq, (size_t)H * 64));
-    HIP_CHECK(hipMalloc(&dsc, (size_t)H * 2));
-    char* recs = reinterpret_cast<char*>(records);
-    const size_t gwpr = H / 8, gspr = H / 128, dwpr = I / 8, dspr = I / 128;
-    for (int e = 0; e < E; e++)
-        for (int g = 0; g < sh.ngrp; g++) {
-            char* rp = recs + ((size_t)e * sh.ngrp + g) * sh.rec;
-            const int32_t* gq = gu_q + (size_t)e * 2 * I * gwpr;
-            const uint16_t* gs = gu_s + (size_t)e * 2 * I * gspr;
-            HIP_CHECK(hipMemcpyAsync(tq, gq + (size_t)g * 128 * gwpr, 128 * gwpr * 4, hipMemcpyDeviceToDevice, st));
-            HIP_CHECK(hipMemcpyAsync(tq + 128 * gwpr, gq + ((size_t)I + g * 128) * gwpr, 128 * gwpr * 4,
-                                     hipMemcpyDeviceToDevice, st));
-            HIP_CHECK(hipMemcpyAsync(ts, gs + (size_t)g * 128 * gspr, 128 * gspr * 2, hipMemcpyDeviceToDevice, st));
-            HIP_CHECK(hipMemcpyAsync(ts + 128 * gspr, gs + ((size_t)I + g * 128) * gspr, 128 * gspr * 2,
-                                     hipMemcpyDeviceToDevice, st));
-            glu_interleave_rows(tq, ts, 256, H, tq2, ts2, st, 4);
-            repack_w4(tq2, ts2, 256, H, reinterpret_cast<uint4*>(rp), reinterpret_cast<uint16_t*>(rp + sh.gg_q), st);
-            const int32_t* eq = dn_q + (size_t)e * H * dwpr;
-            const uint16_t* es = dn_s + (size_t)e * H * dspr;
-            HIP_CHECK(hipMemcpy2DAsync(dq, 64, eq + g * 16, dwpr * 4, 64, H, hipMemcpyDeviceToDevice, st));
-            HIP_CHECK(hipMemcpy2DAsync(dsc, 2, es + g, dspr * 2, 2, H, hipMemcpyDeviceToDevice, st));
-            repack_w4(dq, dsc, H, 128, reinterpret_cast<uint4*>(rp + sh.gg_q + sh.gg_s),
-                      reinterpret_cast<uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q), st);
-        }
-    HIP_CHECK(hipStreamSynchronize(st));
-    HIP_CHECK(hipFree(tq));
-    HIP_CHECK(hipFree(tq2));
-    HIP_CHECK(hipFree(ts));
-    HIP_CHECK(hipFree(ts2));
-    HIP_CHECK(hipFree(dq));
-    HIP_CHECK(hipFree(dsc));
+    const size_t words = (size_t)E * sh.ngrp * (sh.rec / 4);
+    const unsigned blocks = (unsigned)((words + 255) / 256);
+    CHECK(sh.rec % 4 == 0 && blocks > 0, "moe_pack: record of %zu bytes", sh.rec);
+    moe_pack_kernel<<<blocks, 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(gu_q, gu_s, dn_q, dn_s, sh,
+                                                                               reinterpret_cast<uint32_t*>(records));
+    HIP_CHECK(hipGetLastError());
 }
 
 }  // extern "C"

@@ -210,6 +210,7 @@ class MoE:
     def __init__(self, records, E, topk, H, I):
         self.records, self.E, self.topk, self.H, self.I = records, E, topk, H, I
         self._ws = None
+        self._old_ws = []  # outgrown workspaces stay alive: a captured HIP graph may still point at them
 
     @staticmethod
     def pack(gu_q, gu_s, dn_q, dn_s, topk):
@@ -228,6 +229,8 @@ class MoE:
         lib().qe_moe_workspace_bytes.restype = ctypes.c_size_t
         nb = lib().qe_moe_workspace_bytes(T, self.E, self.topk, self.H, self.I)
         if self._ws is None or self._ws.numel() < nb:
+            if self._ws is not None:
+                self._old_ws.append(self._ws)
             self._ws = torch.empty(nb, dtype=torch.uint8, device=self.records.device)
         return self._ws, nb
 

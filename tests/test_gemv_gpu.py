@@ -286,3 +286,41 @@ def test_gemv_w8_reference_hook(dev):
         torch.cuda.synchronize()
         ref = oracle.bf16_to_f32(xh).astype(np.float64) @ wref.T
         assert ref_gate(y.cpu().numpy(), ref) < 1e-2
+
+
+def _unaligned_rows(xh, mode):
+    """x rows whose start is not 16-byte aligned: 'offset' = the block starts 2 elements into its allocation (row
+    stride k), 'stride' = rows k + 2 elements apart (aligned start)"""
+    m, k = xh.shape
+    xd = synth.to_dev(xh)
+    if mode == "offset":
+        buf = torch.empty(m * k + 2, dtype=torch.bfloat16, device=xd.device)
+        x = buf[2:].view(m, k)
+    else:
+        buf = torch.empty(m, k + 2, dtype=torch.bfloat16, device=xd.device)
+        x = buf[:, :k]
+    x.copy_(xd)
+    assert x.data_ptr() % 16 != 0 or x.stride(0) % 8 != 0
+    return x
+
+
+@pytest.mark.parametrize("mode", ["offset", "stride"])
+@pytest.mark.parametrize("n,k", [(1024, 5120), (256, 1280)])
+def test_gemv_unaligned_activations(dev, mode, n, k):
+    """activation rows that are only 4-byte aligned take the VALU GEMV (even K slices, every group's activations
+    staged at once for m = 1 / 2): W4 and W8 against the oracle"""
+    w, q, s = setup_w4(n, k, 1, seed=n + 3 * k)
+    xh = synth.x_host(2, k, seed=k + 7)
+    x = _unaligned_rows(xh, mode)
+    ref_ex = matmul_f64(xh, exact_w4(q, s, n, k, 1))
+    for m in (1, 2):
+        y = ops.gemv_w4(w, x[:m])
+        torch.cuda.synchronize()
+        assert err_ratio(y.cpu().numpy(), ref_ex[:m]) <= 1e-4, (mode, m)
+    q8, s8 = synth.w8_host(n, k, seed=n + k, per_channel=True)
+    w8 = ops.tile_w8(synth.to_dev(q8), synth.to_dev(s8, torch.float16), True)
+    ref8 = matmul_f64(xh, exact_w8(q8, s8, n, k, True))
+    for m in (1, 2):
+        y = ops.gemv_w8(w8, x[:m])
+        torch.cuda.synchronize()
+        assert err_ratio(y.cpu().numpy(), ref8[:m]) <= 1e-4, (mode, m)
