@@ -32,8 +32,9 @@ int qe_abi_version(void);
 
 /* ---- reference-named hooks (src/capi.cpp): bf16 scales, fp32 outputs, default stream ---- */
 
-/* Library workspaces of the current device (split-K partials + counters); call once per device before any
- * graph capture. Replaces gemv_workspace_init, reference src/capi.cpp:131 / gemv.cuh:51. */
+/* Library set-up for the current device (CU count, the address of the device's scratch array used by
+ * qe_moe_w4_noalloc); call once per device before any graph capture. Replaces gemv_workspace_init, reference
+ * src/capi.cpp:131 / gemv.cuh:51. */
 void qe_gemv_workspace_init(void);
 
 /* compressed-tensors int32 [n][k/8] (nibbles LSB first, u = w + 8) + scales [n][k/128] -> W4 layout
@@ -158,6 +159,15 @@ size_t qe_moe_record_bytes(int H, int I);
  * top-k experts e of each token; logits fp32 [T][E], x bf16 [T][H]. H % 512 == 0, I % 128 == 0. */
 void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
                void* out, int flags, void* workspace, size_t ws_bytes, void* stream);
+
+/* allocation-free qe_moe_w4: no counterpart in the reference. For callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc): the workspace is the
+ * library's own per-device scratch array of QE_MOE_SCRATCH_BYTES (held by every GPU that loads the library until the
+ * process ends). Sizes whose qe_moe_workspace_bytes exceeds it are rejected (abort with a message). Calls on one GPU
+ * share the array: calls that overlap on one GPU (two streams) race. Nothing in it needs clearing between calls. */
+#define QE_MOE_SCRATCH_BYTES (8 << 20)
+void qe_moe_w4_noalloc(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H,
+                       int I, void* out, int flags, void* stream);
 
 /* load time: compressed-tensors experts -> group records (reference loader, src/flash/flash.cu:1555-1611).
  * gate_up int32 [E][2I][H/8] (gate rows then up rows) + fp16 [E][2I][H/128]; down int32 [E][H][I/8] + fp16

@@ -51,7 +51,10 @@ extern "C" {
 int qe_abi_version(void) { return QE_ABI_VERSION; }
 
 // ---------------------------------------------------------------- reference-named hooks
-void qe_gemv_workspace_init(void) { gemv_workspace_init(); }
+void qe_gemv_workspace_init(void) {
+    gemv_workspace_init();
+    moe_scratch_ptr();  // the device's scratch address, resolved at set-up rather than on the first no-alloc call
+}
 
 void qe_repack_w4(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds) {
     repack_w4(q, s, n, k, reinterpret_cast<uint4*>(dq), reinterpret_cast<uint16_t*>(ds), 0);

@@ -20,6 +20,7 @@
 #include "gemv_impl.hpp"
 #include "../../include/qe_kernels.h"
 
+#include <mutex>
 
 namespace {
 
@@ -968,7 +969,31 @@ void moe_run(const float* logits, const uint16_t* x, const void* records, int T,
     HIP_CHECK(hipGetLastError());
 }
 
+// ---- the allocation-free variant's workspace: one file-scope device array per GPU (each device that loads the
+// library holds its own copy until the process ends). Host code never uses the array's name as a device address:
+// its address on each device comes from hipGetSymbolAddress, taken once per device with that device current.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
 }  // namespace
+
+static __device__ __align__(256) unsigned char scratch[QE_MOE_SCRATCH_BYTES];
+
+// address of `scratch` on the current device (resolved and kept on the device's first use)
+void* moe_scratch_ptr() {
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    CHECK(dev >= 0 && dev < kMaxDevices, "device %d", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (g_scratch_ptr[dev] == nullptr) {
+        void* p = nullptr;
+        HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        CHECK(p != nullptr && ((uintptr_t)p & 255) == 0, "scratch address");
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
 
 extern "C" {
 
@@ -978,6 +1003,16 @@ void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int 
     const size_t need = moe_ws(nullptr, T, E, topk, H, I).bytes;
     CHECK(workspace && ws_bytes >= need, "moe workspace %zu < %zu bytes", ws_bytes, need);
     moe_run(logits, x, records, T, E, topk, H, I, out, flags, workspace, reinterpret_cast<hipStream_t>(stream));
+}
+
+void qe_moe_w4_noalloc(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H,
+                       int I, void* out, int flags, void* stream) {
+    moe_check(T, E, topk, H, I);
+    const size_t need = moe_ws(nullptr, T, E, topk, H, I).bytes;
+    CHECK(need <= (size_t)QE_MOE_SCRATCH_BYTES,
+          "qe_moe_w4_noalloc: T %d E %d topk %d H %d I %d needs %zu bytes of workspace, above the %d-byte scratch",
+          T, E, topk, H, I, need, QE_MOE_SCRATCH_BYTES);
+    moe_run(logits, x, records, T, E, topk, H, I, out, flags, moe_scratch_ptr(), reinterpret_cast<hipStream_t>(stream));
 }
 
 // compressed-tensors experts -> group records. gate_up: int32 [E][2I][H/8] (rows gate 0..I then up 0..I), fp16

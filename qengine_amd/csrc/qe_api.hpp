@@ -70,6 +70,8 @@ bool gemm_out_bf16();
 void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 
 int qe_num_cus();
+// device address of the MoE scratch array on the current device (moe.hip; resolved once per device)
+void* moe_scratch_ptr();
 
 // ---- grouped prefill GEMMs of the MoE layer on the prefill GEMM's W4 pipeline (gemm.hip) ----
 // Jobs are (expert, first row) pairs over the expert-sorted slots, kMoePfRows rows each (moe.hip's segmentation).
