@@ -6,7 +6,8 @@ A step is one call of the decode GEMV of BASELINE config 0 (W4A16, M=1, K=5120, 
 bf16 output) on seeded synthetic inputs already resident in HBM. The weights rotate over 8 copies (368 MB,
 more than the 256 MB Infinity Cache) so every call streams its weights from HBM. `value` = algorithmic bytes
 (N*K/2 + N*(K/128)*2 + M*K*2 + M*N*2 = 46,002,176 B per call) * K / the elapsed time of the K timed steps.
-The K decode launches are captured in one HIP graph and replayed (as a decode loop is served), so the host's
+Every secondary figure rotates enough weight copies (or MoE routings) that its working set exceeds the Infinity
+Cache and says so (`working_set`, bytes). The K decode launches are captured in one HIP graph and replayed (as a decode loop is served), so the host's
 per-call overhead does not starve the GPU. `roofline.achieved` = bytes per call / the stream time per launch
 (HIP events on the launch stream before and after the K timed launches). The prefill GEMM (config 2) and the other configs are reported beside it in `secondary`.
 The CPU baseline is the oracle's dequantize + fp32 matmul of the same workload on the host cores.
@@ -37,6 +38,9 @@ def parse():
                     help="run one secondary workload alone (profiling); prints its result")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="time a plain device copy of MB megabytes x 20 (scale for FETCH_SIZE / WRITE_SIZE) and exit")
+    ap.add_argument("--read-floor", action="store_true",
+                    help="time the m = 1 GEMV's record stream alone (qe_read_probe, same launch shape, no arithmetic) "
+                         "on config 0 with the same rotation and graph timing, print it and exit")
     return ap.parse_args()
 
 
@@ -94,13 +98,24 @@ def time_launches(fn, steps, warmup, nvar, graph=False):
     return wall_ms, e0.elapsed_time(e1) / steps
 
 
-def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None):
+MALL_BYTES = 256 << 20  # MI355X Infinity Cache
+
+
+def copies_for(bytes_per_copy, minimum):
+    """weight copies to rotate so the working set exceeds the Infinity Cache by >= 15 %"""
+    return max(minimum, -(-int(1.15 * MALL_BYTES) // int(bytes_per_copy)))
+
+
+def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None, invariant=False):
     import torch
     from qengine_amd import ops, synth
     steps = steps or args.steps
     warmup = warmup or args.warmup
+    ncopy = copies_for(gemv_bytes(m, n, k), args.copies)
+    if invariant:
+        set_config(batch_invariant=1)
     ws = []
-    for c in range(args.copies):
+    for c in range(ncopy):
         q, s = synth.w4_dev(n, k, seed=100 + c)
         ws.append(ops.repack_w4(q, s))
         del q, s
@@ -109,11 +124,40 @@ def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None):
     fn = lambda i: ops.gemv_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
     wall_ms, ev_ms = time_launches(fn, steps, warmup, len(ws), graph=True)
     b = gemv_bytes(m, n, k)
-    res = dict(m=m, n=n, k=k, bytes=b, ms_per_step=wall_ms / steps, kernel_ms_mean=ev_ms,
-               gbs_wall=b * steps / (wall_ms * 1e-3) / 1e9, gbs_kernel=b / (ev_ms * 1e-3) / 1e9)
+    res = dict(m=m, n=n, k=k, bytes=b, ms_per_step=wall_ms / steps, kernel_ms_mean=ev_ms, copies=ncopy,
+               working_set=b * ncopy, gbs_wall=b * steps / (wall_ms * 1e-3) / 1e9, gbs_kernel=b / (ev_ms * 1e-3) / 1e9)
+    if invariant:
+        set_config(batch_invariant=0)
     del ws
     torch.cuda.empty_cache()
     return res
+
+
+def set_config(**kw):
+    from qengine_amd import ops
+    ops.set_config(**kw)
+
+
+def bench_read_floor(args, n=17408, k=5120, steps=None, warmup=None):
+    """qe_read_probe: the m = 1 GEMV's launch shape and record loads with no arithmetic, same rotation and timing"""
+    import torch
+    from qengine_amd import call, ops, synth
+    steps = steps or args.steps
+    warmup = warmup or args.warmup
+    ws = []
+    for c in range(args.copies):
+        q, s = synth.w4_dev(n, k, seed=100 + c)
+        ws.append(ops.repack_w4(q, s))
+        del q, s
+    sink = torch.zeros(n // 16, dtype=torch.int32, device="cuda")
+    fn = lambda i: call("qe_read_probe", ws[i].q, n, k, sink, ops._stream())  # noqa: E731
+    wall_ms, ev_ms = time_launches(fn, steps, warmup, len(ws), graph=True)
+    rec = n * k // 2
+    del ws
+    torch.cuda.empty_cache()
+    return {"n": n, "k": k, "record_bytes": rec, "us_per_launch": round(ev_ms * 1e3, 3),
+            "gbs": round(rec / (ev_ms * 1e-3) / 1e9, 1), "frac_of_peak": round(rec / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "working_set": rec * args.copies}
 
 
 def bench_gemm(m, n, k, steps=10, warmup=3, copies=2):
@@ -134,17 +178,18 @@ def bench_gemm(m, n, k, steps=10, warmup=3, copies=2):
     torch.cuda.empty_cache()
     return {"m": m, "n": n, "k": k, "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 1),
             "pct_bf16_peak": round(100 * flop / (ev_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 1),
-            "ms_kernel": round(ev_ms, 4)}
+            "ms_kernel": round(ev_ms, 4), "working_set": copies * (n * k // 2 + n * k // 64) + m * k * 2 + m * n * 2}
 
 
-def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=16):
+def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=32):
     """INT8 W8A16 per-channel: GEMV (m = 1) in GB/s, GEMM (m = 4096) in TFLOP/s"""
     import torch
     from qengine_amd import ops
     g = torch.Generator(device="cuda")
     g.manual_seed(400)
     ws = []
-    for c in range(copies if m <= 16 else 2):
+    ncopy = copies if m <= 16 else 2
+    for c in range(ncopy):
         q = torch.randint(-127, 128, (n, k), dtype=torch.int8, device="cuda", generator=g)
         s = (torch.randn(n, device="cuda", generator=g).abs() * 0.005).half()
         ws.append(ops.tile_w8(q, s, per_channel=True))
@@ -162,15 +207,17 @@ def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=16):
     if m <= 16:
         b = n * k + 2 * n + 2 * m * k + 2 * m * n
         return {"m": m, "gbs": round(b / (ev_ms * 1e-3) / 1e9, 1), "pct_hbm": round(100 * b / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
-                "us_kernel": round(ev_ms * 1e3, 2), "bytes": b}
+                "us_kernel": round(ev_ms * 1e3, 2), "bytes": b, "working_set": b * ncopy}
     flop = 2.0 * m * n * k
     return {"m": m, "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 1),
-            "pct_bf16_peak": round(100 * flop / (ev_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 1), "ms_kernel": round(ev_ms, 4)}
+            "pct_bf16_peak": round(100 * flop / (ev_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 1), "ms_kernel": round(ev_ms, 4),
+            "working_set": ncopy * (n * k + 2 * n) + 2 * m * k + 2 * m * n}
 
 
-def bench_moe(Ts=(1, 16, 4096), E=512, topk=10, H=2048, I=512, nrout=8):
-    """MoE layer: route + segment + gate_up + down + combine per call, 8 rotating routings so the
-    hit experts change every call (the 830 MB of records exceed the Infinity Cache)"""
+def bench_moe(Ts=(1, 16, 4096), E=512, topk=10, H=2048, I=512):
+    """MoE layer: route + segment + gate_up + down + combine per call. The routings rotate (64 at
+    T = 1, 16 at T = 16, 4 at T = 4096) so the experts hit across the rotation hold far more than the 256 MB
+    Infinity Cache (`working_set`: the distinct experts' record bytes over one rotation)."""
     import torch
     from qengine_amd import ops, synth
     g = torch.Generator(device="cuda")
@@ -186,13 +233,16 @@ def bench_moe(Ts=(1, 16, 4096), E=512, topk=10, H=2048, I=512, nrout=8):
     per_expert = 256 * H // 2 + 256 * (H // 128) * 2 + H * 64 + H * 2  # one group record
     per_expert *= I // 128
     for T in Ts:
+        nrout = 64 if T == 1 else 16 if T <= 16 else 4
         lgs = [torch.randn(T, E, device="cuda", generator=g) for _ in range(nrout)]
         x = synth.x_dev(T, H, seed=6)
         y = torch.empty(T, H, dtype=torch.bfloat16, device="cuda")
-        hits = []
+        hits, seen = [], set()
         for lg in lgs:
             sel, _ = ops.moe_route(lg, topk)
-            hits.append(int(torch.unique(sel).numel()))
+            u = torch.unique(sel)
+            hits.append(int(u.numel()))
+            seen.update(u.cpu().tolist())
         fn = lambda i: moe(lgs[i], x, out_bf16=True, out=y)  # noqa: E731
         steps = 100 if T <= 16 else 20
         # decode (T <= 16) replayed from a HIP graph like the GEMV: the five launches of a call cost the host more
@@ -203,7 +253,8 @@ def bench_moe(Ts=(1, 16, 4096), E=512, topk=10, H=2048, I=512, nrout=8):
         t_roof = max(b / (HBM_PEAK_GBS * 1e9), flop / (BF16_PEAK_TFLOPS * 1e12))
         res[f"T{T}"] = {"us_layer": round(ev_ms * 1e3, 2), "experts_hit": round(sum(hits) / len(hits), 1),
                         "gbs": round(b / (ev_ms * 1e-3) / 1e9, 1), "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 2),
-                        "roofline_frac": round(t_roof / (ev_ms * 1e-3), 3)}
+                        "roofline_frac": round(t_roof / (ev_ms * 1e-3), 3), "routings": nrout,
+                        "working_set": len(seen) * per_expert}
         del lgs, x, y
     del moe
     torch.cuda.empty_cache()
@@ -216,7 +267,6 @@ def cpu_baseline(args, m=1, n=17408, k=5120):
     import oracle
     from qengine_amd import synth
     cores = len(os.sched_getaffinity(0))
-    cores = min(cores, 16)
     os.environ["OMP_NUM_THREADS"] = str(cores)
     q, s = synth.w4_host(n, k, seed=100, sdt=1)
     x = synth.x_host(m, k, seed=1)
@@ -236,6 +286,26 @@ def cpu_baseline(args, m=1, n=17408, k=5120):
             "sample": f"{reps} full calls of config 0 (M=1 K=5120 N=17408): oracle dequant_w4 + matmul_bf16 "
                       f"(C, OpenMP {cores} threads); dequant {t_deq / reps * 1e3:.1f} ms + matmul "
                       f"{t_mm / reps * 1e3:.1f} ms per call"}
+
+
+def cpu_baseline_prefill(rows=8192, n=17408, k=5120):
+    """config 2 on the host cores: the oracle's dequantization of the whole matrix and the fp32 matmul
+    of `rows` of the 8192 token rows (TFLOP/s of that sample; the rate does not depend on the row count)"""
+    import numpy as np  # noqa: F401
+    import oracle
+    from qengine_amd import synth
+    cores = len(os.sched_getaffinity(0))
+    q, s = synth.w4_host(n, k, seed=300, sdt=1)
+    x = synth.x_host(rows, k, seed=2)
+    t0 = time.perf_counter()
+    wdq = oracle.dequant_w4(q, s, n, k, 1)
+    t1 = time.perf_counter()
+    oracle.matmul_bf16(x, wdq, nthreads=cores)
+    t2 = time.perf_counter()
+    flop = 2.0 * rows * n * k
+    return {"value": round(flop / (t2 - t1) / 1e12, 4), "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"config 2 (K=5120, N=17408): oracle dequant_w4 of the full matrix ({(t1 - t0) * 1e3:.0f} ms) + "
+                      f"matmul_bf16 of {rows} of the 8192 token rows ({(t2 - t1):.2f} s, OpenMP {cores} threads), 1 rep"}
 
 
 def main():
@@ -258,6 +328,9 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes_per_launch": nb, "launches": 20}))
         return
+    if args.read_floor:
+        print(json.dumps({"read_floor": bench_read_floor(args)}))
+        return
     if args.only:
         fns = {"prefill": lambda: {"k5120_n17408": bench_gemm(8192, 17408, 5120),
                                    "k17408_n5120": bench_gemm(8192, 5120, 17408)},
@@ -271,19 +344,27 @@ def main():
         return
 
     g = bench_gemv(args)
-    secondary = {}
+    secondary = {"gemv_c0": {"copies": g["copies"], "working_set": g["working_set"]}}
     if not args.no_secondary:
+        secondary["read_floor_c0"] = bench_read_floor(args, steps=400, warmup=20)
+        gi = bench_gemv(args, steps=400, warmup=20, invariant=True)
+        secondary["gemv_c0_batch_invariant"] = {"us_kernel": round(gi["kernel_ms_mean"] * 1e3, 3),
+                                                "pct_hbm": round(100 * gi["gbs_kernel"] / HBM_PEAK_GBS, 1),
+                                                "working_set": gi["working_set"]}
         for (m, n) in [(2, 5120), (4, 5120), (8, 5120), (16, 5120), (2, 17408), (4, 17408), (8, 17408), (16, 17408)]:
             r = bench_gemv(args, m=m, n=n, steps=200, warmup=20)
             secondary[f"skinny_m{m}_n{n}"] = {"gbs_kernel": round(r["gbs_kernel"], 1),
                                               "pct_hbm": round(100 * r["gbs_kernel"] / HBM_PEAK_GBS, 1),
-                                              "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2)}
+                                              "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2),
+                                              "working_set": r["working_set"]}
         secondary["prefill_k5120_n17408"] = bench_gemm(8192, 17408, 5120)
         secondary["prefill_k17408_n5120"] = bench_gemm(8192, 5120, 17408)
         secondary["w8_gemv_m1_k2048_n8192"] = bench_w8(1)
         secondary["w8_gemm_m4096_k2048_n8192"] = bench_w8(4096)
         secondary["moe_e512_top10_h2048_i512"] = bench_moe()
     cpu = None if args.no_cpu else cpu_baseline(args)
+    if not args.no_cpu and not args.no_secondary:
+        secondary["cpu_baseline_prefill_k5120_n17408"] = cpu_baseline_prefill()
     achieved = g["gbs_kernel"]
     out = {
         "metric": "W4A16 GEMV GB/s (% HBM peak) at M=1, K=5120, N=17408",

@@ -30,6 +30,28 @@ extern "C" {
 
 int qe_abi_version(void);
 
+/* Kernel policy of this build, set explicitly (the reference reads scattered environment variables: QE_SKINNY*,
+ * QE_GEMV_NW_*, src/kernels/gemv.cu:1349-1357, skinny.cu:563-570). Process-wide; set it before capturing graphs.
+ *   skinny_min_m    smallest row count the W4 decode GEMV sends to the matrix-core skinny kernel (default 2)
+ *   w8_mfma_min_m   the same for INT8 / Q8; 0 = automatic (1 where the m = 1 K slices hold >= 4 groups, else 2)
+ *   batch_invariant 1: every decode row is computed by the same kernel whatever the row count, so a row's bits do
+ *                   not depend on the batch (the reference's skinny == GEMV contract, skinny.cu:1-14); 0 (default):
+ *                   m = 1 takes the faster m = 1 kernel, equal to the batched rows within 1e-5 * rms
+ * Out-of-range values abort with a "check failed" message. No counterpart function in the reference. */
+typedef struct qe_config {
+    int skinny_min_m;
+    int w8_mfma_min_m;
+    int batch_invariant;
+    int reserved[5];
+} qe_config_t;
+void qe_get_config(qe_config_t* cfg);
+void qe_set_config(const qe_config_t* cfg);
+
+/* Measurement helper (no reference counterpart): streams the n*k/2 record bytes of a W4 matrix with the launch shape
+ * of the m = 1 decode GEMV (n/16 blocks, its K slices) and does nothing else, the HBM read floor that GEMV is held
+ * against. sink: n/16 dwords (written only on a 2^-32 chance, so the loads cannot be dropped). */
+void qe_read_probe(const void* q, int n, int k, uint32_t* sink, void* stream);
+
 /* ---- reference-named hooks (src/capi.cpp): bf16 scales, fp32 outputs, default stream ---- */
 
 /* Library set-up for the current device (CU count, the address of the device's scratch array used by

@@ -50,6 +50,29 @@ extern "C" {
 
 int qe_abi_version(void) { return QE_ABI_VERSION; }
 
+void qe_get_config(qe_config_t* cfg) {
+    CHECK(cfg != nullptr, "qe_get_config: null");
+    const QeConfig& c = qe_config();
+    *cfg = qe_config_t{};
+    cfg->skinny_min_m = c.skinny_min_m;
+    cfg->w8_mfma_min_m = c.w8_mfma_min_m;
+    cfg->batch_invariant = c.batch_invariant;
+}
+
+void qe_set_config(const qe_config_t* cfg) {
+    CHECK(cfg != nullptr, "qe_set_config: null");
+    QeConfig c;
+    c.skinny_min_m = cfg->skinny_min_m;
+    c.w8_mfma_min_m = cfg->w8_mfma_min_m;
+    c.batch_invariant = cfg->batch_invariant;
+    qe_config_set(c);
+}
+
+void qe_read_probe(const void* q, int n, int k, uint32_t* sink, void* stream) {
+    CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && q && sink, "read_probe %d %d", n, k);
+    read_probe_w4(q, n, k, sink, reinterpret_cast<hipStream_t>(stream));
+}
+
 // ---------------------------------------------------------------- reference-named hooks
 void qe_gemv_workspace_init(void) {
     gemv_workspace_init();

@@ -6,6 +6,16 @@
 
 namespace {
 int g_cus = 0;
+QeConfig g_cfg;
+}
+
+const QeConfig& qe_config() { return g_cfg; }
+void qe_config_set(const QeConfig& c) {
+    CHECK(c.skinny_min_m >= 1 && c.skinny_min_m <= kMaxGemvRows + 1 && c.w8_mfma_min_m >= 0 &&
+              c.w8_mfma_min_m <= kMaxGemvRows + 1 && (c.batch_invariant == 0 || c.batch_invariant == 1),
+          "config skinny_min_m %d w8_mfma_min_m %d batch_invariant %d", c.skinny_min_m, c.w8_mfma_min_m,
+          c.batch_invariant);
+    g_cfg = c;
 }
 
 int qe_num_cus() {

@@ -234,3 +234,36 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
     HIP_CHECK(hipGetLastError());
     return true;
 }
+
+// ---- the m = 1 GEMV's HBM read floor: the same blocks, waves and record loads, no arithmetic
+namespace qe_gemv1 {
+template <int NG>
+__global__ void __launch_bounds__(64 * kMaxWaves) read_probe_kernel(const uint4* __restrict__ q, int K,
+                                                                    uint32_t* __restrict__ sink) {
+    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const uint4* qp = q + ((size_t)blockIdx.x * (K >> 6) + 2 * w * NG) * 32 + L;
+    u32x4_v v[NG];
+#pragma unroll
+    for (int i = 0; i < NG; i++) v[i] = ld_stream(qp + (size_t)i * 64);
+    u32x4_v a = v[0];
+#pragma unroll
+    for (int i = 1; i < NG; i++) a ^= v[i];
+    const uint32_t r = a[0] ^ a[1] ^ a[2] ^ a[3];
+    if (r == 0x9E3779B9u) sink[blockIdx.x] = r;
+}
+}  // namespace qe_gemv1
+
+void read_probe_w4(const void* q, int n, int k, uint32_t* sink, hipStream_t st) {
+    using namespace qe_gemv1;
+    int ng = decode_groups(n, k);
+    if (ng == 0) ng = (k / 128) % 4 == 0 && k / 128 / 4 <= kMaxWaves ? 4 : 0;
+    CHECK(ng > 0, "read_probe: no even K slicing for k = %d", k);
+    const dim3 grid((unsigned)(n / 16)), block(64 * (k / 128 / ng));
+    const uint4* qq = reinterpret_cast<const uint4*>(q);
+    if (ng == 10) read_probe_kernel<10><<<grid, block, 0, st>>>(qq, k, sink);
+    else if (ng == 8) read_probe_kernel<8><<<grid, block, 0, st>>>(qq, k, sink);
+    else if (ng == 5) read_probe_kernel<5><<<grid, block, 0, st>>>(qq, k, sink);
+    else if (ng == 4) read_probe_kernel<4><<<grid, block, 0, st>>>(qq, k, sink);
+    else read_probe_kernel<2><<<grid, block, 0, st>>>(qq, k, sink);
+    HIP_CHECK(hipGetLastError());
+}

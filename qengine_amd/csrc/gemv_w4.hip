@@ -1,17 +1,7 @@
 // INT4 decode GEMV / skinny GEMM instantiations (kernel: gemv_impl.hpp).
 #include "gemv_impl.hpp"
 
-#include <cstdlib>
-
 using namespace qe_gemv;
-
-int skinny_min_m() {
-    static const int v = [] {
-        const char* e = getenv("QE_SKINNY_MIN_M");
-        return e && atoi(e) >= 1 ? atoi(e) : 2;
-    }();
-    return v;
-}
 
 static void gemv_check(int n, int k, const void* x, int ldx, int ldy, int m, bool glu) {
     CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && m >= 1 && m <= kMaxGemvRows, "gemv %d %d %d", n, k, m);
@@ -22,9 +12,11 @@ static void gemv_check(int n, int k, const void* x, int ldx, int ldy, int m, boo
 void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
     gemv_check(w.n, w.k, x, ldx, ldy, m, w.glu);
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
-    if (m == 1 && gemv1_w4(w, x, y, out, st)) return;
+    const QeConfig& cfg = qe_config();
+    const bool aligned = ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
+    if (m == 1 && !(cfg.batch_invariant && aligned) && gemv1_w4(w, x, y, out, st)) return;
     // the skinny kernel loads activations as 16-byte pieces; unaligned rows take the decode GEMV for every m
-    if (m >= skinny_min_m() && ((uintptr_t)x & 15) == 0 && ldx % 8 == 0) {
+    if ((m >= cfg.skinny_min_m || cfg.batch_invariant) && aligned) {
         skinny_w4_mfma(w, x, ldx, y, ldy, m, out, st);
         return;
     }

@@ -1,19 +1,15 @@
 // INT8 decode GEMV / skinny GEMM instantiations (kernel: gemv_impl.hpp); the scale dtype is a run-time value.
 #include "gemv_impl.hpp"
 
-#include <cstdlib>
-
 using namespace qe_gemv;
 
-// smallest m that the matrix-core kernel takes: QE_W8_MFMA_MIN_M if set, else 2, or 1 where the m = 1 slicing
+// smallest m that the matrix-core kernel takes: the config's w8_mfma_min_m if set, else 2, or 1 where the m = 1 slicing
 // has >= 4 groups per wave (measured, N = 8192: m = 1 at K = 5120 (5-group slices) 10.9 -> 8.9 us on the matrix
-// cores; at K = 2048 (2-group slices) the VALU GEMV is faster, 5.0 vs 6.0 us)
+// cores; at K = 2048 (2-group slices) the VALU GEMV is faster, 5.0 vs 6.0 us); batch_invariant: always 1
 static int w8_mfma_min_m(int n, int k) {
-    static const int env = [] {
-        const char* e = getenv("QE_W8_MFMA_MIN_M");
-        return e && atoi(e) >= 1 ? atoi(e) : 0;
-    }();
-    if (env > 0) return env;
+    const QeConfig& cfg = qe_config();
+    if (cfg.batch_invariant) return 1;
+    if (cfg.w8_mfma_min_m > 0) return cfg.w8_mfma_min_m;
     return decode_groups(n, k) >= 4 ? 1 : 2;
 }
 

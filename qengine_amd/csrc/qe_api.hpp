@@ -56,8 +56,22 @@ void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, i
 // m = 1 decode GEMV on the matrix cores (gemv1.hip); false when the shape takes the VALU GEMV (uneven K slices,
 // x not 16-byte aligned). out as for skinny_w4_mfma
 bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st);
-// smallest row count that gemv_w4 sends to skinny_w4_mfma (QE_SKINNY_MIN_M, default 2)
-int skinny_min_m();
+// the m = 1 GEMV's record stream with no arithmetic (its HBM read floor); falls back to 4-group slices where the
+// GEMV has no even slicing
+void read_probe_w4(const void* q, int n, int k, uint32_t* sink, hipStream_t st);
+// Kernel policy, set explicitly by the caller (qe_set_config) instead of scattered environment reads:
+//   skinny_min_m    smallest row count gemv_w4 sends to the matrix-core skinny kernel (default 2)
+//   w8_mfma_min_m   the same for INT8 / Q8 (0 = automatic: 1 where the m = 1 slicing has >= 4 groups, else 2)
+//   batch_invariant 1: m = 1 also runs the skinny kernel, so a row's bits do not depend on how many rows are in the
+//                   call (m = 1..16 per launch; larger m in 16-row launches of the same kernel); 0 (default): m = 1
+//                   runs the faster m = 1 kernel, whose fp32 summation order differs (results within 1e-5 * rms)
+struct QeConfig {
+    int skinny_min_m = 2;
+    int w8_mfma_min_m = 0;
+    int batch_invariant = 0;
+};
+const QeConfig& qe_config();
+void qe_config_set(const QeConfig& c);
 void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 
 // ---- prefill GEMM (bf16 MFMA on dequantized tiles staged in LDS) ----

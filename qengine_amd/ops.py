@@ -16,6 +16,31 @@ GLU = 4
 W8_PER_CHANNEL = 8
 
 
+class QeConfig(ctypes.Structure):
+    """include/qe_kernels.h qe_config_t"""
+    _fields_ = [("skinny_min_m", ctypes.c_int), ("w8_mfma_min_m", ctypes.c_int), ("batch_invariant", ctypes.c_int),
+                ("reserved", ctypes.c_int * 5)]
+
+
+def get_config():
+    from .qe import lib
+    c = QeConfig()
+    lib().qe_get_config(ctypes.byref(c))
+    return {"skinny_min_m": c.skinny_min_m, "w8_mfma_min_m": c.w8_mfma_min_m, "batch_invariant": c.batch_invariant}
+
+
+def set_config(**kw):
+    """update the library's kernel policy (qe_set_config); returns the previous settings"""
+    from .qe import lib
+    old = get_config()
+    c = QeConfig()
+    lib().qe_get_config(ctypes.byref(c))
+    for key, v in kw.items():
+        setattr(c, key, int(v))
+    lib().qe_set_config(ctypes.byref(c))
+    return old
+
+
 def _stream():
     # a pointer-sized argument: an int would be passed as a 32-bit c_int
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)

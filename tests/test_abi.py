@@ -40,6 +40,7 @@ def test_library_exports_every_declared_symbol():
     ("lib.qe_repack_w4(None, None, 15, 128, None, None)", "repack_w4 15 128"),
     ("lib.qe_tile_w8(None, None, 16, 100, 1, None, None, None)", "tile_w8 16 100"),
     ("lib.qe_dequant_w4(None, None, 16, 64, 0, None, None)", "dequant_w4 16 64"),
+    ("lib.qe_set_config(ctypes.byref((ctypes.c_int * 8)(2, 0, 5, 0, 0, 0, 0, 0)))", "batch_invariant 5"),
     # the allocation-free MoE layer rejects a workspace above its scratch array before touching the GPU
     ("lib.qe_moe_w4_noalloc(None, None, None, 100000, 512, 10, 2048, 512, None, 0, None)",
      "qe_moe_w4_noalloc: T 100000"),

@@ -324,3 +324,54 @@ def test_gemv_unaligned_activations(dev, mode, n, k):
         y = ops.gemv_w8(w8, x[:m])
         torch.cuda.synchronize()
         assert err_ratio(y.cpu().numpy(), ref8[:m]) <= 1e-4, (mode, m)
+
+
+# the reference's row counts for its skinny == GEMV test (reference tests/test_skinny.py:13)
+MS_REF = [1, 2, 5, 8, 9, 12, 15, 16, 17, 20, 24, 25, 31, 32]
+
+
+@pytest.fixture
+def batch_invariant(dev):
+    old = ops.set_config(batch_invariant=1)
+    yield
+    ops.set_config(**old)
+
+
+@pytest.mark.parametrize("glu", [False, True])
+@pytest.mark.parametrize("n,k", [(5120, 5120), (2048, 1280)])
+def test_batch_invariant_rows(dev, batch_invariant, n, k, glu):
+    """with batch_invariant set, every row of a decode call of m = 1..32 rows (qe_matmul_w4_ex: 16-row launches of the
+    skinny kernel) has the same bits as that row decoded alone, plain and GLU (the reference's contract,
+    skinny.cu:1-14)"""
+    w, q, s = setup_w4(n, k, 1, seed=11 + n, glu=glu)
+    xh = synth.x_host(32, k, seed=12)
+    x = synth.to_dev(xh)
+    alone = []
+    for r in range(32):
+        alone.append(synth.bits(ops.matmul_w4(w, x[r:r + 1], out_bf16=True)) if glu else
+                     ops.matmul_w4(w, x[r:r + 1]).cpu().numpy().view(np.uint32))
+    alone = np.concatenate(alone)
+    for m in MS_REF:
+        y = ops.matmul_w4(w, x[:m], out_bf16=glu)
+        torch.cuda.synchronize()
+        yb = synth.bits(y) if glu else y.cpu().numpy().view(np.uint32)
+        assert np.array_equal(yb, alone[:m]), m
+    if not glu:
+        assert err_ratio(ops.matmul_w4(w, x).cpu().numpy(), matmul_f64(xh, exact_w4(q, s, n, k, 1))) <= 1e-4
+
+
+def test_batch_invariant_w8(dev, batch_invariant):
+    """the same for INT8 (per-channel W8): m = 1 runs the matrix-core kernel too"""
+    n, k = 4096, 2048
+    q8, s8 = synth.w8_host(n, k, seed=13, per_channel=True)
+    w8 = ops.tile_w8(synth.to_dev(q8), synth.to_dev(s8, torch.float16), True)
+    x = synth.to_dev(synth.x_host(16, k, seed=14))
+    full = ops.gemv_w8(w8, x).cpu().numpy().view(np.uint32)
+    for r in (0, 7, 15):
+        y = ops.gemv_w8(w8, x[r:r + 1]).cpu().numpy().view(np.uint32)
+        assert np.array_equal(y, full[r:r + 1]), r
+
+
+def test_config_defaults_and_checks(dev):
+    c = ops.get_config()
+    assert c == {"skinny_min_m": 2, "w8_mfma_min_m": 0, "batch_invariant": 0}
