@@ -172,7 +172,9 @@ def bench_gemm(m, n, k, steps=10, warmup=3, copies=2):
     x = synth.x_dev(m, k, seed=2)
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
     fn = lambda i: ops.gemm_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    old = ops.set_config(gemm_tune=1)  # the first (untimed) call times the candidates once; the timed calls reuse it
     _, ev_ms = time_launches(fn, steps, warmup, len(ws))
+    ops.set_config(**old)
     flop = 2.0 * m * n * k
     del ws, x, y
     torch.cuda.empty_cache()

@@ -37,15 +37,36 @@ int qe_abi_version(void);
  *   batch_invariant 1: every decode row is computed by the same kernel whatever the row count, so a row's bits do
  *                   not depend on the batch (the reference's skinny == GEMV contract, skinny.cu:1-14); 0 (default):
  *                   m = 1 takes the faster m = 1 kernel, equal to the batched rows within 1e-5 * rms
+ *   gemm_tune       1: every prefill GEMM times its candidates (tile configuration x split of the last partial round)
+ *                   once per (shape, token bucket), outside graph capture, and keeps the fastest (as qe_gemm_w4_t
+ *                   always does); 0 (default): a stored choice if any, else the cost model
  * Out-of-range values abort with a "check failed" message. No counterpart function in the reference. */
 typedef struct qe_config {
     int skinny_min_m;
     int w8_mfma_min_m;
     int batch_invariant;
-    int reserved[5];
+    int gemm_tune;
+    int reserved[4];
 } qe_config_t;
 void qe_get_config(qe_config_t* cfg);
 void qe_set_config(const qe_config_t* cfg);
+
+/* GEMM tuning table (reference TuneStore, src/kernels/gemm.cu:4116-4348, QE_TUNE_FILE): path = a text file that
+ * holds the measured choices per device; entries already in it are loaded (a file of another build is ignored) and
+ * every new choice rewrites it, so later processes reuse the choices (bit-identical results across restarts).
+ * NULL or "": in memory only. qe_gemm_tune_clear forgets the choices (in memory; the file is left as it is). */
+void qe_gemm_tune_file(const char* path);
+void qe_gemm_tune_clear(void);
+int qe_gemm_tune_entries(void);
+/* The prefill GEMM's split-K workspace is the library's (per device, grown on demand outside graph capture; a call
+ * captured into a graph without enough of it runs unsplit). Reserve `bytes` on the current device before capturing
+ * (the reference's gemm_reserve_ws). */
+void qe_gemm_reserve(size_t bytes);
+/* test hook: qe_gemm_w4_ex with a given choice instead of the tuner's (cfg 0: 256 x 256 tiles, 1: 256 x 128; ks: K
+ * ranges of the last partial round's tiles, 1 / 2 / 4); returns 1 if that split applies to the shape (else it runs
+ * unsplit and returns 0). The reference's QE_GEMM_FORCE (src/kernels/gemm.cu:4376-4394). */
+int qe_gemm_w4_choice(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                      int flags, int cfg, int ks, void* stream);
 
 /* Measurement helper (no reference counterpart): streams the n*k/2 record bytes of a W4 matrix with the launch shape
  * of the m = 1 decode GEMV (n/16 blocks, its K slices) and does nothing else, the HBM read floor that GEMV is held

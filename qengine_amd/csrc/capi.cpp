@@ -3,6 +3,7 @@
 // pointers, default stream, bf16 scales, fp32 outputs, fatal abort on a violated precondition.
 // Build-defined *_ex entry points take an explicit stream, row strides and flags (QeFlags).
 #include "qe_api.hpp"
+#include "gemm_tune.hpp"
 #include "../../include/qe_kernels.h"
 
 #include <atomic>
@@ -57,6 +58,7 @@ void qe_get_config(qe_config_t* cfg) {
     cfg->skinny_min_m = c.skinny_min_m;
     cfg->w8_mfma_min_m = c.w8_mfma_min_m;
     cfg->batch_invariant = c.batch_invariant;
+    cfg->gemm_tune = c.gemm_tune;
 }
 
 void qe_set_config(const qe_config_t* cfg) {
@@ -65,7 +67,20 @@ void qe_set_config(const qe_config_t* cfg) {
     c.skinny_min_m = cfg->skinny_min_m;
     c.w8_mfma_min_m = cfg->w8_mfma_min_m;
     c.batch_invariant = cfg->batch_invariant;
+    c.gemm_tune = cfg->gemm_tune;
     qe_config_set(c);
+}
+
+void qe_gemm_tune_file(const char* path) { gemm_tune_file(path); }
+void qe_gemm_tune_clear(void) { gemm_table_clear(); }
+int qe_gemm_tune_entries(void) { return (int)gemm_table_size(); }
+void qe_gemm_reserve(size_t bytes) { gemm_reserve(bytes); }
+
+int qe_gemm_w4_choice(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                      int flags, int cfg, int ks, void* stream) {
+    const W4 w = mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16);
+    gemm_w4_choice(w, x, ldx, y, ldy, t, (flags & QE_OUT_BF16) != 0, cfg, ks, as_stream(stream));
+    return ks > 1 && gemm_split_applies(cfg, n, k, t, ks) ? 1 : 0;
 }
 
 void qe_read_probe(const void* q, int n, int k, uint32_t* sink, void* stream) {
@@ -111,7 +126,7 @@ void qe_gemm_w4(const void* q, const void* s, int n, int k, const uint16_t* x, f
 }
 
 void qe_gemm_w4_t(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t) {
-    gemm_w4(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, t, gemm_out_bf16(), 0);
+    gemm_w4(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, t, gemm_out_bf16(), 0, true);
 }
 
 void qe_gemm_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, void* st) {

@@ -16,6 +16,11 @@
 //   grid: one block per output tile, tiles ordered so that the 8 XCDs (blockIdx % 8) each sweep a contiguous band
 //        of tiles (their L2 keeps the shared X / W tiles).
 #include "mfma_tile.hpp"
+#include "gemm_tune.hpp"
+
+#include <algorithm>
+#include <mutex>
+#include <vector>
 
 namespace {
 
@@ -48,6 +53,14 @@ __device__ __forceinline__ void dma4(const void* src, unsigned lds_dst) {  // 4 
     asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
 }
 
+// MODE 0 split tiles: the tiles from `ndirect` on run as `ks` K ranges each (stream-K of the last, partly filled
+// round); their fp32 partials go to part [(tile - ndirect) * ks + split][BM][BN] and splitk_reduce_kernel adds them
+struct SplitArgs {
+    int ndirect = 1 << 30;
+    int ks = 1;
+    float* part = nullptr;
+};
+
 // MODE 0: the dense GEMM. MODE 1 / 2: the MoE grouped gate_up / down GEMMs (MoePfArgs), INT4 only: block
 // (job, n tile) with the job's rows gathered (gate_up: x rows of the slots' tokens, down: act rows of the slots),
 // the W tile from the job's expert records (gate_up: the 256 GLU rows of record n tile, K = H; down: H rows, K = I,
@@ -56,7 +69,7 @@ template <int FMT, int SDT, int WMT, int WNT, int MODE = 0>
 __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                    int N, int K, const uint16_t* __restrict__ x, int ldx, int T,
                                                    void* __restrict__ c, int ldc, int out, int sdt, int nbn, int nbt,
-                                                   MoePfArgs ma) {
+                                                   MoePfArgs ma, SplitArgs sp) {
     using C = Cfg<WMT, WNT>;
     constexpr int BM = C::BM, BN = C::BN;
     constexpr bool W4 = FMT == kFmtW4;
@@ -69,10 +82,25 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     // n-major tile sequence (consecutive tiles share the X tile, a band of them shares W tiles)
     int n0, t0;
     int e = 0, slot0 = 0, nt = 0;
+    int kt0 = 0, KTL = K / BK;  // this block's k steps [kt0, kt0 + KTL)
+    int split_slot = -1;        // >= 0: a split tile's part, stored raw to sp.part
     if constexpr (MODE == 0) {
-        const int ntiles = nbn * nbt, per = (ntiles + 7) >> 3;
-        const int b = blockIdx.x, tile = (b & 7) * per + (b >> 3);
-        if (tile >= ntiles) return;
+        // tiles [0, sp.ndirect): whole K, XCD bands; tiles [sp.ndirect, ntiles): split into sp.ks K ranges whose
+        // fp32 partials splitk_reduce_kernel sums (the blocks of the otherwise partly idle last round)
+        const int ntiles = nbn * nbt, per = (sp.ndirect + 7) >> 3;
+        const int b = blockIdx.x;
+        int tile;
+        if (b < 8 * per) {
+            tile = (b & 7) * per + (b >> 3);
+            if (tile >= sp.ndirect) return;
+        } else {
+            const int j = b - 8 * per;
+            tile = sp.ndirect + j / sp.ks;
+            if (tile >= ntiles) return;
+            KTL = K / BK / sp.ks;
+            kt0 = (j % sp.ks) * KTL;
+            split_slot = j;
+        }
         n0 = (tile % nbn) * BN;
         t0 = (tile / nbn) * BM;
     } else {
@@ -93,7 +121,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             s = reinterpret_cast<const uint16_t*>(rp + ma.gg_q);
         }
     }
-    const int G = K >> 7, KT = K / BK;
+    const int G = K >> 7;
 
     // ---- X (every format): LDS DMA (global_load_lds_dwordx4), 1 KB = 8 rows per wave instruction. Lane i lands at
     //      LDS slot i of the 8-row block, so it loads the chunk that the swizzle puts there. Rows past T re-read
@@ -325,22 +353,23 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         constexpr unsigned kRawOff = 2 * C::kStage, kScOff = kRawOff + 2 * C::kRaw;
         char* raw = lds + kRawOff;
         char* scb = lds + kScOff;
-        dma_x(0, 0);
-        dma_w4(0, kRawOff);
-        dma_w4(1, kRawOff + C::kRaw);
-        dma_sc(0, kScOff);
+        // buffers by the local step kt, addresses by the global step kt0 + kt (kt0 is even: group aligned)
+        dma_x(kt0, 0);
+        dma_w4(kt0, kRawOff);
+        dma_w4(kt0 + 1, kRawOff + C::kRaw);
+        dma_sc(kt0 >> 1, kScOff);
         asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
         store_w4(lds + BM * BK * 2, raw, scb, 0);
         store_w4(lds + BM * BK * 2, raw, scb, 1);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        for (int kt = 0; kt < KT; kt++) {
+        for (int kt = 0; kt < KTL; kt++) {
             char* st = lds + ((kt + 1) & 1) * C::kStage;
-            if (kt + 1 < KT) dma_x(kt + 1, ((kt + 1) & 1) * C::kStage);
-            if (kt + 2 < KT) {
-                dma_w4(kt + 2, kRawOff + (kt & 1) * C::kRaw);
-                if (((kt + 2) & 1) == 0) dma_sc((kt + 2) >> 1, kScOff + (((kt + 2) >> 1) & 1) * C::kSc);
+            if (kt + 1 < KTL) dma_x(kt0 + kt + 1, ((kt + 1) & 1) * C::kStage);
+            if (kt + 2 < KTL) {
+                dma_w4(kt0 + kt + 2, kRawOff + (kt & 1) * C::kRaw);
+                if (((kt + 2) & 1) == 0) dma_sc((kt0 + kt + 2) >> 1, kScOff + (((kt + 2) >> 1) & 1) * C::kSc);
             }
-            const bool more = kt + 1 < KT;
+            const bool more = kt + 1 < KTL;
             const char* rnext = raw + ((kt + 1) & 1) * C::kRaw;
             const char* snext = scb + (((kt + 1) >> 1) & 1) * C::kSc;
             mfma_step(kt, [&](int ks) {
@@ -352,26 +381,26 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         // X by LDS DMA (as the INT4 path), INT8 records through two register sets: step kt issues the DMA of X
         // (kt + 1) and the record loads of kt + 2 at its top, dequantizes the records of kt + 1 (loaded one step
         // earlier) into the other stage during its MFMAs, and ends with vmcnt(0) + the barrier.
-        dma_x(0, 0);
-        load_w8(wsA, 0);
-        if (KT > 1) load_w8(wsB, 1);
+        dma_x(kt0, 0);
+        load_w8(wsA, kt0);
+        if (KTL > 1) load_w8(wsB, kt0 + 1);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
 #pragma unroll
         for (int d = 0; d < 4; d++) store_w8x(wsA, lds + BM * BK * 2, d);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
         auto step = [&](int kt, const WSet& cur, WSet& nxt_regs) {
             char* nxt = lds + ((kt + 1) & 1) * C::kStage;
-            if (kt + 1 < KT) dma_x(kt + 1, ((kt + 1) & 1) * C::kStage);
-            const bool more = kt + 1 < KT;
+            if (kt + 1 < KTL) dma_x(kt0 + kt + 1, ((kt + 1) & 1) * C::kStage);
+            const bool more = kt + 1 < KTL;
             mfma_step(kt, [&](int ks) {
                 if (more) store_w8x(cur, nxt + BM * BK * 2, ks);
-                if (ks == 0 && kt + 2 < KT) load_w8(nxt_regs, kt + 2);  // after the first stores free no registers
+                if (ks == 0 && kt + 2 < KTL) load_w8(nxt_regs, kt0 + kt + 2);  // after the first stores free no registers
             });
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         };
-        for (int kt = 0; kt < KT; kt += 2) {
+        for (int kt = 0; kt < KTL; kt += 2) {
             step(kt, wsB, wsA);
-            if (kt + 1 < KT) step(kt + 1, wsA, wsB);
+            if (kt + 1 < KTL) step(kt + 1, wsA, wsB);
         }
     }
 
@@ -381,6 +410,22 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     //      ldc / c are not aligned for them. GLU: gate row g and up row g + 8 of a 16-row tile are registers r and
     //      r + 4 of the same lane.
     const int cj = lane & 31, ci = 4 * (lane >> 5);
+    if (MODE == 0 && split_slot >= 0) {
+        // raw fp32 partial of the whole BM x BN tile, [token][row] (rows past N / tokens past T included)
+        float* pp = sp.part + (size_t)split_slot * BM * BN;
+#pragma unroll
+        for (int a = 0; a < WMT; a++)
+#pragma unroll
+            for (int bb = 0; bb < WNT; bb++)
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++) {
+                    const int tl = wm * 32 * WMT + a * 32 + cj, nl = wn * 32 * WNT + bb * 32 + 8 * rb + ci;
+                    const f32x16_v& v = acc[a][bb];
+                    *reinterpret_cast<f32x4_v*>(pp + (size_t)tl * BN + nl) =
+                        f32x4_v{v[4 * rb], v[4 * rb + 1], v[4 * rb + 2], v[4 * rb + 3]};
+                }
+        return;
+    }
     const bool vec = MODE != 0 || ((ldc & 3) == 0 && ((uintptr_t)c & (out == kOutF32 ? 15u : 7u)) == 0);
     auto st4 = [&](uint16_t* p, float v0, float v1, float v2, float v3) {  // 4 consecutive bf16
         if (vec) {
@@ -439,27 +484,233 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         }
 }
 
-template <int FMT, int SDT, int WMT, int WNT>
-void launch_cfg(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc,
-                int out, int sdt, hipStream_t st) {
-    using C = Cfg<WMT, WNT>;
-    const int nbn = (n + C::BN - 1) / C::BN, nbt = (t + C::BM - 1) / C::BM;
-    const int ntiles = nbn * nbt, per = (ntiles + 7) / 8;
-    gemm_kernel<FMT, SDT, WMT, WNT><<<dim3((unsigned)(8 * per)), dim3(NTH), FMT == kFmtW4 ? C::kLdsW4 : 2 * C::kStage, st>>>(
-        q, s, n, k, x, ldx, t, c, ldc, out, sdt, nbn, nbt, MoePfArgs{});
-    HIP_CHECK(hipGetLastError());
+// Split tiles' partials -> outputs: one thread per (split tile, token row, 16 output columns); the ks partials are
+// added in split order (fixed order: the result does not depend on timing), then the epilogue of the GEMM
+template <int BM, int BN>
+__global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restrict__ part, int ks, int ndirect,
+                                                            int nsplit, int nbn, int T, int N, void* __restrict__ c,
+                                                            int ldc, int out) {
+    constexpr int CB = BN / 16;
+    const size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (size_t)nsplit * BM * CB) return;
+    const int st = (int)(idx / ((size_t)BM * CB)), r = (int)((idx / CB) % BM), cb = (int)(idx % CB);
+    const int tile = ndirect + st;
+    const int tok = (tile / nbn) * BM + r, n = (tile % nbn) * BN + 16 * cb;
+    if (tok >= T || n >= N) return;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = 0.f;
+    for (int z = 0; z < ks; z++) {
+        const f32x4_v* p = reinterpret_cast<const f32x4_v*>(part + (((size_t)st * ks + z) * BM + r) * BN + 16 * cb);
+#pragma unroll
+        for (int q4 = 0; q4 < 4; q4++) {
+            const f32x4_v a = p[q4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) v[4 * q4 + j] += a[j];
+        }
+    }
+    if (out == kOutGLU) {
+        uint16_t* o = reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + (n >> 4) * 8;
+#pragma unroll
+        for (int j = 0; j < 8; j++) o[j] = f32_to_bf16(silu_f32(v[j]) * v[j + 8]);
+    } else if (out == kOutBF16) {
+        uint16_t* o = reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + n;
+#pragma unroll
+        for (int j = 0; j < 16; j++) o[j] = f32_to_bf16(v[j]);
+    } else {
+        float* o = reinterpret_cast<float*>(c) + (size_t)tok * ldc + n;
+#pragma unroll
+        for (int j = 0; j < 16; j++) o[j] = v[j];
+    }
 }
 
-// block tile choice: 256 tokens x 256 rows when that fills the CUs in whole rounds, else 256 x 128
+// ---- library-owned split-K workspace, one per device: grown outside graph capture, outgrown buffers retired (kept
+//      allocated: a graph captured earlier may still use them); nullptr while capturing when it is too small
+constexpr int kMaxDev = 64;
+std::mutex g_ws_mu;
+struct SplitWs {
+    void* p = nullptr;
+    size_t bytes = 0;
+    std::vector<void*> retired;
+} g_ws[kMaxDev];
+
+float* split_ws(size_t bytes, hipStream_t st) {
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    CHECK(dev >= 0 && dev < kMaxDev, "device %d", dev);
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    SplitWs& w = g_ws[dev];
+    if (w.bytes >= bytes) return reinterpret_cast<float*>(w.p);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_CHECK(hipStreamIsCapturing(st, &cs));
+    if (cs != hipStreamCaptureStatusNone) return nullptr;
+    void* np = nullptr;
+    HIP_CHECK(hipMalloc(&np, bytes));
+    if (w.p) w.retired.push_back(w.p);
+    w.p = np;
+    w.bytes = bytes;
+    return reinterpret_cast<float*>(np);
+}
+
+// tile configurations: 0 = 256 tokens x 256 rows (WMT 4, WNT 2), 1 = 256 x 128 (4, 1)
+constexpr int kNumCfg = 2;
+template <int CFG>
+struct CfgOf;
+template <>
+struct CfgOf<0> {
+    static constexpr int WMT = 4, WNT = 2;
+};
+template <>
+struct CfgOf<1> {
+    static constexpr int WMT = 4, WNT = 1;
+};
+
+struct GemmGeom {
+    int nbn, nbt, ntiles, ndirect, nsplit, ks;
+    size_t ws_bytes;
+};
+// tiles of configuration cfg and, for ks > 1, the split of the last partial round (stream-K): whole rounds of
+// tiles run directly, the remaining tiles as ks K ranges; false when that split does not apply (no partial round,
+// K steps not divisible into even ranges)
+bool gemm_geom(int cfg, int n, int k, int t, int ks, GemmGeom& g) {
+    const int BM = 256, BN = cfg == 0 ? 256 : 128;
+    g.nbn = (n + BN - 1) / BN;
+    g.nbt = (t + BM - 1) / BM;
+    g.ntiles = g.nbn * g.nbt;
+    g.ks = ks;
+    g.ndirect = g.ntiles;
+    g.nsplit = 0;
+    g.ws_bytes = 0;
+    if (ks == 1) return true;
+    const int cus = qe_num_cus(), KT = k / BK;
+    if (KT % (2 * ks) != 0) return false;
+    const int tail = g.ntiles % cus;
+    if (tail == 0 || tail * ks > cus) return false;
+    g.ndirect = g.ntiles - tail;
+    g.nsplit = tail;
+    g.ws_bytes = (size_t)tail * ks * BM * BN * 4;
+    return true;
+}
+
+}  // namespace
+
+void gemm_reserve(size_t bytes) {
+    if (bytes > 0) CHECK(split_ws(bytes, 0) != nullptr, "gemm_reserve: called during graph capture");
+}
+
+namespace {
+
+template <int FMT, int SDT, int CFG>
+void launch_cfg(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc,
+                int out, int sdt, const GemmGeom& g, float* part, hipStream_t st) {
+    constexpr int WMT = CfgOf<CFG>::WMT, WNT = CfgOf<CFG>::WNT;
+    using C = Cfg<WMT, WNT>;
+    SplitArgs sp;
+    sp.ndirect = g.ndirect;
+    sp.ks = g.ks;
+    sp.part = part;
+    const int per = (g.ndirect + 7) / 8;
+    const unsigned blocks = (unsigned)(8 * per + g.nsplit * g.ks);
+    gemm_kernel<FMT, SDT, WMT, WNT><<<dim3(blocks), dim3(NTH), FMT == kFmtW4 ? C::kLdsW4 : 2 * C::kStage, st>>>(
+        q, s, n, k, x, ldx, t, c, ldc, out, sdt, g.nbn, g.nbt, MoePfArgs{}, sp);
+    HIP_CHECK(hipGetLastError());
+    if (g.nsplit > 0) {
+        const size_t threads = (size_t)g.nsplit * C::BM * (C::BN / 16);
+        splitk_reduce_kernel<C::BM, C::BN><<<dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st>>>(
+            part, g.ks, g.ndirect, g.nsplit, g.nbn, t, n, c, ldc, out);
+        HIP_CHECK(hipGetLastError());
+    }
+}
+
 template <int FMT, int SDT>
-void launch_gemm(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc,
-                 int out, int sdt, hipStream_t st) {
+void run_choice(int cfg, int ks, const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t,
+                void* c, int ldc, int out, int sdt, hipStream_t st) {
+    GemmGeom g;
+    float* part = nullptr;
+    if (ks > 1) {
+        if (!gemm_geom(cfg, n, k, t, ks, g) || (part = split_ws(g.ws_bytes, st)) == nullptr) ks = 1;
+    }
+    if (ks == 1) gemm_geom(cfg, n, k, t, 1, g);
+    if (cfg == 0) launch_cfg<FMT, SDT, 0>(q, s, n, k, x, ldx, t, c, ldc, out, sdt, g, part, st);
+    else launch_cfg<FMT, SDT, 1>(q, s, n, k, x, ldx, t, c, ldc, out, sdt, g, part, st);
+}
+
+// untuned choice (cost model): 256 x 256 tiles when they fill the CUs at least once (else 256 x 128), with the last
+// partial round split in two K ranges when it is at most half full
+GemmChoice gemm_model_choice(int n, int k, int t) {
     const int cus = qe_num_cus();
     const long tiles_big = (long)((n + 255) / 256) * ((t + 255) / 256);
-    const long rounds_big = (tiles_big + cus - 1) / cus;
-    const bool big = tiles_big >= cus && (double)tiles_big / (rounds_big * cus) >= 0.9;
-    if (big) launch_cfg<FMT, SDT, 4, 2>(q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
-    else launch_cfg<FMT, SDT, 4, 1>(q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
+    GemmChoice ch{tiles_big >= cus ? 0 : 1, 1};
+    GemmGeom g;
+    if (ch.cfg == 0 && gemm_geom(0, n, k, t, 2, g)) ch.ks = 2;
+    else if (ch.cfg == 0) {
+        const long rounds = (tiles_big + cus - 1) / cus;
+        if ((double)tiles_big / (rounds * cus) < 0.9) ch.cfg = 1;
+    }
+    return ch;
+}
+
+// timed choice: every (configuration, split) candidate once untimed, then 5 rounds in rotating order, the median;
+// outside graph capture only (during capture: the cost model)
+template <int FMT, int SDT>
+GemmChoice gemm_tune_choice(int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc, int out, int sdt,
+                            const uint4* q, const uint16_t* s, hipStream_t st) {
+    std::vector<GemmChoice> cl;
+    for (int cfg = 0; cfg < kNumCfg; cfg++)
+        for (int ks : {1, 2, 4}) {
+            GemmGeom g;
+            if (gemm_geom(cfg, n, k, t, ks, g)) cl.push_back(GemmChoice{cfg, ks});
+        }
+    hipEvent_t e0, e1;
+    HIP_CHECK(hipEventCreate(&e0));
+    HIP_CHECK(hipEventCreate(&e1));
+    auto time1 = [&](const GemmChoice& ch) {
+        HIP_CHECK(hipEventRecord(e0, st));
+        run_choice<FMT, SDT>(ch.cfg, ch.ks, q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
+        HIP_CHECK(hipEventRecord(e1, st));
+        HIP_CHECK(hipEventSynchronize(e1));
+        float ms = 0.f;
+        HIP_CHECK(hipEventElapsedTime(&ms, e0, e1));
+        return ms;
+    };
+    for (const auto& ch : cl) time1(ch);
+    constexpr int kReps = 5;
+    std::vector<std::vector<float>> ts(cl.size());
+    for (int r = 0; r < kReps; r++)
+        for (size_t j = 0; j < cl.size(); j++) {
+            const size_t i = (j + r) % cl.size();
+            ts[i].push_back(time1(cl[i]));
+        }
+    size_t best = 0;
+    float best_ms = 1e30f;
+    for (size_t j = 0; j < cl.size(); j++) {
+        std::sort(ts[j].begin(), ts[j].end());
+        if (ts[j][kReps / 2] < best_ms) {
+            best_ms = ts[j][kReps / 2];
+            best = j;
+        }
+    }
+    HIP_CHECK(hipEventDestroy(e0));
+    HIP_CHECK(hipEventDestroy(e1));
+    return cl[best];
+}
+
+template <int FMT, int SDT>
+void launch_gemm(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc,
+                 int out, int sdt, bool tuned, hipStream_t st) {
+    GemmChoice ch;
+    const GemmKey key{FMT, n, k, gemm_bucket(t), out == kOutGLU ? 1 : 0};
+    if (!gemm_table_find(key, ch)) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        HIP_CHECK(hipStreamIsCapturing(st, &cs));
+        if ((tuned || qe_config().gemm_tune) && cs == hipStreamCaptureStatusNone) {
+            ch = gemm_tune_choice<FMT, SDT>(n, k, x, ldx, t, c, ldc, out, sdt, q, s, st);
+            gemm_table_add(key, ch);
+        } else {
+            ch = gemm_model_choice(n, k, t);
+        }
+    }
+    run_choice<FMT, SDT>(ch.cfg, ch.ks, q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
 }
 
 void gemm_check(int n, int k, const void* x, int ldx, int ldc, int t, bool glu) {
@@ -481,27 +732,43 @@ void moe_pf_gemm(int mode, const MoePfArgs& a, hipStream_t st) {
     const unsigned grid = 8u * (unsigned)((a.max_jobs + 7) / 8) * (unsigned)nbn;
     if (mode == 1)
         gemm_kernel<kFmtW4, kScaleF16, 2, 2, 1><<<dim3(grid), dim3(NTH), C::kLdsW4, st>>>(
-            nullptr, nullptr, 256, a.H, nullptr, 0, 0, nullptr, 0, kOutGLU, kScaleF16, nbn, 0, a);
+            nullptr, nullptr, 256, a.H, nullptr, 0, 0, nullptr, 0, kOutGLU, kScaleF16, nbn, 0, a, SplitArgs{});
     else
         gemm_kernel<kFmtW4, kScaleF16, 2, 2, 2><<<dim3(grid), dim3(NTH), C::kLdsW4, st>>>(
-            nullptr, nullptr, a.H, a.I, nullptr, 0, 0, nullptr, 0, kOutBF16, kScaleF16, nbn, 0, a);
+            nullptr, nullptr, a.H, a.I, nullptr, 0, 0, nullptr, 0, kOutBF16, kScaleF16, nbn, 0, a, SplitArgs{});
     HIP_CHECK(hipGetLastError());
 }
 
-void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st) {
+void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st,
+             bool tuned) {
     gemm_check(w.n, w.k, x, ldx, ldc, t, w.glu);
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
-    if (w.sdt == kScaleF16) launch_gemm<kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
-    else launch_gemm<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
+    if (w.sdt == kScaleF16) launch_gemm<kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, tuned, st);
+    else launch_gemm<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, tuned, st);
 }
 
-void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st) {
+void gemm_w4_choice(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, int cfg, int ks,
+                    hipStream_t st) {
+    gemm_check(w.n, w.k, x, ldx, ldc, t, w.glu);
+    CHECK(cfg >= 0 && cfg < kNumCfg && (ks == 1 || ks == 2 || ks == 4), "gemm choice cfg %d ks %d", cfg, ks);
+    const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    if (w.sdt == kScaleF16) run_choice<kFmtW4, kScaleF16>(cfg, ks, w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
+    else run_choice<kFmtW4, kScaleBF16>(cfg, ks, w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
+}
+
+bool gemm_split_applies(int cfg, int n, int k, int t, int ks) {
+    GemmGeom g;
+    return gemm_geom(cfg, n, k, t, ks, g) && g.nsplit > 0;
+}
+
+void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st,
+             bool tuned) {
     gemm_check(w.n, w.k, x, ldx, ldc, t, w.glu);
     CHECK(!w.glu || w.q8, "gemm_w8: GLU is for Q8 matrices");
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
-    if (w.q8) launch_gemm<kFmtQ8, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
-    else if (w.per_channel) launch_gemm<kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
-    else launch_gemm<kFmtW8G, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, st);
+    if (w.q8) launch_gemm<kFmtQ8, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, tuned, st);
+    else if (w.per_channel) launch_gemm<kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, tuned, st);
+    else launch_gemm<kFmtW8G, -1>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, tuned, st);
 }
 
 void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {

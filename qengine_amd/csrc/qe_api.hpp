@@ -65,19 +65,33 @@ void read_probe_w4(const void* q, int n, int k, uint32_t* sink, hipStream_t st);
 //   batch_invariant 1: m = 1 also runs the skinny kernel, so a row's bits do not depend on how many rows are in the
 //                   call (m = 1..16 per launch; larger m in 16-row launches of the same kernel); 0 (default): m = 1
 //                   runs the faster m = 1 kernel, whose fp32 summation order differs (results within 1e-5 * rms)
+//   gemm_tune       1: every prefill GEMM call times its candidates once per (shape, token bucket) (outside graph
+//                   capture) and keeps the fastest; 0 (default): stored choices, else the cost model
 struct QeConfig {
     int skinny_min_m = 2;
     int w8_mfma_min_m = 0;
     int batch_invariant = 0;
+    int gemm_tune = 0;
 };
 const QeConfig& qe_config();
 void qe_config_set(const QeConfig& c);
 void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 
 // ---- prefill GEMM (bf16 MFMA on dequantized tiles staged in LDS) ----
-void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
-void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
+// tuned: time the candidates on the first call of a (shape, token bucket) outside graph capture (also when the
+// config's gemm_tune is set); otherwise the stored choice, else the cost model
+void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st,
+             bool tuned = false);
+void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st,
+             bool tuned = false);
+// a given choice (tile configuration 0: 256 x 256, 1: 256 x 128; ks K ranges of the last partial round, 1 = none);
+// falls back to ks = 1 where the split does not apply (gemm_split_applies false) or has no workspace
+void gemm_w4_choice(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, int cfg, int ks,
+                    hipStream_t st);
+bool gemm_split_applies(int cfg, int n, int k, int t, int ks);
 void gemm_set_out_bf16(bool on);
+// reserve the split-K workspace of the current device (grown on demand otherwise, never during graph capture)
+void gemm_reserve(size_t bytes);
 bool gemm_out_bf16();
 
 // GEMV for m <= 32 (split into row blocks of 16), GEMM above (reference gemv.cuh:187-190)

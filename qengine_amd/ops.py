@@ -19,14 +19,15 @@ W8_PER_CHANNEL = 8
 class QeConfig(ctypes.Structure):
     """include/qe_kernels.h qe_config_t"""
     _fields_ = [("skinny_min_m", ctypes.c_int), ("w8_mfma_min_m", ctypes.c_int), ("batch_invariant", ctypes.c_int),
-                ("reserved", ctypes.c_int * 5)]
+                ("gemm_tune", ctypes.c_int), ("reserved", ctypes.c_int * 4)]
 
 
 def get_config():
     from .qe import lib
     c = QeConfig()
     lib().qe_get_config(ctypes.byref(c))
-    return {"skinny_min_m": c.skinny_min_m, "w8_mfma_min_m": c.w8_mfma_min_m, "batch_invariant": c.batch_invariant}
+    return {"skinny_min_m": c.skinny_min_m, "w8_mfma_min_m": c.w8_mfma_min_m, "batch_invariant": c.batch_invariant,
+            "gemm_tune": c.gemm_tune}
 
 
 def set_config(**kw):
@@ -132,6 +133,18 @@ def gemm_w4(w: W4, x, out_bf16=False, y=None):
     call("qe_gemm_w4_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
          w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
     return y
+
+
+def gemm_w4_choice(w: W4, x, cfg, ks, out_bf16=False, y=None):
+    """prefill GEMM with a given (tile configuration, split) instead of the tuner's; returns (y, split applied)"""
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, w.glu, x.device) if y is None else y
+    from .qe import lib
+    lib().qe_gemm_w4_choice.restype = ctypes.c_int
+    r = call("qe_gemm_w4_choice", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
+             w.flags | (OUT_BF16 if out_bf16 else 0), cfg, ks, _stream())
+    return y, bool(r)
 
 
 def matmul_w4(w: W4, x, out_bf16=False, y=None):

@@ -4,6 +4,8 @@ Gate (BASELINE): max|y - ref| <= 2e-2 * rms(ref), ref = the oracle's dequantize-
 to bf16 as the reference does, bf16_rn((u - 8) * s), product in float64). That bf16 weight is exactly the operand
 this kernel multiplies, so fp32 outputs are also held to 1e-4 * rms (fp32 sums only), far inside the reference's own
 gate (tests/test_gemm.py:26-27, max|err| / max|ref| < 1e-2). Full BASELINE shapes are checked on sampled rows."""
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -84,11 +86,16 @@ def test_reference_named_gemm_hooks(dev):
     w, q, s = setup(n, k, 0, seed=11)
     x = synth.to_dev(synth.x_host(t, k, seed=12))
     ref = ops.gemm_w4(w, x)
-    for name in ("qe_gemm_w4", "qe_gemm_w4_t"):
-        y = torch.full((t, n), float("nan"), device=dev)
-        call(name, w.q, w.s, n, k, x, y, t)
-        torch.cuda.synchronize()
-        assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+    y = torch.full((t, n), float("nan"), device=dev)
+    call("qe_gemm_w4", w.q, w.s, n, k, x, y, t)
+    torch.cuda.synchronize()
+    assert torch.equal(y.view(torch.int32), ref.view(torch.int32))
+    # the tuned hook may choose another tile configuration: the same products, another fp32 summation order
+    yt = torch.full((t, n), float("nan"), device=dev)
+    call("qe_gemm_w4_t", w.q, w.s, n, k, x, yt, t)
+    torch.cuda.synchronize()
+    assert err_ratio(yt.cpu().numpy(), ref.cpu().numpy()) <= 1e-5
+    call("qe_gemm_tune_clear")
     call("qe_gemm_set_out_bf16", 1)
     try:
         yb = torch.full((t, n), float("nan"), device=dev, dtype=torch.bfloat16)
@@ -142,3 +149,69 @@ def test_gemm_w8_baseline_shape_sampled(dev):
     sel = torch.from_numpy(rows).to(dev)
     ref = oracle_ref_w8(synth.bits(x[sel].contiguous()), q, s, n, k, True)
     assert_bf16_close(out_f32(y[sel].contiguous()), ref)
+
+
+# n = 40960, t = 512: 2 x 160 tiles of 256 x 256 on 256 CUs leave a last round of 64 tiles, which the split runs as
+# 2 or 4 K ranges (stream-K of the tail); 256 x 128 tiles: 640, a tail of 128
+SPLIT_SHAPE = (40960, 1024, 512)
+
+
+@pytest.mark.parametrize("cfg,ks", [(0, 2), (0, 4), (1, 2)])
+def test_gemm_split_tail(dev, cfg, ks):
+    """the split of the last partial round: every output (split tiles and direct tiles) equals the unsplit GEMM to
+    fp32 summation order (1e-5 * rms), fp32, bf16 and GLU outputs; sampled rows vs the oracle"""
+    n, k, t = SPLIT_SHAPE
+    w, q, s = setup(n, k, 1, seed=5)
+    xh = synth.x_host(t, k, seed=6)
+    x = synth.to_dev(xh)
+    base, applied0 = ops.gemm_w4_choice(w, x, cfg, 1)
+    y, applied = ops.gemm_w4_choice(w, x, cfg, ks)
+    torch.cuda.synchronize()
+    assert applied and not applied0
+    b, yv = base.cpu().numpy(), y.cpu().numpy()
+    assert err_ratio(yv, b) <= 1e-5
+    rows = [0, 255, 256, 300, 511]  # the split tiles hold tokens 256..511
+    ref = oracle_ref(xh[rows], q, s, n, k, 1)
+    assert err_ratio(yv[rows], ref) <= 1e-4
+    yb, _ = ops.gemm_w4_choice(w, x, cfg, ks, out_bf16=True)
+    assert_bf16_close(out_f32(yb)[rows], ref)
+    wg, qg, sg = setup(n, k, 1, seed=7, glu=True)
+    ag, _ = ops.gemm_w4_choice(wg, x, cfg, ks)
+    a1, _ = ops.gemm_w4_choice(wg, x, cfg, 1)
+    torch.cuda.synchronize()
+    act = glu_act(matmul_f64(xh[rows], oracle.bf16_to_f32(oracle.dequant_w4(qg, sg, n, k, 1))))
+    assert_glu_close(out_f32(ag)[rows], act, 1e-4)
+    # two bf16 roundings of fp32 sums that differ in summation order: at most one bf16 step (2^-7 relative) apart
+    a1v, agv = out_f32(a1).astype(np.float64), out_f32(ag).astype(np.float64)
+    assert np.all(np.abs(agv - a1v) <= 1e-5 * np.sqrt(np.mean(a1v ** 2)) + 2.0 ** -7 * np.abs(a1v))
+
+
+def test_gemm_tuner_table_and_file(dev, tmp_path):
+    """qe_gemm_w4_t times the candidates once per (shape, token bucket) and keeps the choice; with a tuning file the
+    choice survives a cleared table (reloaded from the file) and the output is bit-identical"""
+    from qengine_amd import lib
+    lib().qe_gemm_tune_entries.restype = ctypes.c_int
+    n, k, t = 2048, 1024, 300
+    w, q, s = setup(n, k, 0, seed=9)
+    xh = synth.x_host(t, k, seed=10)
+    x = synth.to_dev(xh)
+    path = str(tmp_path / "tune.txt")
+    call("qe_gemm_tune_file", ctypes.c_char_p(path.encode()))
+    call("qe_gemm_tune_clear")
+    y = torch.empty(t, n, device=dev)
+    call("qe_gemm_w4_t", w.q, w.s, n, k, x, y, t)
+    torch.cuda.synchronize()
+    assert lib().qe_gemm_tune_entries() == 1
+    assert err_ratio(y.cpu().numpy(), oracle_ref(xh, q, s, n, k, 0)) <= 1e-4
+    txt = open(path).read().splitlines()
+    assert txt[0].startswith("qengine_amd gemm tune v1") and txt[1].startswith("device ") and len(txt) == 3
+    call("qe_gemm_tune_clear")
+    assert lib().qe_gemm_tune_entries() == 0
+    call("qe_gemm_tune_file", ctypes.c_char_p(path.encode()))
+    assert lib().qe_gemm_tune_entries() == 1
+    y2 = torch.empty(t, n, device=dev)
+    call("qe_gemm_w4_t", w.q, w.s, n, k, x, y2, t)
+    torch.cuda.synchronize()
+    assert lib().qe_gemm_tune_entries() == 1 and torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    call("qe_gemm_tune_file", ctypes.c_char_p(b""))
+    call("qe_gemm_tune_clear")
