@@ -99,6 +99,22 @@ int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, 
 /* qe_gemv_w4 on an explicit stream. Replaces reference src/capi.cpp:101. */
 void qe_gemv_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, void* stream);
 
+/* ---- H16 decode numerics (the reference's default decode, src/kernels/gemv_h16.cuh, gemv.cu:1537-1583) ----
+ * XH layout: fp16 x / 16 with |x| clamped to 2047, the columns of each 64-k chunk permuted (k bits b0..b5 ->
+ * b0 | b3<<1 | b4<<2 | b5<<3 | b1<<4 | b2<<5). Weights as exact integers in fp16, f16 MFMA over each 64-k chunk, the
+ * chunk partial rounded to fp16, then added to fp32 at group scale x 16. Every row count gives the same bits per row.
+ * Replaces reference src/capi.cpp:55-66. */
+/* bf16 x [m][k] -> XH [m][ldxh] (k % 64 == 0) */
+void qe_xh_pack(const uint16_t* x, int k, int m, void* xh, int ldxh);
+/* packs x into xh_ws [m][k] fp16, then the H16 GEMV; glu: y is the bf16 act [m][n/2]; yh (optional): XH copy of y */
+void qe_gemv_w4h(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu, void* xh_ws,
+                 void* yh);
+/* x already XH, stride ldx */
+void qe_gemv_w4hx(const void* q, const void* s, int n, int k, const uint16_t* xh, float* y, int m, int glu, int ldx);
+/* build-defined: scales dtype / output bf16 / GLU by flags, explicit strides and stream, optional yh [m][ldyh] */
+void qe_gemv_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* xh, int ldx, void* y, int ldy, int m,
+                    int flags, void* yh, int ldyh, void* stream);
+
 /* prefill GEMM: c[t][n] (fp32, or bf16 after qe_gemm_set_out_bf16(1)) = x[t][k] . W^T.
  * Replaces reference src/capi.cpp:84 (gemm_w4, gemm.cu:4361). */
 void qe_gemm_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t);
@@ -134,9 +150,10 @@ void qe_repack_q8(const int32_t* q, const uint16_t* s, int n, int k, void* dq, v
 void qe_glu_rows8(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq, uint16_t* ds);
 
 /* decode GEMV of a Q8 matrix, y fp32 [m][n] (glu: the bf16 activation [m][n/2]), any m (row blocks of 16).
- * Replaces reference src/capi.cpp:28. h16 selects the reference's fp16-accumulate XH numerics there; this build
- * computes fp32 accumulation of bf16 products for both values (xh_ws unused) and does not produce the XH copy
- * (yh must be NULL). */
+ * Replaces reference src/capi.cpp:28. h16 = 1: the H16 numerics (x packed into xh_ws [m][k] fp16 in the XH layout,
+ * w / 16 in fp16, f16 MFMA per 64-k chunk rounded to fp16, flushed into fp32 at scale x 256), and yh (if not NULL)
+ * receives the outputs again in the XH layout [m][n or n/2] (n or n/2 a multiple of 64); h16 = 0: fp32 accumulation of
+ * bf16 products, xh_ws unused, yh must be NULL. */
 void qe_gemv_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu, int h16,
                 void* xh_ws, void* yh);
 

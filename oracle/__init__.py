@@ -21,6 +21,10 @@ Parity pins (each function is checked against something other than itself in tes
   dequant_q8        closed form bf16_rn((u - 128) * s) in numpy
   moe_pack          records decoded back to the source rows with the independent fragment decoder
   moe_ref           float64 composite of the pinned pieces above (the layer's checker)
+  xh_pos / xh_pack  the lane / k-step statement of the XH layout (gemv_h16.cuh:8-10) for every position, bijection
+                    per 64-k chunk, torch's clamp + fp16 conversion for the values
+  gemv_h16          exact on integer-valued inputs (equal to the float64 product), and elsewhere within the
+                    closed-form bound of one fp16 rounding per 64-k chunk of the float64 product
 """
 import ctypes
 import os
@@ -281,3 +285,46 @@ def moe_ref(logits, x, gu_q, gu_s, dn_q, dn_s, topk, H, I, tokens=None, exact=Fa
             act = gu[:I] / (1 + np.exp(-gu[:I])) * gu[I:]
             out[r] += float(w[t, k]) * (wdn @ act)
     return out, sel, w
+
+
+# ---------------------------------------------------------------- H16 (fp16-accumulate decode on XH activations)
+def xh_pos(k):
+    """column of activation k inside an XH row (reference src/kernels/gemv_h16.cuh:22-27): within each 64-k chunk
+    the k bits b0..b5 move to b0 | b3<<1 | b4<<2 | b5<<3 | b1<<4 | b2<<5"""
+    k = np.asarray(k, np.int64)
+    return (k & ~63) | (k & 1) | ((k >> 2) & 14) | ((k & 6) << 3)
+
+
+def to_xh(v):
+    """fp32 values -> fp16 bits of clamp(v, -2047, 2047) / 16, round to nearest even (gemv_h16.cuh:28-30)"""
+    c = np.clip(np.asarray(v, np.float32), np.float32(-2047), np.float32(2047)) * np.float32(0.0625)
+    return c.astype(np.float16).view(np.uint16)
+
+
+def xh_pack(x, ldxh=None):
+    """bf16 bits [m][k] -> XH fp16 bits [m][ldxh] (gemv.cu:1530-1534 xh_pack); columns k..ldxh stay 0"""
+    m, k = x.shape
+    out = np.zeros((m, ldxh or k), np.uint16)
+    out[:, xh_pos(np.arange(k))] = to_xh(bf16_to_f32(x))
+    return out
+
+
+def xh_values(xh, k):
+    """XH fp16 bits [m][>= k] -> the stored values x / 16 in natural column order (float64)"""
+    return np.ascontiguousarray(xh[:, xh_pos(np.arange(k))]).view(np.float16).astype(np.float64)
+
+
+def gemv_h16(xv, w, s, wdiv=1):
+    """the H16 decode arithmetic (gemv_h16.cuh:12-15 and xh_flush :59-67; Q8: gemv.cu:786-792): xv [m][k] the XH
+    values (x / 16), w [n][k] the exact integer weights, s [n][k/128] the group scales (float). Every 64-k chunk's
+    partial sum of xv * (w / wdiv) (wdiv = 16 for Q8) is formed exactly and rounded once to fp16, then added at
+    scale * 16 * wdiv. Returns float64 [m][n]; the kernels add the flushed chunks in fp32."""
+    xv = np.asarray(xv, np.float64)
+    m, k = xv.shape
+    wf = np.asarray(w, np.float64) / wdiv
+    sf = np.asarray(s, np.float64) * (16.0 * wdiv)
+    acc = np.zeros((m, wf.shape[0]))
+    for c in range(k // 64):
+        part = xv[:, 64 * c:64 * c + 64] @ wf[:, 64 * c:64 * c + 64].T
+        acc += part.astype(np.float16).astype(np.float64) * sf[:, c // 2][None, :]
+    return acc

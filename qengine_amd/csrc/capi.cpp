@@ -135,6 +135,34 @@ void qe_gemm_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x,
 
 void qe_gemm_set_out_bf16(int on) { gemm_set_out_bf16(on != 0); }
 
+void qe_xh_pack(const uint16_t* x, int k, int m, void* xh, int ldxh) {
+    xh_pack(x, k, k, m, reinterpret_cast<uint16_t*>(xh), ldxh, 0);
+}
+
+void qe_gemv_w4h(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu, void* xh_ws,
+                 void* yh) {
+    CHECK(xh_ws != nullptr, "qe_gemv_w4h: needs the XH workspace xh_ws [m][k] fp16");
+    gemv_workspace_init();
+    xh_pack(x, k, k, m, reinterpret_cast<uint16_t*>(xh_ws), k, 0);
+    const int ldy = glu ? n / 2 : n;
+    gemv_h16(reinterpret_cast<const uint4*>(q), reinterpret_cast<const uint16_t*>(s), n, k, kScaleBF16, false, glu != 0,
+             reinterpret_cast<const uint16_t*>(xh_ws), k, y, ldy, m, false, reinterpret_cast<uint16_t*>(yh), ldy, 0);
+}
+
+void qe_gemv_w4hx(const void* q, const void* s, int n, int k, const uint16_t* xh, float* y, int m, int glu, int ldx) {
+    gemv_workspace_init();
+    gemv_h16(reinterpret_cast<const uint4*>(q), reinterpret_cast<const uint16_t*>(s), n, k, kScaleBF16, false, glu != 0,
+             xh, ldx, y, glu ? n / 2 : n, m, false, nullptr, 0, 0);
+}
+
+void qe_gemv_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* xh, int ldx, void* y, int ldy, int m,
+                    int flags, void* yh, int ldyh, void* stream) {
+    gemv_workspace_init();
+    gemv_h16(reinterpret_cast<const uint4*>(q), reinterpret_cast<const uint16_t*>(s), n, k,
+             (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16, false, (flags & QE_GLU) != 0, xh, ldx, y, ldy, m,
+             (flags & QE_OUT_BF16) != 0, reinterpret_cast<uint16_t*>(yh), ldyh, as_stream(stream));
+}
+
 void qe_quantize_w8(const uint16_t* w, int n, int k, void* dq, void* ds) {
     quantize_w8(w, n, k, reinterpret_cast<uint4*>(dq), reinterpret_cast<uint16_t*>(ds), 0);
 }
@@ -163,14 +191,20 @@ void qe_glu_rows8(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq
 
 void qe_gemv_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu, int h16,
                 void* xh_ws, void* yh) {
-    (void)h16;
-    (void)xh_ws;
-    CHECK(yh == nullptr, "qe_gemv_q8: the fp16 (XH) activation copy yh is not produced by this build");
+    CHECK(!h16 || xh_ws != nullptr, "qe_gemv_q8: h16 needs the XH workspace xh_ws [m][k] fp16");
+    CHECK(h16 || yh == nullptr, "qe_gemv_q8: yh (the XH copy) is an output of the h16 path");
     gemv_workspace_init();
+    const int ldy = glu ? n / 2 : n;
+    if (h16) {
+        xh_pack(x, k, k, m, reinterpret_cast<uint16_t*>(xh_ws), k, 0);
+        gemv_h16(reinterpret_cast<const uint4*>(q), reinterpret_cast<const uint16_t*>(s), n, k, kScaleBF16, true,
+                 glu != 0, reinterpret_cast<const uint16_t*>(xh_ws), k, y, ldy, m, false,
+                 reinterpret_cast<uint16_t*>(yh), ldy, 0);
+        return;
+    }
     W8 w = mk_w8(q, s, n, k, false, kScaleBF16);
     w.q8 = true;
     w.glu = glu != 0;
-    const int ldy = glu ? n / 2 : n;
     const size_t esz = glu ? 2 : 4;
     for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
         const int mm = m - r0 < kMaxGemvRows ? m - r0 : kMaxGemvRows;

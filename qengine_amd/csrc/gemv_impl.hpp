@@ -43,6 +43,32 @@ __device__ __forceinline__ u32x4_v ld_stream(const uint4* p) {
 __device__ __forceinline__ uint32_t bf16x2_b02(uint32_t t) { return __builtin_amdgcn_perm(0x43434343u, t, 0x04020400u); }
 __device__ __forceinline__ uint32_t bf16x2_b13(uint32_t t) { return __builtin_amdgcn_perm(0x43434343u, t, 0x04030401u); }
 constexpr uint32_t kNib = 0x0F0F0F0Fu;
+// the same with the fp16 magic 0x64 (1024 + u) and packed fp16 arithmetic (v_pk_add_f16 / v_pk_fma_f16; packed fp16
+// is not the packed fp32 these kernels avoid): the exact integer u - 8, and for bytes u = w + 128, w / 16
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint32_t f16x2_b02(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04020400u); }
+__device__ __forceinline__ uint32_t f16x2_b13(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04030401u); }
+__device__ __forceinline__ uint32_t f16x2_sub1032(uint32_t p) {
+    const f16x2_v v = __builtin_bit_cast(f16x2_v, p) - f16x2_v{(_Float16)1032.f, (_Float16)1032.f};
+    return __builtin_bit_cast(uint32_t, v);
+}
+// XH activation layout (reference gemv_h16.cuh:1-30): x / 16 in fp16 with |x| clamped to 2047 first, the columns of
+// every 64-k chunk permuted: k bits b0..b5 -> p = b0 | b3 << 1 | b4 << 2 | b5 << 3 | b1 << 4 | b2 << 5, which is
+// p = 16 t + 4 j + e for k = 16 j + 2 t + {0, 1, 8, 9}[e]: the class-major order the decode kernels stage
+__device__ __forceinline__ int xh_pos(int k) { return (k & ~63) | (k & 1) | ((k >> 2) & 14) | ((k & 6) << 3); }
+// The magnitude is scaled and rounded, then the sign is put back by hand: hipcc folds a scale-and-convert into
+// v_fma_mixlo_f16 with a +0 addend, which turns -0 into +0. NaN clamps to -2047 (what fmaxf(NaN, -2047) gives).
+__device__ __forceinline__ uint16_t to_xh(float v) {
+    const float c = v == v ? v : -2047.f;
+    const uint16_t mag = __builtin_bit_cast(uint16_t, (_Float16)(fminf(fabsf(c), 2047.f) * 0.0625f));
+    return mag | static_cast<uint16_t>((__builtin_bit_cast(uint32_t, c) >> 16) & 0x8000u);
+}
+__device__ __forceinline__ uint32_t f16x2_q8(uint32_t p) {
+    const f16x2_v v = __builtin_bit_cast(f16x2_v, p) * f16x2_v{(_Float16)0.0625f, (_Float16)0.0625f} -
+                      f16x2_v{(_Float16)72.f, (_Float16)72.f};
+    return __builtin_bit_cast(uint32_t, v);
+}
 template <int CTRL>
 __device__ __forceinline__ float dpp_add(float v) {
     return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,

@@ -23,3 +23,19 @@ void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     if (w.sdt == kScaleF16) launch_gemv<kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else launch_gemv<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }
+
+void gemv_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8, bool glu, const uint16_t* xh, int ldx,
+              void* y, int ldy, int m, bool out_bf16, uint16_t* yh, int ldyh, hipStream_t st) {
+    CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && m >= 1, "gemv_h16 %d %d %d", n, k, m);
+    CHECK(ldx >= k && ldx % 8 == 0 && ((uintptr_t)xh & 15) == 0, "gemv_h16: XH rows 16-byte aligned, ldx %d", ldx);
+    CHECK(ldy >= (glu ? n / 2 : n), "gemv_h16 ldy %d", ldy);
+    CHECK(!yh || (ldyh >= (glu ? n / 2 : n) && (glu ? n / 2 : n) % 64 == 0), "gemv_h16: yh needs %d columns, a "
+          "multiple of 64 (ldyh %d)", glu ? n / 2 : n, ldyh);
+    const int out = glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    const size_t esz = (glu || out_bf16) ? 2 : 4;
+    for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
+        const int mm = m - r0 < kMaxGemvRows ? m - r0 : kMaxGemvRows;
+        skinny_h16(q, s, n, k, sdt, q8, xh + (size_t)r0 * ldx, ldx, reinterpret_cast<char*>(y) + (size_t)r0 * ldy * esz,
+                   ldy, mm, out, yh ? yh + (size_t)r0 * ldyh : nullptr, ldyh, st);
+    }
+}

@@ -56,6 +56,14 @@ void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, i
 // m = 1 decode GEMV on the matrix cores (gemv1.hip); false when the shape takes the VALU GEMV (uneven K slices,
 // x not 16-byte aligned). out as for skinny_w4_mfma
 bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st);
+// H16 decode numerics (the reference's gemv_w4h, gemv_h16.cuh): XH activations (xh_pack), m = 1..16 per launch,
+// W4 or Q8 (q8) records; out as for skinny_w4_mfma; yh: optional XH copy of the outputs [m][ldyh]
+void xh_pack(const uint16_t* x, int ldx, int k, int m, uint16_t* xh, int ldxh, hipStream_t st);
+void skinny_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8, const uint16_t* xh, int ldx, void* y,
+                int ldy, int m, int out, uint16_t* yh, int ldyh, hipStream_t st);
+// any m (16-row launches); checks the shapes
+void gemv_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8, bool glu, const uint16_t* xh, int ldx,
+              void* y, int ldy, int m, bool out_bf16, uint16_t* yh, int ldyh, hipStream_t st);
 // the m = 1 GEMV's record stream with no arithmetic (its HBM read floor); falls back to 4-group slices where the
 // GEMV has no even slicing
 void read_probe_w4(const void* q, int n, int k, uint32_t* sink, hipStream_t st);

@@ -71,12 +71,15 @@ constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][
     return stage > RT * 256 ? stage : RT * 256;
 }
 
-template <int MT, int SDT, int NG, int RT, int FMT, int D = skinny_d<MT, NG, RT, FMT>(),
+// H16: the reference's fp16 decode numerics (XH activations x / 16 in fp16 already in class-major order, weights as
+// exact integers in fp16 (Q8: w / 16), f16 MFMAs, every 64-k chunk's partial rounded to fp16 and flushed into fp32
+// with the group scale x 16 (Q8 x 256)); W4 and Q8 only
+template <int MT, int SDT, int NG, int RT, int FMT, bool H16 = false, int D = skinny_d<MT, NG, RT, FMT>(),
           int WPE = skinny_wpe<MT, NG, RT, FMT>()>
 __global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
 __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K, const uint16_t* __restrict__ x,
-    int ldx, void* __restrict__ y, int ldy, int m, int out, int sdt) {
+    int ldx, void* __restrict__ y, int ldy, int m, int out, int sdt, uint16_t* __restrict__ yh = nullptr, int ldyh = 0) {
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
     constexpr bool UPX = skinny_upx<MT, NG>();
     constexpr int WSZ = skinny_wsz<MT, NG, RT>();
@@ -118,7 +121,8 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             if (MT >= 4 || (L >> 4) < MT) {
 #pragma unroll
                 for (int c = 0; c < 4; c++)
-                    xl[(buf * MT + xrow_of(e)) * kXStride + x_slot<kFmtW4>(4 * (L & 15) + c)] = src[e][c];
+                    xl[(buf * MT + xrow_of(e)) * kXStride + (H16 ? 4 * (L & 15) + c : x_slot<kFmtW4>(4 * (L & 15) + c))] =
+                        src[e][c];
             }
     };
 
@@ -176,7 +180,8 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                 for (int tok = 0; tok < MT; tok++)
 #pragma unroll
                     for (int e = 0; e < 8; e++)
-                        xl[((pc >> 3) * MT + tok) * kXStride + x_slot<kFmtW4>(8 * (pc & 7) + e)] = xv[pr][tok][e >> 2][e & 3];
+                        xl[((pc >> 3) * MT + tok) * kXStride + (H16 ? 8 * (pc & 7) + e : x_slot<kFmtW4>(8 * (pc & 7) + e))] =
+                            xv[pr][tok][e >> 2][e & 3];
             }
         }
     } else {
@@ -240,11 +245,26 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
 #pragma unroll
             for (int r = 0; r < RT; r++) {
                 u32x4_v a;
-                if constexpr (FMT == kFmtW4) {
+                if constexpr (FMT == kFmtW4 && H16) {
+                    // fp16 (1024 + u) by the 0x64 magic, minus 1032: the exact integer w = u - 8
+                    const u32x4_v rec = rc[r][mm >> 1];
+                    const uint32_t t0 = (rec[j0] >> sh) & kNib, t1 = (rec[j0 + 1] >> sh) & kNib;
+                    const uint32_t p[4] = {f16x2_b02(t0), f16x2_b13(t0), f16x2_b02(t1), f16x2_b13(t1)};
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) a[q4] = f16x2_sub1032(p[q4]);
+                } else if constexpr (FMT == kFmtW4) {
                     const u32x4_v rec = rc[r][mm >> 1];
                     const uint32_t w0 = rec[j0], w1 = rec[j0 + 1];
                     const uint32_t t0 = (w0 >> sh) & kNib, t1 = (w1 >> sh) & kNib;  // row i: k0, k0 + 8, k0 + 1, k0 + 9
                     a = u32x4_v{bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
+                } else if constexpr (FMT == kFmtQ8 && H16) {
+                    // bytes u = w + 128 -> fp16 (1024 + u) by the 0x64 magic -> (1024 + u) / 16 - 72 = w / 16 (exact)
+                    const u32x4_v rec = rc[r][mm];
+                    const bool hh = sh != 0;
+                    const uint32_t wa = (hh ? rec[1] : rec[0]) ^ 0x80808080u, wb = (hh ? rec[3] : rec[2]) ^ 0x80808080u;
+                    const uint32_t p[4] = {f16x2_b02(wa), f16x2_b13(wa), f16x2_b02(wb), f16x2_b13(wb)};
+#pragma unroll
+                    for (int q4 = 0; q4 < 4; q4++) a[q4] = f16x2_q8(p[q4]);
                 } else if constexpr (FMT == kFmtQ8) {
                     // record of 32-k chunk mm: word 2 s + hh holds row g + 8 hh, the signed weights w at
                     // k0 + {0, 8, 1, 9}, k0 = 32 mm + 16 s + 2 t: bytes (0, 2) and (1, 3) of u = w + 128 are the B
@@ -272,12 +292,34 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                                                       0x07060302u);
                     }
                 }
-                c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c[r], 0, 0, 0);
-                c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c[r], 0, 0, 0);
+                if constexpr (H16) {
+                    c[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a),
+                                                                   __builtin_bit_cast(f16x8_v, b), c[r], 0, 0, 0);
+                } else {
+                    c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c[r], 0, 0, 0);
+                    c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c[r], 0, 0, 0);
+                }
+            }
+            if constexpr (H16) {
+                if (mm & 1) {  // end of a 64-k chunk: its partial in fp16, then into fp32 at the group scale x 16 (x 256)
+#pragma unroll
+                    for (int r = 0; r < RT; r++) {
+                        const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[(r * NGM + ii) * 16 + 4 * qg]);
+                        constexpr float kF = FMT == kFmtQ8 ? 256.f : 16.f;
+                        const float sc[4] = {scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt) * kF,
+                                             scale_rt<SDT>((uint16_t)(sv.x >> 16), sdt) * kF,
+                                             scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt) * kF,
+                                             scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt) * kF};
+#pragma unroll
+                        for (int j = 0; j < 4; j++) acc[r][j] = fmaf((float)(_Float16)c[r][j], sc[j], acc[r][j]);
+                        c[r] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+                    }
+                }
             }
         }
 #pragma unroll
         for (int r = 0; r < RT; r++) {
+            if constexpr (H16) break;  // flushed per 64-k chunk above
             // rows 4 qg .. 4 qg + 3 of the group's scales
             const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[(r * NGM + (FMT == kFmtW8C ? 0 : ii)) * 16 + 4 * qg]);
             acc[r][0] = fmaf(scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt), c[r][0], acc[r][0]);
@@ -309,23 +351,27 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     if (out == kOutGLU) {
         for (int idx = threadIdx.x; idx < RT * m * 8; idx += blockDim.x) {
             const int r = idx / (m * 8), tok = (idx >> 3) - r * m, gg = idx & 7;
-            reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + 8 * (tile0 + r) + gg] =
-                f32_to_bf16(silu_f32(rsum(r, tok, gg)) * rsum(r, tok, gg + 8));
+            const int col = 8 * (tile0 + r) + gg;
+            const float v = silu_f32(rsum(r, tok, gg)) * rsum(r, tok, gg + 8);
+            reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + col] = f32_to_bf16(v);
+            if (yh) yh[(size_t)tok * ldyh + xh_pos(col)] = to_xh(v);
         }
     } else {
         for (int idx = threadIdx.x; idx < RT * m * 16; idx += blockDim.x) {
             const int r = idx / (m * 16), tok = (idx >> 4) - r * m, rr = idx & 15;
             const float v = rsum(r, tok, rr);
-            const size_t o = (size_t)tok * ldy + 16 * (tile0 + r) + rr;
+            const int col = 16 * (tile0 + r) + rr;
+            const size_t o = (size_t)tok * ldy + col;
             if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[o] = f32_to_bf16(v);
             else reinterpret_cast<float*>(y)[o] = v;
+            if (yh) yh[(size_t)tok * ldyh + xh_pos(col)] = to_xh(v);
         }
     }
 }
 
-template <int FMT, int SDT>
+template <int FMT, int SDT, bool H16 = false>
 void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
-            int out, int sdt, hipStream_t st) {
+            int out, int sdt, hipStream_t st, uint16_t* yh = nullptr, int ldyh = 0) {
     // the K slices of the m = 1 matrix-core kernel where they divide K, else the generic uneven slices; they depend
     // on (n, k) only, so every m in 2..16 sums a row in the same order (the rows of a batch equal the rows alone)
     const int dg = decode_groups(n, k);
@@ -341,13 +387,13 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     do {                                                                                                            \
         constexpr int RT_ = skinny_rt<MT_, NG_, FMT>();                                                             \
         if (RT_ == 2 && rt2)                                                                                        \
-            skinny_kernel<MT_, SDT, NG_, RT_, FMT><<<dim3((unsigned)(n / (16 * RT_))), block,                       \
+            skinny_kernel<MT_, SDT, NG_, RT_, FMT, H16><<<dim3((unsigned)(n / (16 * RT_))), block,                  \
                                          (size_t)sc.S * skinny_wsz<MT_, NG_, RT_>() * 4, st>>>(                    \
-                q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                           \
+                q, s, n, k, x, ldx, y, ldy, m, out, sdt, yh, ldyh);                                                 \
         else                                                                                                        \
-            skinny_kernel<MT_, SDT, NG_, 1, FMT><<<dim3((unsigned)(n / 16)), block,                                 \
+            skinny_kernel<MT_, SDT, NG_, 1, FMT, H16><<<dim3((unsigned)(n / 16)), block,                            \
                                               (size_t)sc.S * skinny_wsz<MT_, NG_, 1>() * 4, st>>>(                 \
-                    q, s, n, k, x, ldx, y, ldy, m, out, sdt);                                                       \
+                    q, s, n, k, x, ldx, y, ldy, m, out, sdt, yh, ldyh);                                             \
     } while (0)
 #define QE_SK_NG(MT_)                             \
     do {                                          \
@@ -374,6 +420,31 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
 void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
     if (w.sdt == kScaleF16) qe_skinny::launch<qe_gemv::kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else qe_skinny::launch<qe_gemv::kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+}
+
+// bf16 activations -> the XH layout (one thread per value)
+__global__ void xh_pack_kernel(const uint16_t* __restrict__ x, int ldx, int K, int m, uint16_t* __restrict__ xh,
+                               int ldxh) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)m * K) return;
+    const int r = (int)(idx / K), k = (int)(idx % K);
+    xh[(size_t)r * ldxh + qe_gemv::xh_pos(k)] = qe_gemv::to_xh(bf16_to_f32(x[(size_t)r * ldx + k]));
+}
+
+void xh_pack(const uint16_t* x, int ldx, int k, int m, uint16_t* xh, int ldxh, hipStream_t st) {
+    CHECK(k % 64 == 0 && m >= 1 && ldx >= k && ldxh >= k && ldxh % 64 == 0, "xh_pack k %d m %d ldxh %d", k, m, ldxh);
+    const size_t nthreads = (size_t)m * k;
+    xh_pack_kernel<<<dim3((unsigned)((nthreads + 255) / 256)), dim3(256), 0, st>>>(x, ldx, k, m, xh, ldxh);
+    HIP_CHECK(hipGetLastError());
+}
+
+// H16 numerics (XH activations, see skinny_kernel): W4 and Q8; yh (optional): the outputs again as XH
+void skinny_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8, const uint16_t* xh, int ldx, void* y,
+                int ldy, int m, int out, uint16_t* yh, int ldyh, hipStream_t st) {
+    using namespace qe_gemv;
+    if (q8) qe_skinny::launch<kFmtQ8, -1, true>(reinterpret_cast<const uint4*>(q), s, n, k, xh, ldx, y, ldy, m, out, sdt, st, yh, ldyh);
+    else if (sdt == kScaleF16) qe_skinny::launch<kFmtW4, kScaleF16, true>(q, s, n, k, xh, ldx, y, ldy, m, out, sdt, st, yh, ldyh);
+    else qe_skinny::launch<kFmtW4, kScaleBF16, true>(q, s, n, k, xh, ldx, y, ldy, m, out, sdt, st, yh, ldyh);
 }
 
 // INT8 (W8 layout with per-channel or group scales, or the Q8 layout; the scale dtype a run-time value)

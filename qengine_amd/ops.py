@@ -126,6 +126,40 @@ def gemv_w4(w: W4, x, out_bf16=False, y=None):
     return y
 
 
+def xh_pack(x, ldxh=None):
+    """bf16 [m][k] -> the XH layout [m][ldxh] fp16 (x / 16, |x| clamped to 2047, columns of each 64-k chunk permuted);
+    reference hook qe_xh_pack"""
+    m, k = x.shape
+    ldxh = k if ldxh is None else ldxh
+    assert x.dtype == torch.bfloat16 and x.is_contiguous() and k % 64 == 0 and ldxh >= k and ldxh % 64 == 0
+    xh = torch.zeros(m, ldxh, dtype=torch.float16, device=x.device)
+    call("qe_xh_pack", x, k, m, xh, ldxh)
+    return xh
+
+
+def gemv_w4h(w: W4, x, yh=False):
+    """H16 decode GEMV on bf16 activations (reference hook qe_gemv_w4h, bf16 scales): packs x into an XH workspace,
+    then fp16 chunk partials flushed into fp32. -> (y, xh, yh): y fp32 [m][n] (GLU: bf16 act [m][n/2]), yh the XH
+    copy of y when asked for"""
+    m = x.shape[0]
+    assert w.s.dtype == torch.bfloat16 and x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.is_contiguous()
+    y = _out(m, w.n, False, w.glu, x.device)
+    xh = torch.empty(m, w.k, dtype=torch.float16, device=x.device)
+    yo = torch.empty(m, w.n // 2 if w.glu else w.n, dtype=torch.float16, device=x.device) if yh else None
+    call("qe_gemv_w4h", w.q, w.s, w.n, w.k, x, y, m, int(w.glu), xh, yo)
+    return y, xh, yo
+
+
+def gemv_w4hx(w: W4, xh, out_bf16=False, yh=None, y=None):
+    """H16 decode GEMV on activations already in the XH layout (qe_gemv_w4h_ex: any scale dtype, strides, stream)"""
+    m = xh.shape[0]
+    assert xh.dtype == torch.float16 and xh.shape[1] >= w.k and xh.stride(1) == 1
+    y = _out(m, w.n, out_bf16, w.glu, xh.device) if y is None else y
+    call("qe_gemv_w4h_ex", w.q, w.s, w.n, w.k, xh, xh.stride(0), y, y.stride(0), m,
+         w.flags | (OUT_BF16 if out_bf16 else 0), yh, 0 if yh is None else yh.stride(0), _stream())
+    return y
+
+
 def gemm_w4(w: W4, x, out_bf16=False, y=None):
     t = x.shape[0]
     assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
@@ -224,13 +258,20 @@ def repack_q8(q, s, glu=False):
     return Q8(dq, ds, n, k, glu)
 
 
-def gemv_q8(w: Q8, x):
-    """decode GEMV (any m): fp32 [m][n], or the GLU bf16 activation [m][n/2] (reference hook qe_gemv_q8)"""
+def gemv_q8(w: Q8, x, h16=False, yh=False):
+    """decode GEMV (any m): fp32 [m][n], or the GLU bf16 activation [m][n/2] (reference hook qe_gemv_q8).
+    h16: the fp16-accumulate XH numerics; returns (y, xh workspace, yh or None) then, else y"""
     m = x.shape[0]
     assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.is_contiguous()
+    assert h16 or not yh
     y = _out(m, w.n, False, w.glu, x.device)
-    call("qe_gemv_q8", w.q, w.s, w.n, w.k, x, y, m, int(w.glu), 0, None, None)
-    return y
+    if not h16:
+        call("qe_gemv_q8", w.q, w.s, w.n, w.k, x, y, m, int(w.glu), 0, None, None)
+        return y
+    xh = torch.empty(m, w.k, dtype=torch.float16, device=x.device)
+    yo = torch.empty(m, w.n // 2 if w.glu else w.n, dtype=torch.float16, device=x.device) if yh else None
+    call("qe_gemv_q8", w.q, w.s, w.n, w.k, x, y, m, int(w.glu), 1, xh, yo)
+    return y, xh, yo
 
 
 def gemm_q8(w: Q8, x):

@@ -44,6 +44,10 @@ def test_library_exports_every_declared_symbol():
     # the allocation-free MoE layer rejects a workspace above its scratch array before touching the GPU
     ("lib.qe_moe_w4_noalloc(None, None, None, 100000, 512, 10, 2048, 512, None, 0, None)",
      "qe_moe_w4_noalloc: T 100000"),
+    # the H16 paths need the caller's XH workspace (reference tests/test_q8.py:62-67 passes it)
+    ("lib.qe_gemv_q8(None, None, 64, 256, None, None, 1, 0, 1, None, None)", "h16 needs the XH workspace"),
+    ("lib.qe_gemv_q8(None, None, 64, 256, None, None, 1, 0, 0, None, ctypes.c_void_p(64))", "output of the h16 path"),
+    ("lib.qe_gemv_w4h(None, None, 64, 256, None, None, 1, 0, None, None)", "qe_gemv_w4h: needs the XH workspace"),
 ])
 def test_precondition_aborts_with_check_message(call, msg):
     code = f"import ctypes; lib = ctypes.CDLL({LIB!r}); {call}"

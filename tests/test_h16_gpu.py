@@ -1,0 +1,247 @@
+"""H16 decode numerics (reference src/kernels/gemv_h16.cuh, hooks src/capi.cpp:55-66 and :28 with h16 = 1) through the
+C-ABI vs the CPU oracle.
+
+Gates:
+  * XH packing (qe_xh_pack, the workspace the hooks fill): bit-exact with the oracle.
+  * integer-valued inputs (x / 16 and the weights integers, power-of-two row scales): every fp16 chunk partial and
+    every fp32 sum is exact, so the outputs equal the float64 product bit for bit.
+  * random inputs: within 1e-5 relative rms (max 1e-3 of rms) of the oracle's H16 emulation (the chunk partial
+    formed exactly and rounded once to fp16; the kernels sum a chunk in fp32 before that rounding, which moves a
+    partial by one fp16 ulp where the exact sum lies next to a rounding boundary).
+  * the reference's own gate (tests/test_q8.py:102-105): error vs the exact float64 product below twice the bf16
+    rounding of that product + 1e-4 (relative rms); GLU within 1e-2.
+  * batch == alone (tests/test_q8.py:86-100): every row bit-identical for m in MS against the same rows of an m = 64
+    call, plain, GLU and the XH output copy yh.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qengine_amd import ops, synth
+from test_gemv_gpu import assert_glu_close, glu_act
+
+pytestmark = pytest.mark.gpu
+
+MS = [1, 2, 3, 5, 8, 9, 12, 16, 17, 24, 25, 32, 33, 40, 48, 64]  # reference tests/test_q8.py:28
+
+
+def relrms(a, b):
+    a, b = np.asarray(a, np.float64), np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def x_outliers(m, k, seed):
+    """bf16 activations with channel outliers (amax / rms per row ~ 15-60), the distribution of the reference's
+    make_x (tests/test_gemm_i8.py:41-49), drawn with numpy"""
+    rng = np.random.default_rng(seed)
+    ch = np.exp(rng.standard_normal(k) * 0.6)
+    ch[rng.permutation(k)[:max(1, k // 200)]] *= 12.0
+    x = rng.standard_normal((m, k)) * ch * np.exp(rng.standard_normal((m, 1)) * 0.3)
+    return synth.np_bf16(x.astype(np.float32))
+
+
+def w4_bf16(n, k, seed, glu=False):
+    """W4 with bf16 scales (the reference hooks' scale type) -> (device W4, signed weights [n][k], scales f32)"""
+    q, s = synth.w4_host(n, k, seed=seed, sdt=0)
+    if glu:
+        q, s = oracle.glu_rows(q, s, n, k)
+    w = ops.repack_w4(synth.to_dev(q), synth.to_dev(s, torch.bfloat16), glu=glu)
+    return w, oracle.unpack_w4(q, n, k), oracle.bf16_to_f32(s)
+
+
+def q8_bf16(n, k, seed, glu=False, wmul=1):
+    """Q8 layer weights -> (device Q8, signed weights [n][k] in the kernel's row order, scales f32)"""
+    rng = np.random.default_rng(seed)
+    w = rng.integers(-127 // wmul, 127 // wmul + 1, size=(n, k)).astype(np.int64) * wmul
+    u = (w + 128).astype(np.uint32).reshape(n, k // 4, 4)
+    q = (u[..., 0] | (u[..., 1] << 8) | (u[..., 2] << 16) | (u[..., 3] << 24)).view(np.int32)
+    s = synth.np_bf16((rng.random((n, k // 128)) * 0.01 + 0.001).astype(np.float32))
+    if glu:
+        q, s = oracle.glu_rows(q, s, n, k, bits=8)
+        w = interleave(w)
+    wq = ops.repack_q8(synth.to_dev(q), synth.to_dev(s, torch.bfloat16))
+    wq.glu = glu
+    return wq, w, oracle.bf16_to_f32(s)
+
+
+def interleave(w):
+    """rows [gate 0..n/2)[up 0..n/2) -> the GLU tile order (8 gate rows, 8 up rows per 16-row tile)"""
+    n = w.shape[0]
+    g, u = w[:n // 2].reshape(-1, 8, w.shape[1]), w[n // 2:].reshape(-1, 8, w.shape[1])
+    return np.stack([g, u], 1).reshape(n, -1)
+
+
+def emul(x, w, s, wdiv=1):
+    k = x.shape[1]
+    return oracle.gemv_h16(oracle.xh_values(oracle.xh_pack(x), k), w, s, wdiv)
+
+
+def exact(x, w, s):
+    return oracle.bf16_to_f32(x).astype(np.float64) @ (w * np.repeat(s.astype(np.float64), 128, axis=1)).T
+
+
+def f16(t):
+    return synth.bits(t).view(np.float16).astype(np.float64)
+
+
+def check_h16(y, ref):
+    y = np.asarray(y, np.float64)
+    assert relrms(y, ref) < 1e-5, relrms(y, ref)
+    assert np.abs(y - ref).max() <= 1e-3 * np.sqrt(np.mean(ref ** 2))
+
+
+def test_xh_pack_bit_exact(dev):
+    m, k, ldxh = 5, 320, 384
+    x = x_outliers(m, k, 1)
+    x[0, :6] = synth.np_bf16(np.array([3000.0, -3000.0, 2047.0, -2048.0, 1e-6, -0.0], np.float32))
+    xh = ops.xh_pack(synth.to_dev(x), ldxh)
+    torch.cuda.synchronize()
+    got, want = synth.bits(xh), oracle.xh_pack(x, ldxh)
+    bad = np.argwhere(got != want)
+    assert not len(bad), [(int(r), int(c), hex(got[r, c]), hex(want[r, c])) for r, c in bad[:8]]
+
+
+@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048)])
+def test_gemv_w4h_exact_on_integer_inputs(dev, n, k):
+    rng = np.random.default_rng(n)
+    q, _ = synth.w4_host(n, k, seed=n + 1, sdt=0)
+    s = synth.np_bf16(np.repeat(2.0 ** rng.integers(-10, -4, (n, 1)), k // 128, axis=1).astype(np.float32))
+    w = ops.repack_w4(synth.to_dev(q), synth.to_dev(s, torch.bfloat16))
+    x = synth.np_bf16((rng.integers(-3, 4, (20, k)) * 16).astype(np.float32))
+    want = exact(x, oracle.unpack_w4(q, n, k), oracle.bf16_to_f32(s)).astype(np.float32)
+    for m in (1, 5, 16, 20):
+        y, _, _ = ops.gemv_w4h(w, synth.to_dev(x[:m]))
+        torch.cuda.synchronize()
+        assert np.array_equal(y.cpu().numpy(), want[:m]), m
+
+
+@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048), (2048, 5120)])
+def test_gemv_w4h_parity(dev, n, k):
+    w, wi, s = w4_bf16(n, k, seed=n + k)
+    x = x_outliers(33, k, seed=k)
+    ref, ex = emul(x, wi, s), exact(x, wi, s)
+    rb = relrms(oracle.bf16_to_f32(oracle.f32_to_bf16(ex.astype(np.float32))), ex)
+    for m in (1, 3, 16, 33):
+        y, xh, _ = ops.gemv_w4h(w, synth.to_dev(x[:m]))
+        torch.cuda.synchronize()
+        assert np.array_equal(synth.bits(xh), oracle.xh_pack(x[:m]))
+        yv = y.cpu().numpy()
+        check_h16(yv, ref[:m])
+        assert relrms(yv, ex[:m]) < 2 * rb + 1e-4
+
+
+def test_gemv_w4h_glu_and_yh(dev):
+    n, k = 2048, 2048
+    w, wi, s = w4_bf16(n, k, seed=7, glu=True)
+    x = x_outliers(12, k, seed=8)
+    act = glu_act(emul(x, wi, s))
+    y, _, yh = ops.gemv_w4h(w, synth.to_dev(x), yh=True)
+    torch.cuda.synchronize()
+    yv = oracle.bf16_to_f32(synth.bits(y))
+    assert_glu_close(yv, act, 1e-4)
+    assert relrms(yv, glu_act(exact(x, wi, s))) < 1e-2
+    # yh: the fp32 activation before its bf16 rounding, as x / 16 in fp16 at the XH positions
+    yhv = f16(yh)[:, oracle.xh_pos(np.arange(n // 2))] * 16
+    assert np.all(np.abs(yhv - yv) <= 2.0 ** -8 * np.abs(yv) + 2.0 ** -20)
+
+
+def test_gemv_w4h_yh_plain_bit_exact(dev):
+    n, k = 1024, 1024
+    w, _, _ = w4_bf16(n, k, seed=9)
+    x = x_outliers(7, k, seed=9)
+    y, _, yh = ops.gemv_w4h(w, synth.to_dev(x), yh=True)
+    torch.cuda.synchronize()
+    want = np.zeros((7, n), np.uint16)
+    want[:, oracle.xh_pos(np.arange(n))] = oracle.to_xh(y.cpu().numpy())
+    assert np.array_equal(synth.bits(yh), want)
+
+
+@pytest.mark.parametrize("glu", [False, True])
+def test_gemv_w4h_batch_equals_alone(dev, glu):
+    n, k = 4096, 2048
+    w, _, _ = w4_bf16(n, k, seed=21, glu=glu)
+    x = synth.to_dev(x_outliers(64, k, seed=22))
+    full, _, fyh = ops.gemv_w4h(w, x, yh=True)
+    bad = []
+    for m in MS:
+        y, _, yh = ops.gemv_w4h(w, x[:m].contiguous(), yh=True)
+        torch.cuda.synchronize()
+        same = torch.equal(y.view(torch.int16) if glu else y.view(torch.int32),
+                           (full.view(torch.int16) if glu else full.view(torch.int32))[:m])
+        if not (same and torch.equal(yh.view(torch.int16), fyh.view(torch.int16)[:m])):
+            bad.append(m)
+    assert not bad, bad
+
+
+def test_gemv_w4h_ex_strides_scale_f16_out_bf16(dev):
+    """the build-defined entry point: fp16 scales, bf16 output, padded XH rows (ldx > k) on a side stream"""
+    n, k, m = 512, 1024, 6
+    q, s = synth.w4_host(n, k, seed=3, sdt=1)
+    w = ops.repack_w4(synth.to_dev(q), synth.to_dev(s, torch.float16))
+    x = x_outliers(m, k, seed=4)
+    xh = ops.xh_pack(synth.to_dev(x), ldxh=k + 128)
+    st = torch.cuda.Stream()
+    with torch.cuda.stream(st):
+        y32 = ops.gemv_w4hx(w, xh)
+        y16 = ops.gemv_w4hx(w, xh, out_bf16=True)
+    st.synchronize()
+    ref = emul(x, oracle.unpack_w4(q, n, k), oracle.f16_to_f32(s))
+    check_h16(y32.cpu().numpy(), ref)
+    assert np.array_equal(synth.bits(y16), oracle.f32_to_bf16(y32.cpu().numpy()))
+
+
+# ---------------------------------------------------------------- Q8 through qe_gemv_q8(h16 = 1)
+@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048), (2048, 5120)])
+def test_gemv_q8_h16_parity(dev, n, k):
+    wq, w, s = q8_bf16(n, k, seed=n)
+    x = x_outliers(40, k, seed=n + 1)
+    ref, ex = emul(x, w, s, wdiv=16), exact(x, w, s)
+    rb = relrms(oracle.bf16_to_f32(oracle.f32_to_bf16(ex.astype(np.float32))), ex)
+    for m in (1, 8, 17, 40):
+        y, xh, _ = ops.gemv_q8(wq, synth.to_dev(x[:m]), h16=True)
+        torch.cuda.synchronize()
+        assert np.array_equal(synth.bits(xh), oracle.xh_pack(x[:m]))
+        yv = y.cpu().numpy()
+        check_h16(yv, ref[:m])
+        assert relrms(yv, ex[:m]) < 2 * rb + 1e-4
+
+
+def test_gemv_q8_h16_exact_on_integer_inputs(dev):
+    n, k = 256, 1024
+    rng = np.random.default_rng(4)
+    wq, w, _ = q8_bf16(n, k, seed=5, wmul=16)
+    s = synth.np_bf16(np.repeat(2.0 ** rng.integers(-10, -4, (n, 1)), k // 128, axis=1).astype(np.float32))
+    u = (w + 128).astype(np.uint32).reshape(n, k // 4, 4)
+    q = (u[..., 0] | (u[..., 1] << 8) | (u[..., 2] << 16) | (u[..., 3] << 24)).view(np.int32)
+    wq = ops.repack_q8(synth.to_dev(q), synth.to_dev(s, torch.bfloat16))
+    x = synth.np_bf16((rng.integers(-3, 4, (9, k)) * 16).astype(np.float32))
+    y, _, _ = ops.gemv_q8(wq, synth.to_dev(x), h16=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(y.cpu().numpy(), exact(x, w, oracle.bf16_to_f32(s)).astype(np.float32))
+
+
+def test_gemv_q8_h16_batch_equals_alone_as_reference(dev):
+    """tests/test_q8.py:80-100 with its call shape: qe_gemv_q8(..., h16 = 1, xh, yh), plain and GLU + yh"""
+    n, k = 2048, 2048
+    wq, w, s = q8_bf16(n, k, seed=31)
+    gq, gw, gs = q8_bf16(n, k, seed=31, glu=True)
+    x = synth.to_dev(x_outliers(64, k, seed=3))
+    full = ops.gemv_q8(wq, x, h16=True)[0]
+    gfull, _, gyh = ops.gemv_q8(gq, x, h16=True, yh=True)
+    bad = []
+    for m in MS:
+        y = ops.gemv_q8(wq, x[:m].contiguous(), h16=True)[0]
+        g, _, yh = ops.gemv_q8(gq, x[:m].contiguous(), h16=True, yh=True)
+        torch.cuda.synchronize()
+        if not (torch.equal(y.view(torch.int32), full.view(torch.int32)[:m]) and
+                torch.equal(g.view(torch.int16), gfull.view(torch.int16)[:m]) and
+                torch.equal(yh.view(torch.int16), gyh.view(torch.int16)[:m])):
+            bad.append(m)
+    assert not bad, bad
+    xv = x.cpu().view(torch.int16).numpy().view(np.uint16)
+    ex = exact(xv, w, s)
+    rb = relrms(oracle.bf16_to_f32(oracle.f32_to_bf16(ex.astype(np.float32))), ex)
+    assert relrms(full.cpu().numpy(), ex) < 2 * rb + 1e-4
+    assert relrms(oracle.bf16_to_f32(synth.bits(gfull)), glu_act(exact(xv, gw, gs))) < 1e-2
+

@@ -333,3 +333,65 @@ def test_repack_q8_places_signed_weights():
     deq = oracle.dequant_q8(q, s, n, k)
     ref = synth.np_bf16(w.astype(np.float32) * np.repeat(oracle.bf16_to_f32(s), 128, axis=1))
     assert np.array_equal(deq, ref)
+
+
+# ------------------------------------------------------------------ H16 (XH activations, fp16 chunk partials)
+def test_xh_pos_matches_lane_kstep_statement():
+    """gemv_h16.cuh:8-10: lane t of a token's quad reads halves [16 t, 16 t + 16) of a chunk, i.e. for k-step j the
+    values at k = 16 j + {2t, 2t+1, 2t+8, 2t+9}; every 64-k chunk is a permutation of itself"""
+    for base in (0, 64, 640):
+        for t in range(4):
+            for j in range(4):
+                ks = base + 16 * j + np.array([2 * t, 2 * t + 1, 2 * t + 8, 2 * t + 9])
+                assert list(oracle.xh_pos(ks)) == [base + 16 * t + 4 * j + e for e in range(4)]
+    p = oracle.xh_pos(np.arange(64 * 7))
+    assert np.array_equal(np.sort(p), np.arange(64 * 7))
+    assert np.array_equal(p // 64, np.arange(64 * 7) // 64)
+
+
+def test_xh_pack_matches_torch_clamp_and_half():
+    rng = np.random.default_rng(5)
+    m, k = 3, 256
+    x = synth.np_bf16((rng.standard_normal((m, k)) * 10.0 ** rng.integers(-6, 4, (m, k))).astype(np.float32))
+    x[0, :4] = synth.np_bf16(np.array([3000.0, -3000.0, 2047.0, -2048.0], np.float32))
+    xh = oracle.xh_pack(x, ldxh=320)
+    xt = torch.from_numpy(oracle.bf16_to_f32(x))
+    want = (xt.clamp(-2047, 2047) / 16).half().view(torch.int16).numpy().view(np.uint16)
+    p = oracle.xh_pos(np.arange(k))
+    assert np.array_equal(xh[:, p], want)
+    assert not xh[:, k:].any()
+    assert np.array_equal(oracle.xh_values(xh, k), want.view(np.float16).astype(np.float64))
+
+
+@pytest.mark.parametrize("wdiv", [1, 16])
+def test_gemv_h16_exact_on_integer_inputs(wdiv):
+    """x / 16 and w / wdiv small integers, power-of-two scales: every chunk partial is an integer below 2048 (exact in
+    fp16), so the H16 arithmetic must equal the float64 product x . (w * s)^T exactly"""
+    rng = np.random.default_rng(wdiv)
+    m, n, k = 5, 24, 640
+    xv = rng.integers(-3, 4, (m, k)).astype(np.float64)
+    w = rng.integers(-7, 8, (n, k)) * wdiv
+    s = 2.0 ** rng.integers(-12, -4, (n, k // 128))
+    got = oracle.gemv_h16(xv, w, s, wdiv)
+    want = (xv * 16) @ (w * np.repeat(s, 128, axis=1)).T
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("wdiv", [1, 16])
+def test_gemv_h16_within_one_fp16_rounding_per_chunk(wdiv):
+    """random XH values: |h16 - exact| <= sum over 64-k chunks of half an fp16 ulp of the chunk's magnitude bound,
+    at that chunk's scale; and the rounding really happens (not equal to the exact product)"""
+    rng = np.random.default_rng(10 + wdiv)
+    m, n, k = 4, 32, 1024
+    x = synth.np_bf16(rng.standard_normal((m, k)).astype(np.float32) * 3)
+    xv = oracle.xh_values(oracle.xh_pack(x), k)
+    w = rng.integers(-8, 8, (n, k)) if wdiv == 1 else rng.integers(-127, 128, (n, k))
+    s = np.abs(rng.standard_normal((n, k // 128))) * 0.01
+    got = oracle.gemv_h16(xv, w, s, wdiv)
+    exact = (xv * 16) @ (w * np.repeat(s, 128, axis=1)).T
+    mag = np.einsum("mci,nci->mcn", np.abs(xv).reshape(m, k // 64, 64), np.abs(w / wdiv).reshape(n, k // 64, 64))
+    half_ulp = 2.0 ** (np.floor(np.log2(np.maximum(mag, 2.0 ** -14))) - 11)  # [m][chunks][n]
+    bound = (half_ulp * (np.repeat(s, 2, axis=1).T * 16 * wdiv)[None]).sum(axis=1)
+    assert np.all(np.abs(got - exact) <= bound)
+    assert not np.array_equal(got, exact)
+    assert np.abs(got - exact).max() > 1e-3 * bound.max()
