@@ -7,6 +7,9 @@
   waits and barriers in asm are allowed.
 * Every asm LDS DMA (global_load_lds_*) is preceded in its statement by the scalar write of m0 and one s_nop: on
   GFX9 an LDS DMA needs one wait state after a scalar write of m0, which the compiler cannot insert into asm.
+* No __builtin_bit_cast whose operand is a subscripted element (`__builtin_bit_cast(int, v[r])`): this hipcc lowers
+  the bit_cast of an ext_vector_type element as a load of the vector's first element, whatever the index (seen on
+  gfx950 with ROCm 7.2: every lane of an unrolled loop got element 0). Copy the element into a scalar first.
 """
 import os
 import re
@@ -40,3 +43,14 @@ def test_lds_dma_asm_waits_after_m0():
         for i, op in enumerate(ins):
             if op.startswith("global_load_lds"):
                 assert i >= 2 and ins[i - 1] == "s_nop" and ins[i - 2] == "s_mov_b32", (f, b)
+
+
+def test_no_bit_cast_of_subscripted_element():
+    bad = []
+    for f in sorted(os.listdir(CSRC)):
+        if not f.endswith((".hip", ".hpp", ".cpp")):
+            continue
+        txt = re.sub(r"//[^\n]*", "", open(os.path.join(CSRC, f)).read())
+        for m in re.finditer(r"__builtin_bit_cast\(\s*[^,()]+,\s*[A-Za-z_][A-Za-z0-9_.]*(\[[^\]]+\])+\s*\)", txt):
+            bad.append((f, m.group(0)))
+    assert not bad, bad
