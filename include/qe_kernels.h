@@ -236,6 +236,28 @@ void qe_moe_w4_noalloc(const float* logits, const uint16_t* x, const void* recor
 void qe_moe_pack_w4(const int32_t* gu_q, const uint16_t* gu_s, const int32_t* dn_q, const uint16_t* dn_s, int E, int H,
                     int I, void* records, void* stream);
 
+/* ---- on-disk weights: .safetensors files (host, memory-mapped) and the quantized-matrix loader ----
+ * qe_st_open maps a file and indexes its tensors by name (reference SafeTensors::open, src/safetensors.h:40; a
+ * malformed file aborts with a message); qe_st_close unmaps it. qe_st_count / qe_st_name list the names (sorted);
+ * qe_st_tensor is the reference's has / get (src/safetensors.h:41-42): 0 if absent, else the dtype string
+ * ("I32", "BF16", ... up to 11 chars + NUL into dtype[12]), shape (up to 8 dims), the mapped bytes. Host only. */
+void* qe_st_open(const char* path);
+void qe_st_close(void* st);
+int qe_st_count(void* st);
+const char* qe_st_name(void* st, int i);
+int qe_st_tensor(void* st, const char* name, char* dtype, int64_t* shape, int* ndim, const void** data,
+                 size_t* nbytes);
+/* A quantized matrix from compressed-tensors tensors <names[i]>.weight_packed (int32) / .weight_scale (bf16 or
+ * fp16, per 128-k group): rows [r0[i], r1[i]) of each name in order, columns [c0, c1) (c0 < 0: all), bits per
+ * weight from the packed width (4: W4 layout, dq n*k/2 bytes; 8: Q8 layout, n*k bytes; ds n*k/128 16-bit), GLU
+ * (gate rows then up rows) interleaved per 16-row tile before the repack. Replaces reference Worker::load_w4
+ * (src/model.cpp:994-1059). qe_load_w4_dims: the matrix's n, k, bits, scale dtype (0 bf16, 1 fp16) without loading
+ * (host only); qe_load_w4 copies, interleaves and repacks on `stream` and returns when done. */
+void qe_load_w4_dims(void* st, const char* const* names, const int* r0, const int* r1, int nspec, int c0, int c1,
+                     int* n, int* k, int* bits, int* sdt);
+void qe_load_w4(void* st, const char* const* names, const int* r0, const int* r1, int nspec, int c0, int c1, int glu,
+                void* dq, void* ds, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -345,3 +345,67 @@ def moe_segment(sel, w, E, chunk):
     njobs = torch.empty(1, dtype=torch.int32, device=dev)
     call("qe_moe_segment", sel, w, T, E, topk, chunk, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs, _stream())
     return dict(off=off, slot_pair=slot_pair, slot_tok=slot_tok, slot_w=slot_w, inv=inv, jobs=jobs, njobs=njobs)
+
+
+# ---------------------------------------------------------------- on-disk weights (safetensors)
+class SafeTensorsFile:
+    """a memory-mapped .safetensors file (qe_st_open; the reference's SafeTensors, src/safetensors.h)"""
+
+    def __init__(self, path):
+        from .qe import lib
+        L = lib()
+        L.qe_st_open.restype = ctypes.c_void_p
+        L.qe_st_name.restype = ctypes.c_char_p
+        L.qe_st_count.restype = ctypes.c_int
+        L.qe_st_tensor.restype = ctypes.c_int
+        self._lib = L
+        self.h = ctypes.c_void_p(L.qe_st_open(str(path).encode()))
+
+    def close(self):
+        if self.h:
+            self._lib.qe_st_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def names(self):
+        return [self._lib.qe_st_name(self.h, i).decode() for i in range(self._lib.qe_st_count(self.h))]
+
+    def info(self, name):
+        """-> (dtype, shape, nbytes, address) or None"""
+        dt = ctypes.create_string_buffer(12)
+        shape = (ctypes.c_int64 * 8)()
+        nd = ctypes.c_int()
+        data = ctypes.c_void_p()
+        nb = ctypes.c_size_t()
+        if not self._lib.qe_st_tensor(self.h, name.encode(), dt, shape, ctypes.byref(nd), ctypes.byref(data),
+                                      ctypes.byref(nb)):
+            return None
+        return dt.value.decode(), tuple(shape[i] for i in range(nd.value)), nb.value, data.value
+
+    def _specs(self, rows):
+        names = (ctypes.c_char_p * len(rows))(*[r[0].encode() for r in rows])
+        r0 = (ctypes.c_int * len(rows))(*[int(r[1]) for r in rows])
+        r1 = (ctypes.c_int * len(rows))(*[int(r[2]) for r in rows])
+        return names, r0, r1
+
+    def w4_dims(self, rows, c0=-1, c1=-1):
+        """rows: [(name, r0, r1), ...] -> (n, k, bits, sdt) of the matrix load_w4 builds"""
+        names, r0, r1 = self._specs(rows)
+        out = [ctypes.c_int() for _ in range(4)]
+        self._lib.qe_load_w4_dims(self.h, names, r0, r1, len(rows), c0, c1, *[ctypes.byref(o) for o in out])
+        return tuple(o.value for o in out)
+
+    def load_w4(self, rows, c0=-1, c1=-1, glu=False, device="cuda"):
+        """the reference's Worker::load_w4: -> W4 (4-bit) or Q8 (8-bit) on the device"""
+        n, k, bits, sdt = self.w4_dims(rows, c0, c1)
+        names, r0, r1 = self._specs(rows)
+        dq = torch.empty(n * k * bits // 8, dtype=torch.uint8, device=device)
+        ds = torch.empty(n * (k // 128), dtype=torch.float16 if sdt == SCALE_F16 else torch.bfloat16, device=device)
+        self._lib.qe_load_w4(self.h, names, r0, r1, len(rows), c0, c1, int(glu), ctypes.c_void_p(dq.data_ptr()),
+                             ctypes.c_void_p(ds.data_ptr()), _stream())
+        return Q8(dq, ds, n, k, glu) if bits == 8 else W4(dq, ds, n, k, glu)
