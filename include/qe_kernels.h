@@ -84,8 +84,8 @@ void qe_gemv_workspace_init(void);
  * (dq: n*k/2 bytes, ds: n*k/128 16-bit). Replaces reference src/capi.cpp:13 (repack_w4, gemv.cu:1686-1694). */
 void qe_repack_w4(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds);
 
-/* y[m][n] (fp32, stride n) = x[m][k] (bf16, stride k) . W^T; m = 1..32 (GEMV for m <= 16 per launch, larger m
- * in row blocks). Replaces reference src/capi.cpp:47 (gemv_w4, gemv.cu:1585). */
+/* y[m][n] (fp32, stride n) = x[m][k] (bf16, stride k) . W^T; any m (the decode GEMV in 16-row launches up to 64
+ * rows, the prefill GEMM above, as qe_matmul_w4_ex). Replaces reference src/capi.cpp:47 (gemv_w4, gemv.cu:1585). */
 void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m);
 
 /* as qe_gemv_w4; glu != 0: y is the bf16 activation [m][n/2] = bf16(silu(gate) * up).
@@ -179,7 +179,9 @@ void qe_gemv_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x
 void qe_gemm_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                    int flags, void* stream);
 
-/* GEMV for m <= 32 (row blocks of 16), GEMM above: the reference's matmul() dispatch (gemv.cuh:187-190). */
+/* GEMV for m <= 64 (row blocks of 16), GEMM above: the reference's matmul() dispatch (gemv.cuh:187-190) with the
+ * decode range widened from 32 to 64 rows (measured faster on MI355X; every row of a 1..64-row call has the bits it
+ * has alone). */
 void qe_matmul_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
                      int flags, void* stream);
 

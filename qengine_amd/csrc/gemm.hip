@@ -772,7 +772,7 @@ void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, b
 }
 
 void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
-    if (m > kMaxGemvW4Tokens) {
+    if (m > kMatmulGemvRows) {
         gemm_w4(w, x, ldx, y, ldy, m, out_bf16, st);
         return;
     }

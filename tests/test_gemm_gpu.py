@@ -70,23 +70,24 @@ def test_gemm_w4_strided_output(dev, glu):
 
 
 def test_gemm_matches_gemv_rows(dev):
-    """matmul dispatch: m <= 32 runs the GEMV, from 33 rows the GEMM; both meet the gate on the same rows. The GEMV
-    multiplies the exact weights (u - 8) * s, the GEMM their bf16 rounding (the reference's operand), so a row's
-    result at m = 32 and m = 33 differs by at most the weight rounding: |dy| <= 2^-9 * sum_k |x_k (u_k - 8) s_k|
-    (plus fp32 summation noise), checked element by element"""
+    """matmul dispatch: m <= 64 runs the decode GEMV (16-row launches), from 65 rows the GEMM; both meet the gate on
+    the same rows. The GEMV multiplies the exact weights (u - 8) * s, the GEMM their bf16 rounding (the reference's
+    operand), so a row's result at m = 64 and m = 65 differs by at most the weight rounding:
+    |dy| <= 2^-9 * sum_k |x_k (u_k - 8) s_k| (plus fp32 summation noise), checked element by element"""
     n, k = 1024, 2048
     w, q, s = setup(n, k, 1, seed=9)
-    xh = synth.x_host(64, k, seed=10)
+    xh = synth.x_host(96, k, seed=10)
     x = synth.to_dev(xh)
     ref = oracle_ref(xh, q, s, n, k, 1)
-    yg = out_f32(ops.matmul_w4(w, x))                       # GEMM (64 rows)
-    y33 = out_f32(ops.matmul_w4(w, x[:33].contiguous()))    # GEMM (33 rows)
-    y32 = out_f32(ops.matmul_w4(w, x[:32].contiguous()))    # GEMV (32 rows in two launches)
-    assert err_ratio(yg, ref) <= 1e-4 and err_ratio(y32, ref[:32]) <= TOL
+    yg = out_f32(ops.matmul_w4(w, x))                       # GEMM (96 rows)
+    y65 = out_f32(ops.matmul_w4(w, x[:65].contiguous()))    # GEMM (65 rows)
+    y64 = out_f32(ops.matmul_w4(w, x[:64].contiguous()))    # GEMV (64 rows in four launches)
+    assert err_ratio(yg, ref) <= 1e-4 and err_ratio(y64, ref[:64]) <= TOL
+    assert err_ratio(y64, matmul_f64(xh[:64], exact_w4(q, s, n, k, 1))) <= 1e-4
     wabs = np.abs(exact_w4(q, s, n, k, 1)).astype(np.float64)
-    bound = 2.0 ** -9 * (np.abs(oracle.bf16_to_f32(xh[:32]).astype(np.float64)) @ wabs.T)
+    bound = 2.0 ** -9 * (np.abs(oracle.bf16_to_f32(xh[:64]).astype(np.float64)) @ wabs.T)
     rms = np.sqrt(np.mean(ref ** 2))
-    assert np.all(np.abs(y33[:32].astype(np.float64) - y32) <= bound + 1e-5 * rms)
+    assert np.all(np.abs(y65[:64].astype(np.float64) - y64) <= bound + 1e-5 * rms)
 
 
 def test_reference_named_gemm_hooks(dev):

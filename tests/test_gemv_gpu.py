@@ -326,8 +326,9 @@ def test_gemv_unaligned_activations(dev, mode, n, k):
         assert err_ratio(y.cpu().numpy(), ref8[:m]) <= 1e-4, (mode, m)
 
 
-# the reference's row counts for its skinny == GEMV test (reference tests/test_skinny.py:13)
-MS_REF = [1, 2, 5, 8, 9, 12, 15, 16, 17, 20, 24, 25, 31, 32]
+# the reference's row counts for its skinny == GEMV test (reference tests/test_skinny.py:13), with the 33..64 rows of
+# its decode batch test (tests/test_q8.py:28)
+MS_REF = [1, 2, 5, 8, 9, 12, 15, 16, 17, 20, 24, 25, 31, 32, 33, 40, 48, 63, 64]
 
 
 @pytest.fixture
@@ -340,14 +341,14 @@ def batch_invariant(dev):
 @pytest.mark.parametrize("glu", [False, True])
 @pytest.mark.parametrize("n,k", [(5120, 5120), (2048, 1280)])
 def test_batch_invariant_rows(dev, batch_invariant, n, k, glu):
-    """with batch_invariant set, every row of a decode call of m = 1..32 rows (qe_matmul_w4_ex: 16-row launches of the
+    """with batch_invariant set, every row of a decode call of m = 1..64 rows (qe_matmul_w4_ex: 16-row launches of the
     skinny kernel) has the same bits as that row decoded alone, plain and GLU (the reference's contract,
-    skinny.cu:1-14)"""
+    skinny.cu:1-14; its test takes m up to 64, tests/test_q8.py:28)"""
     w, q, s = setup_w4(n, k, 1, seed=11 + n, glu=glu)
-    xh = synth.x_host(32, k, seed=12)
+    xh = synth.x_host(64, k, seed=12)
     x = synth.to_dev(xh)
     alone = []
-    for r in range(32):
+    for r in range(64):
         alone.append(synth.bits(ops.matmul_w4(w, x[r:r + 1], out_bf16=True)) if glu else
                      ops.matmul_w4(w, x[r:r + 1]).cpu().numpy().view(np.uint32))
     alone = np.concatenate(alone)
