@@ -34,7 +34,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="only the headline GEMV")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["prefill", "w8", "moe", "skinny"], default=None,
+    ap.add_argument("--only", choices=["prefill", "w8", "moe", "skinny", "decode"], default=None,
                     help="run one secondary workload alone (profiling); prints its result")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="time a plain device copy of MB megabytes x 20 (scale for FETCH_SIZE / WRITE_SIZE) and exit")
@@ -106,7 +106,9 @@ def copies_for(bytes_per_copy, minimum):
     return max(minimum, -(-int(1.15 * MALL_BYTES) // int(bytes_per_copy)))
 
 
-def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None, invariant=False):
+def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None, invariant=False, mode="w4"):
+    """decode GEMV / skinny at m rows. mode "w4": qe_gemv_w4_ex (m <= 16); "matmul": qe_matmul_w4_ex (m <= 64: 16-row
+    launches); "h16": the H16 numerics on activations already in the XH layout (qe_gemv_w4h_ex)"""
     import torch
     from qengine_amd import ops, synth
     steps = steps or args.steps
@@ -121,7 +123,13 @@ def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None, invariant=Fa
         del q, s
     x = synth.x_dev(m, k, seed=1)
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-    fn = lambda i: ops.gemv_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    if mode == "h16":
+        xh = ops.xh_pack(x)
+        fn = lambda i: ops.gemv_w4hx(ws[i], xh, out_bf16=True, y=y)  # noqa: E731
+    elif mode == "matmul":
+        fn = lambda i: ops.matmul_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    else:
+        fn = lambda i: ops.gemv_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
     wall_ms, ev_ms = time_launches(fn, steps, warmup, len(ws), graph=True)
     b = gemv_bytes(m, n, k)
     res = dict(m=m, n=n, k=k, bytes=b, ms_per_step=wall_ms / steps, kernel_ms_mean=ev_ms, copies=ncopy,
@@ -341,7 +349,11 @@ def main():
                "skinny": lambda: {f"m{m}_n{n}": (lambda r: {"us": round(r["kernel_ms_mean"] * 1e3, 2),
                                                              "gbs": round(r["gbs_kernel"], 1)})(
                    bench_gemv(args, m=m, n=n, steps=200, warmup=20))
-                   for n in (5120, 17408) for m in (1, 2, 4, 8, 16)}}
+                   for n in (5120, 17408) for m in (1, 2, 4, 8, 16)},
+               "decode": lambda: {f"{mode}_m{m}": (lambda r: {"us": round(r["kernel_ms_mean"] * 1e3, 2),
+                                                              "gbs": round(r["gbs_kernel"], 1)})(
+                   bench_gemv(args, m=m, steps=200, warmup=20, mode=mode))
+                   for (m, mode) in [(1, "h16"), (16, "h16"), (32, "matmul"), (48, "matmul"), (64, "matmul")]}}
         print(json.dumps({args.only: fns[args.only]()}))
         return
 
@@ -359,6 +371,11 @@ def main():
                                               "pct_hbm": round(100 * r["gbs_kernel"] / HBM_PEAK_GBS, 1),
                                               "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2),
                                               "working_set": r["working_set"]}
+        for (m, mode) in [(32, "matmul"), (64, "matmul"), (1, "h16"), (16, "h16")]:
+            r = bench_gemv(args, m=m, steps=200, warmup=20, mode=mode)
+            key = f"decode_m{m}_n17408" if mode == "matmul" else f"h16_m{m}_n17408"
+            secondary[key] = {"gbs_kernel": round(r["gbs_kernel"], 1), "pct_hbm": round(100 * r["gbs_kernel"] / HBM_PEAK_GBS, 1),
+                              "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2), "working_set": r["working_set"]}
         secondary["prefill_k5120_n17408"] = bench_gemm(8192, 17408, 5120)
         secondary["prefill_k17408_n5120"] = bench_gemm(8192, 5120, 17408)
         secondary["w8_gemv_m1_k2048_n8192"] = bench_w8(1)

@@ -776,10 +776,21 @@ void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m,
         gemm_w4(w, x, ldx, y, ldy, m, out_bf16, st);
         return;
     }
+    // row blocks: 32 rows per launch (the skinny kernel's wide variant) while more than 16 remain and the rows are
+    // 16-byte aligned, else 16; a row's bits do not depend on the block it falls in
     const size_t esz = (w.glu || out_bf16) ? 2 : 4;
-    for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
-        const int mm = m - r0 < kMaxGemvRows ? m - r0 : kMaxGemvRows;
-        gemv_w4(w, x + (size_t)r0 * ldx, ldx, reinterpret_cast<char*>(y) + (size_t)r0 * ldy * esz, ldy, mm, out_bf16,
-                st);
+    const bool aligned = ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
+    for (int r0 = 0; r0 < m;) {
+        const int left = m - r0;
+        char* yr = reinterpret_cast<char*>(y) + (size_t)r0 * ldy * esz;
+        if (aligned && left > kMaxGemvRows) {
+            const int mm = left < kWideRows ? left : kWideRows;
+            skinny_w4_wide(w, x + (size_t)r0 * ldx, ldx, yr, ldy, mm, out_bf16, st);
+            r0 += mm;
+        } else {
+            const int mm = left < kMaxGemvRows ? left : kMaxGemvRows;
+            gemv_w4(w, x + (size_t)r0 * ldx, ldx, yr, ldy, mm, out_bf16, st);
+            r0 += mm;
+        }
     }
 }

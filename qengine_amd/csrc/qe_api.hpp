@@ -51,6 +51,8 @@ void gemv_workspace_init();
 void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 // skinny GEMM on the matrix cores (skinny.hip), m = 1..16; out: 0 fp32, 1 bf16, 2 GLU (bf16 act)
 void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st);
+// 17..32 rows in one pass (INT4, x 16-byte aligned, ldx % 8 == 0); the rows' bits equal the 16-row launches'
+void skinny_w4_wide(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 // the same kernel on W8 / Q8 records (GLU for Q8): m = 1..16, x 16-byte aligned, ldx % 8 == 0
 void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st);
 // m = 1 decode GEMV on the matrix cores (gemv1.hip); false when the shape takes the VALU GEMV (uneven K slices,

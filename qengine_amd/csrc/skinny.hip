@@ -48,7 +48,7 @@ constexpr int skinny_d() {
 }
 template <int MT, int NG, int RT, int FMT>
 constexpr int skinny_wpe() {  // minimum waves per SIMD asked of the register allocator
-    return FMT != kFmtW4 ? 1 : RT == 2 ? (NG <= 5 ? 4 : 1) : (MT <= 4 && NG > 0 && NG <= 5 ? 6 : 1);
+    return FMT != kFmtW4 ? 1 : MT > 16 ? 2 : RT == 2 ? (NG <= 5 ? 4 : 1) : (MT <= 4 && NG > 0 && NG <= 5 ? 6 : 1);
 }
 
 // UPX (MT <= 4 with even slices): every group's activations are loaded before the weights and staged in LDS
@@ -67,8 +67,9 @@ template <int MT, int NG, int RT>
 constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][kXStride], scales [RT][NGM][16] half
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
     constexpr int stage = (skinny_upx<MT, NG>() ? NGM : 2) * MT * kXStride + RT * NGM * 8;
-    // after its loop a wave writes its partial sums [RT][16][16] floats over its own (then dead) staging area
-    return stage > RT * 256 ? stage : RT * 256;
+    // after its loop a wave writes its partial sums [RT][max(MT, 16)][16] floats over its own (then dead) staging area
+    constexpr int part = RT * (MT > 16 ? MT : 16) * 16;
+    return stage > part ? stage : part;
 }
 
 // H16: the reference's fp16 decode numerics (XH activations x / 16 in fp16 already in class-major order, weights as
@@ -83,6 +84,9 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     constexpr int NGM = NG > 0 ? NG : kGenericNG;
     constexpr bool UPX = skinny_upx<MT, NG>();
     constexpr int WSZ = skinny_wsz<MT, NG, RT>();
+    // MT > 16 (the wide batch kernel): NB blocks of 16 activation rows, each the B operand of its own MFMAs against
+    // the same A (weight) operand; every row's arithmetic is that of MT = 16 (MFMA columns are independent)
+    constexpr int NB = MT > 16 ? MT / 16 : 1, MTR = MT > 16 ? MT : 16;
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
     const int tile0 = blockIdx.x * RT, G = K >> 7;
@@ -201,9 +205,11 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     // the bias as bf16 pairs: W4 -136 (u = w + 8 over the magic's 128), W8 -128 (u = w + 128)
     constexpr uint32_t kBias = FMT == kFmtW4 ? 0xC308C308u : 0xC300C300u;
     const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{kBias, kBias, kBias, kBias});
-    f32x4_v acc[RT];
+    f32x4_v acc[RT][NB];
 #pragma unroll
-    for (int r = 0; r < RT; r++) acc[r] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++) acc[r][nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
     // groups in rounds of D (register slot d = group % D, a compile-time index). MT = 8 on slices of more than 5
     // groups keeps the rounds rolled: fully unrolled, the compiler hoists operand reads across the whole slice and
     // needs 200+ registers (2 waves per SIMD); the other shapes run faster fully unrolled
@@ -232,15 +238,23 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
         }
         // per k step: one B operand read (the group's activations) serves the weight MFMA and the bias MFMA
         // (A = -136) of each tile: c = sum (128 + u) x - 136 sum x = sum (u - 8) x
-        f32x4_v c[RT];
+        f32x4_v c[RT][NB];
 #pragma unroll
-        for (int r = 0; r < RT; r++) c[r] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) c[r][nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
-            u32x4_v b = {0u, 0u, 0u, 0u};
-            if (MT == 16 || i < MT)
-                b = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + (i < MT ? i : 0)) * kXStride + (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
-            const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
+            u32x4_v b[NB];
+            bf16x8_v bb[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                b[nb] = u32x4_v{0u, 0u, 0u, 0u};
+                if (MT >= 16 || i < MT)
+                    b[nb] = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + 16 * nb + (i < MT ? i : 0)) * kXStride +
+                                                                  (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
+                bb[nb] = __builtin_bit_cast(bf16x8_v, b[nb]);
+            }
             const int j0 = 2 * (mm & 1);
 #pragma unroll
             for (int r = 0; r < RT; r++) {
@@ -292,12 +306,15 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                                                       0x07060302u);
                     }
                 }
-                if constexpr (H16) {
-                    c[r] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a),
-                                                                   __builtin_bit_cast(f16x8_v, b), c[r], 0, 0, 0);
-                } else {
-                    c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c[r], 0, 0, 0);
-                    c[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c[r], 0, 0, 0);
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++) {
+                    if constexpr (H16) {
+                        c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a),
+                                                                          __builtin_bit_cast(f16x8_v, b[nb]), c[r][nb], 0, 0, 0);
+                    } else {
+                        c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb[nb], c[r][nb], 0, 0, 0);
+                        c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb[nb], c[r][nb], 0, 0, 0);
+                    }
                 }
             }
             if constexpr (H16) {
@@ -311,8 +328,11 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                                              scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt) * kF,
                                              scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt) * kF};
 #pragma unroll
-                        for (int j = 0; j < 4; j++) acc[r][j] = fmaf((float)(_Float16)c[r][j], sc[j], acc[r][j]);
-                        c[r] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+                        for (int nb = 0; nb < NB; nb++) {
+#pragma unroll
+                            for (int j = 0; j < 4; j++) acc[r][nb][j] = fmaf((float)(_Float16)c[r][nb][j], sc[j], acc[r][nb][j]);
+                            c[r][nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+                        }
                     }
                 }
             }
@@ -322,10 +342,15 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             if constexpr (H16) break;  // flushed per 64-k chunk above
             // rows 4 qg .. 4 qg + 3 of the group's scales
             const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[(r * NGM + (FMT == kFmtW8C ? 0 : ii)) * 16 + 4 * qg]);
-            acc[r][0] = fmaf(scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt), c[r][0], acc[r][0]);
-            acc[r][1] = fmaf(scale_rt<SDT>((uint16_t)(sv.x >> 16), sdt), c[r][1], acc[r][1]);
-            acc[r][2] = fmaf(scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt), c[r][2], acc[r][2]);
-            acc[r][3] = fmaf(scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt), c[r][3], acc[r][3]);
+            const float s0 = scale_rt<SDT>((uint16_t)(sv.x & 0xffffu), sdt), s1 = scale_rt<SDT>((uint16_t)(sv.x >> 16), sdt);
+            const float s2 = scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt), s3 = scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt);
+#pragma unroll
+            for (int nb = 0; nb < NB; nb++) {
+                acc[r][nb][0] = fmaf(s0, c[r][nb][0], acc[r][nb][0]);
+                acc[r][nb][1] = fmaf(s1, c[r][nb][1], acc[r][nb][1]);
+                acc[r][nb][2] = fmaf(s2, c[r][nb][2], acc[r][nb][2]);
+                acc[r][nb][3] = fmaf(s3, c[r][nb][3], acc[r][nb][3]);
+            }
         }
         if constexpr (!UPX) {
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -341,11 +366,14 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-    for (int r = 0; r < RT; r++) *reinterpret_cast<f32x4_v*>(&red[(size_t)w * WSZ + (r * 16 + i) * 16 + 4 * qg]) = acc[r];
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+        for (int nb = 0; nb < NB; nb++)
+            *reinterpret_cast<f32x4_v*>(&red[(size_t)w * WSZ + (r * MTR + 16 * nb + i) * 16 + 4 * qg]) = acc[r][nb];
     __syncthreads();
     auto rsum = [&](int r, int tok, int rr) {
         float v = 0.f;
-        for (int ws = 0; ws < S; ws++) v += red[(size_t)ws * WSZ + (r * 16 + tok) * 16 + rr];
+        for (int ws = 0; ws < S; ws++) v += red[(size_t)ws * WSZ + (r * MTR + tok) * 16 + rr];
         return v;
     };
     if (out == kOutGLU) {
@@ -376,7 +404,8 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     // on (n, k) only, so every m in 2..16 sums a row in the same order (the rows of a batch equal the rows alone)
     const int dg = decode_groups(n, k);
     const Slicing sc = dg > 0 ? Slicing{dg, (k >> 7) / dg} : gemv_slicing(n, k);
-    const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : 16;
+    const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : m <= 16 ? 16 : 32;
+    CHECK(mt <= 16 || (FMT == qe_gemv::kFmtW4 && !H16), "skinny: %d rows per launch (32-row launches: INT4 only)", m);
     const dim3 block(64 * sc.S);
     // two tiles per wave (where n / 16 is even) at m >= 5, and for m <= 4 on grids of fewer than 16 waves per CU at
     // one tile per wave. Measured (K = 5120): RT = 2 is 3 % slower at m = 2, 4 on N = 17408 (8704 waves), 3 % faster
@@ -409,7 +438,24 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     else if (mt == 2) QE_SK_NG(2);
     else if (mt == 4) QE_SK_NG(4);
     else if (mt == 8) QE_SK_NG(8);
-    else QE_SK_NG(16);
+    else if (mt == 16) QE_SK_NG(16);
+    else if constexpr (FMT == qe_gemv::kFmtW4 && !H16) {
+        // 32 rows: even slices only (the uneven-slice variant's 16 waves x 32 staged rows exceed the LDS); else two
+        // launches of 16 and m - 16 rows (the same sums per row)
+        if (sc.ng == 0) {
+            const size_t esz = out == qe_gemv::kOutF32 ? 4 : 2;
+            launch<FMT, SDT, H16>(q, s, n, k, x, ldx, y, ldy, 16, out, sdt, st, yh, ldyh);
+            launch<FMT, SDT, H16>(q, s, n, k, x + (size_t)16 * ldx, ldx, reinterpret_cast<char*>(y) + (size_t)16 * ldy * esz,
+                                  ldy, m - 16, out, sdt, st, yh ? yh + (size_t)16 * ldyh : nullptr, ldyh);
+            return;
+        }
+        if (sc.ng == 10) QE_SK_K(32, 10);
+        else if (sc.ng == 8) QE_SK_K(32, 8);
+        else if (sc.ng == 5) QE_SK_K(32, 5);
+        else if (sc.ng == 4) QE_SK_K(32, 4);
+        else if (sc.ng == 2) QE_SK_K(32, 2);
+        else CHECK(false, "skinny: slice of %d groups", sc.ng);
+    }
 #undef QE_SK_NG
 #undef QE_SK_K
     HIP_CHECK(hipGetLastError());
@@ -420,6 +466,15 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
 void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
     if (w.sdt == kScaleF16) qe_skinny::launch<qe_gemv::kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else qe_skinny::launch<qe_gemv::kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+}
+
+// 17..32 activation rows in one pass over the weights (two 16-row B blocks per MFMA A operand)
+void skinny_w4_wide(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
+    CHECK(w.n > 0 && w.k > 0 && w.n % 16 == 0 && w.k % 128 == 0 && m > kMaxGemvRows && m <= kWideRows,
+          "skinny_w4_wide %d %d %d", w.n, w.k, m);
+    CHECK(((uintptr_t)x & 15) == 0 && ldx % 8 == 0 && ldx >= w.k, "skinny_w4_wide: x 16-byte aligned, ldx %d", ldx);
+    CHECK(ldy >= (w.glu ? w.n / 2 : w.n), "skinny_w4_wide ldy %d", ldy);
+    skinny_w4_mfma(w, x, ldx, y, ldy, m, w.glu ? qe_gemv::kOutGLU : out_bf16 ? qe_gemv::kOutBF16 : qe_gemv::kOutF32, st);
 }
 
 // bf16 activations -> the XH layout (one thread per value)
