@@ -245,15 +245,14 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             for (int nb = 0; nb < NB; nb++) c[r][nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
-            u32x4_v b[NB];
-            bf16x8_v bb[NB];
+            bf16x8_v bb[NB];  // the B operands (H16: the same bits as f16x8)
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
-                b[nb] = u32x4_v{0u, 0u, 0u, 0u};
+                u32x4_v bv = {0u, 0u, 0u, 0u};
                 if (MT >= 16 || i < MT)
-                    b[nb] = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + 16 * nb + (i < MT ? i : 0)) * kXStride +
-                                                                  (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
-                bb[nb] = __builtin_bit_cast(bf16x8_v, b[nb]);
+                    bv = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + 16 * nb + (i < MT ? i : 0)) * kXStride +
+                                                               (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
+                bb[nb] = __builtin_bit_cast(bf16x8_v, bv);
             }
             const int j0 = 2 * (mm & 1);
 #pragma unroll
@@ -309,8 +308,9 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
 #pragma unroll
                 for (int nb = 0; nb < NB; nb++) {
                     if constexpr (H16) {
+                        const bf16x8_v bn = bb[nb];
                         c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a),
-                                                                          __builtin_bit_cast(f16x8_v, b[nb]), c[r][nb], 0, 0, 0);
+                                                                          __builtin_bit_cast(f16x8_v, bn), c[r][nb], 0, 0, 0);
                     } else {
                         c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb[nb], c[r][nb], 0, 0, 0);
                         c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb[nb], c[r][nb], 0, 0, 0);
