@@ -169,9 +169,11 @@ void qe_gemm_q8(const void* q, const void* s, int n, int k, const uint16_t* x, f
 void qe_dequant_w4(const void* q, const void* s, int n, int k, int flags, uint16_t* out, void* stream);
 
 /* decode GEMV / skinny GEMM, m = 1..16, x rows of stride ldx, y rows of stride ldy.
- * flags: QE_SCALE_F16 | QE_OUT_BF16 | QE_GLU. Deterministic. m = 1 runs the VALU decode kernel, m = 2..16 the
- * matrix-core skinny kernel, whose rows are bit-identical for every m in 2..16 (a row does not depend on the other
- * rows of the batch); the two kernels agree to ~1e-6 relative (fp32 sums in another order). */
+ * flags: QE_SCALE_F16 | QE_OUT_BF16 | QE_GLU. Deterministic. m = 1 runs the m = 1 matrix-core kernel (gemv1),
+ * m = 2..16 the matrix-core skinny kernel, whose rows are bit-identical for every m in 2..16 (a row does not depend
+ * on the other rows of the batch); the two kernels agree to ~1e-6 relative (fp32 sums in another order), and with
+ * qe_config_t.batch_invariant set m = 1 takes the skinny kernel too. Activation rows that are not 16-byte aligned
+ * (x, or ldx not a multiple of 8) take the VALU decode kernel for every m. */
 void qe_gemv_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
                    int flags, void* stream);
 

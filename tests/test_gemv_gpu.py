@@ -8,7 +8,8 @@ Gates:
     fp32 outputs are within 1e-4 * rms of that exact product (float64).
   * bit-identity: every row count from 2 to 16 (the matrix-core skinny kernel) gives the same bits per row (the
     reference's skinny == GEMV contract, tests/test_skinny.py:1-2), and repeated calls are identical (deterministic
-    split-K). The m = 1 decode GEMV (VALU kernel, other summation order) agrees with them to 1e-5 * rms.
+    split-K). The m = 1 matrix-core GEMV (gemv1.hip, another summation order) agrees with them to 1e-5 * rms; with
+    the batch_invariant config m = 1 takes the skinny kernel and every m in 1..64 has the row's own bits.
 """
 import numpy as np
 import pytest
