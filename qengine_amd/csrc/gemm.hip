@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 #include <vector>
 
 namespace {
@@ -189,7 +190,9 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     };
     // dequantize half h (0: row g, 1: row g + 8) of this thread's job from the raw records into the W tile
     auto store_w4 = [&](char* wtile, const char* raw, const char* sc, int h) {
-        if (!jactive) return;
+        if constexpr (NJOB < NTH) {
+            if (!jactive) return;
+        }
         const uint32_t* rw = reinterpret_cast<const uint32_t*>(raw + (jtr >> 1) * 1024) + (8 * (jtr & 1) + jg) * 4 + jj;
         const float scl = scale_rt<SDT>(reinterpret_cast<const uint16_t*>(sc)[jtr * 16 + jg + 8 * h], sdt);
         const float bias = -8.f * scl;
@@ -312,7 +315,11 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     int lane_off[BK / 16];  // swz(l % 32, 2 ks + l / 32) of this lane
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ks++) lane_off[ks] = swz(lane & 31, 2 * ks + (lane >> 5));
-    auto mfma_step = [&](int kt, auto&& store_part) {
+    // pre() runs after the first fragment reads, between(slot) after each row of WNT MFMAs (slot = ks * WMT + row).
+    // pin: nothing is scheduled across those calls, so the work placed in them keeps its place among the MFMAs
+    // (the INT4 dequantization: left to the scheduler it clusters into one VALU block per k16 step, during which
+    // the wave issues no MFMA).
+    auto mfma_step = [&](int kt, auto&& pre, auto&& between, auto pin) {
         const char* xt = lds + (kt & 1) * C::kStage;
         const char* wt = xt + BM * BK * 2;
         // fragments of lane l: row l % 32, k = 16 ks + 8 (l / 32) .. + 8 -> chunk 2 ks + l / 32; the reads of k16
@@ -330,17 +337,24 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             for (int bb = 0; bb < WNT; bb++)
                 bfr[buf][bb] = *reinterpret_cast<const bf16x8_v*>(wl + (wn * 32 * WNT + bb * 32) * 128);
         };
+        auto fence = [&] {
+            if constexpr (decltype(pin)::value) __builtin_amdgcn_sched_barrier(0);
+        };
         read_frags(0, 0);
+        pre();
+        fence();
 #pragma unroll
         for (int ks = 0; ks < BK / 16; ks++) {
             if (ks + 1 < BK / 16) read_frags(ks + 1, (ks + 1) & 1);
 #pragma unroll
-            for (int a = 0; a < WMT; a++)
+            for (int a = 0; a < WMT; a++) {
 #pragma unroll
                 for (int bb = 0; bb < WNT; bb++)
                     if (MODE == 0 || (alive >> a) & 1)
                         acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][bb], af[ks & 1][a], acc[a][bb], 0, 0, 0);
-            store_part(ks);
+                between(ks * WMT + a);
+                fence();
+            }
         }
     };
 
@@ -349,7 +363,12 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         // inserts no waits inside the step; each step ends with vmcnt(0) (its DMAs landed), lgkmcnt(0) and the
         // barrier that publishes them. Step kt: DMA X of step kt + 1 into the other stage and the raw W of step
         // kt + 2 (plus the scales of its group when it starts one), then the MFMAs of step kt with the dequantization
-        // of step kt + 1 (raw records published by the previous step) into the other stage.
+        // of step kt + 1 (raw records published by the previous step) into the other stage: this thread's 4 raw
+        // words and 2 scales are read at the top, and its 8 (row half, word) units run one after every
+        // NSLOT / 8-th MFMA row, each half's two 16-byte stores after its last unit. The last step, which has no
+        // next step to dequantize, is a separate instance, so the steps before it are one basic block (measured on
+        // C2: 41-42 % -> 44-46 % of the bf16 peak against the dequantization left to the scheduler after a branch;
+        // matrix pipes busy 51 % -> 61 % of the busy cycles).
         constexpr unsigned kRawOff = 2 * C::kStage, kScOff = kRawOff + 2 * C::kRaw;
         char* raw = lds + kRawOff;
         char* scb = lds + kScOff;
@@ -362,21 +381,48 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         store_w4(lds + BM * BK * 2, raw, scb, 0);
         store_w4(lds + BM * BK * 2, raw, scb, 1);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        for (int kt = 0; kt < KTL; kt++) {
-            char* st = lds + ((kt + 1) & 1) * C::kStage;
-            if (kt + 1 < KTL) dma_x(kt0 + kt + 1, ((kt + 1) & 1) * C::kStage);
+        constexpr int NSLOT = (BK / 16) * WMT, STRIDE = NSLOT >= 8 ? NSLOT / 8 : 1;
+        static_assert(NSLOT >= 8, "eight dequantization units per k step");
+        auto kstep = [&](int kt, auto more) {
+            constexpr bool MORE = decltype(more)::value;
+            char* wnext = lds + ((kt + 1) & 1) * C::kStage + BM * BK * 2;
+            if (MORE) dma_x(kt0 + kt + 1, ((kt + 1) & 1) * C::kStage);
             if (kt + 2 < KTL) {
                 dma_w4(kt0 + kt + 2, kRawOff + (kt & 1) * C::kRaw);
                 if (((kt + 2) & 1) == 0) dma_sc((kt0 + kt + 2) >> 1, kScOff + (((kt + 2) >> 1) & 1) * C::kSc);
             }
-            const bool more = kt + 1 < KTL;
             const char* rnext = raw + ((kt + 1) & 1) * C::kRaw;
-            const char* snext = scb + (((kt + 1) >> 1) & 1) * C::kSc;
-            mfma_step(kt, [&](int ks) {
-                if (more && ks >= 2) store_w4(st + BM * BK * 2, rnext, snext, ks - 2);
-            });
+            const uint16_t* snext = reinterpret_cast<const uint16_t*>(scb + (((kt + 1) >> 1) & 1) * C::kSc);
+            const uint32_t* rw = reinterpret_cast<const uint32_t*>(rnext + (jtr >> 1) * 1024) + (8 * (jtr & 1) + jg) * 4 + jj;
+            uint32_t wd[4], lo[2][4], hi[2][4];
+            float scl[2];
+            mfma_step(kt, [&] {
+                if constexpr (MORE) {
+#pragma unroll
+                    for (int t = 0; t < 4; t++) wd[t] = rw[64 * t];
+#pragma unroll
+                    for (int h = 0; h < 2; h++) scl[h] = scale_rt<SDT>(snext[jtr * 16 + jg + 8 * h], sdt);
+                }
+            }, [&](int slot) {
+                if constexpr (MORE) {
+                    if (slot % STRIDE != STRIDE - 1 || slot / STRIDE >= 8) return;
+                    // unit (h, t): word t, nibbles of row g + 8 h -> bf16 pairs at k0 (lo) and k0 + 8 (hi)
+                    const int un = slot / STRIDE, h = un >> 2, t = un & 3;
+                    const float bias = -8.f * scl[h];
+                    const uint32_t u = (h ? wd[t] >> 4 : wd[t]) & nib_mask();  // bytes: k0, k0+8, k0+1, k0+9
+                    lo[h][t] = pack_bf16x2(fmaf(cvt_ubyte<0>(u), scl[h], bias), fmaf(cvt_ubyte<2>(u), scl[h], bias));
+                    hi[h][t] = pack_bf16x2(fmaf(cvt_ubyte<1>(u), scl[h], bias), fmaf(cvt_ubyte<3>(u), scl[h], bias));
+                    if (t == 3 && (NJOB >= NTH || jactive)) {
+                        const int row = jtr * 16 + jg + 8 * h;
+                        *reinterpret_cast<u32x4_v*>(wnext + swz(row, 2 * jj)) = u32x4_v{lo[h][0], lo[h][1], lo[h][2], lo[h][3]};
+                        *reinterpret_cast<u32x4_v*>(wnext + swz(row, 2 * jj + 1)) = u32x4_v{hi[h][0], hi[h][1], hi[h][2], hi[h][3]};
+                    }
+                }
+            }, std::true_type{});
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        }
+        };
+        for (int kt = 0; kt + 1 < KTL; kt++) kstep(kt, std::true_type{});
+        kstep(KTL - 1, std::false_type{});
     } else {
         // X by LDS DMA (as the INT4 path), INT8 records through two register sets: step kt issues the DMA of X
         // (kt + 1) and the record loads of kt + 2 at its top, dequantizes the records of kt + 1 (loaded one step
@@ -392,10 +438,12 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             char* nxt = lds + ((kt + 1) & 1) * C::kStage;
             if (kt + 1 < KTL) dma_x(kt0 + kt + 1, ((kt + 1) & 1) * C::kStage);
             const bool more = kt + 1 < KTL;
-            mfma_step(kt, [&](int ks) {
+            mfma_step(kt, [] {}, [&](int slot) {
+                if (slot % WMT != WMT - 1) return;  // after the last MFMA row of k16 step ks
+                const int ks = slot / WMT;
                 if (more) store_w8x(cur, nxt + BM * BK * 2, ks);
                 if (ks == 0 && kt + 2 < KTL) load_w8(nxt_regs, kt0 + kt + 2);  // after the first stores free no registers
-            });
+            }, std::false_type{});
             asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
         };
         for (int kt = 0; kt < KTL; kt += 2) {
