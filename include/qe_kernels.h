@@ -40,13 +40,17 @@ int qe_abi_version(void);
  *   gemm_tune       1: every prefill GEMM times its candidates (tile configuration x split of the last partial round)
  *                   once per (shape, token bucket), outside graph capture, and keeps the fastest (as qe_gemm_w4_t
  *                   always does); 0 (default): a stored choice if any, else the cost model
+ *   gemm_h16        1: the W4 prefill GEMM entry points (qe_gemm_w4*, the GEMM leg of qe_matmul_w4_ex) run the
+ *                   reference's fp16-accumulate numerics (qe_gemm_w4h_ex below; the reference's QE_GEMM_H16 with
+ *                   W4A8 off, src/kernels/gemm.cu:3360-3362,4047-4070); 0 (default): the bf16 MFMA GEMM
  * Out-of-range values abort with a "check failed" message. No counterpart function in the reference. */
 typedef struct qe_config {
     int skinny_min_m;
     int w8_mfma_min_m;
     int batch_invariant;
     int gemm_tune;
-    int reserved[4];
+    int gemm_h16;
+    int reserved[3];
 } qe_config_t;
 void qe_get_config(qe_config_t* cfg);
 void qe_set_config(const qe_config_t* cfg);
@@ -62,6 +66,17 @@ int qe_gemm_tune_entries(void);
  * captured into a graph without enough of it runs unsplit). Reserve `bytes` on the current device before capturing
  * (the reference's gemm_reserve_ws). */
 void qe_gemm_reserve(size_t bytes);
+/* Prefill GEMM with the reference's fp16-accumulate numerics (gemm_h_kernel + x_to_h_kernel,
+ * src/kernels/gemm.cu:236-461): activations scaled per token to |x| <= 16 (xs = amax / 16) and rounded to fp16,
+ * weights as the exact integers u - 8 in fp16, each 64-k chunk's partial rounded to fp16 and scaled by its group
+ * scale into fp32, the token scale in the epilogue. flags: QE_SCALE_F16, QE_OUT_BF16, QE_GLU (y = the bf16
+ * activation [t][n / 2]). The pre-pass buffer (t * (2 k + 4) bytes) is the library's, grown on first use per
+ * device; qe_gemm_h_reserve(k, t) sizes it before graph capture (a capture that needs more aborts with a message).
+ * No single counterpart function in the reference (its gemm_w4 picks this path by QE_GEMM_H16); also reached
+ * through qe_gemm_w4* with qe_config_t.gemm_h16 = 1. */
+void qe_gemm_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                    int flags, void* stream);
+void qe_gemm_h_reserve(int k, int t);
 /* test hook: qe_gemm_w4_ex with a given choice instead of the tuner's (cfg 0: 256 x 256 tiles, 1: 256 x 128; ks: K
  * ranges of the last partial round's tiles, 1 / 2 / 4); returns 1 if that split applies to the shape (else it runs
  * unsplit and returns 0). The reference's QE_GEMM_FORCE (src/kernels/gemm.cu:4376-4394). */

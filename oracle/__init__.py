@@ -25,6 +25,10 @@ Parity pins (each function is checked against something other than itself in tes
                     per 64-k chunk, torch's clamp + fp16 conversion for the values
   gemv_h16          exact on integer-valued inputs (equal to the float64 product), and elsewhere within the
                     closed-form bound of one fp16 rounding per 64-k chunk of the float64 product
+  x_to_h            torch's float32 amax / division / product and fp16 conversion (an independent RNE
+                    implementation), known answers (zero row, amax = 16)
+  gemm_h            exact on integer-valued inputs (equal to the float64 product), and elsewhere within the
+                    closed-form bound of one fp16 rounding per 64-k chunk of the float64 product
 """
 import ctypes
 import os
@@ -328,3 +332,30 @@ def gemv_h16(xv, w, s, wdiv=1):
         part = xv[:, 64 * c:64 * c + 64] @ wf[:, 64 * c:64 * c + 64].T
         acc += part.astype(np.float16).astype(np.float64) * sf[:, c // 2][None, :]
     return acc
+
+
+# ---------------------------------------------------------------- fp16-accumulate prefill GEMM (gemm_h)
+def x_to_h(x):
+    """bf16 bits [t][k] -> (xh float64 [t][k], xs float32 [t]) of the reference's x_to_h_kernel (gemm.cu:262-289):
+    xs = amax / 16 in fp32 (1 for a zero row), inv = fp32(1 / xs), xh = fp16_rn(fp32(x * inv))"""
+    xf = bf16_to_f32(np.asarray(x, np.uint16))
+    amax = np.abs(xf).max(axis=1)
+    xs = np.where(amax > 0, amax / np.float32(16), np.float32(1)).astype(np.float32)
+    inv = (np.float32(1) / xs).astype(np.float32)
+    prod = (xf * inv[:, None]).astype(np.float32)
+    return prod.astype(np.float16).astype(np.float64), xs
+
+
+def gemm_h(xh, xs, w, s):
+    """the fp16-accumulate prefill arithmetic (gemm.cu:236-461): xh [t][k] the fp16 activation values, xs [t] the
+    token scales, w [n][k] the exact integer weights u - 8, s [n][k/128] the group scales (float). Every 64-k
+    chunk's partial sum is formed exactly and rounded once to fp16 (the reference rounds inside the chunk too),
+    added at its group scale, and the token scale multiplies the sum. Returns float64 [t][n]."""
+    xh = np.asarray(xh, np.float64)
+    t, k = xh.shape
+    sf = np.asarray(s, np.float64)
+    acc = np.zeros((t, w.shape[0]))
+    for c in range(k // 64):  # the weights are converted chunk by chunk (full-size matrices stay integer)
+        part = xh[:, 64 * c:64 * c + 64] @ np.asarray(w[:, 64 * c:64 * c + 64], np.float64).T
+        acc += part.astype(np.float16).astype(np.float64) * sf[:, c // 2][None, :]
+    return acc * np.asarray(xs, np.float64)[:, None]

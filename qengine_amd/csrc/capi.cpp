@@ -59,6 +59,7 @@ void qe_get_config(qe_config_t* cfg) {
     cfg->w8_mfma_min_m = c.w8_mfma_min_m;
     cfg->batch_invariant = c.batch_invariant;
     cfg->gemm_tune = c.gemm_tune;
+    cfg->gemm_h16 = c.gemm_h16;
 }
 
 void qe_set_config(const qe_config_t* cfg) {
@@ -68,6 +69,8 @@ void qe_set_config(const qe_config_t* cfg) {
     c.w8_mfma_min_m = cfg->w8_mfma_min_m;
     c.batch_invariant = cfg->batch_invariant;
     c.gemm_tune = cfg->gemm_tune;
+    c.gemm_h16 = cfg->gemm_h16;
+    CHECK(cfg->reserved[0] == 0 && cfg->reserved[1] == 0 && cfg->reserved[2] == 0, "qe_set_config: reserved fields must be 0");
     qe_config_set(c);
 }
 
@@ -75,6 +78,7 @@ void qe_gemm_tune_file(const char* path) { gemm_tune_file(path); }
 void qe_gemm_tune_clear(void) { gemm_table_clear(); }
 int qe_gemm_tune_entries(void) { return (int)gemm_table_size(); }
 void qe_gemm_reserve(size_t bytes) { gemm_reserve(bytes); }
+void qe_gemm_h_reserve(int k, int t) { gemm_h_reserve(k, t); }
 
 int qe_gemm_w4_choice(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                       int flags, int cfg, int ks, void* stream) {
@@ -237,6 +241,12 @@ void qe_gemm_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x
                    int flags, void* st) {
     gemm_w4(mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y,
             ldy, t, (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+void qe_gemm_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                    int flags, void* st) {
+    gemm_w4h(mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y,
+             ldy, t, (flags & QE_OUT_BF16) != 0, as_stream(st));
 }
 
 void qe_matmul_w4_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,

@@ -42,18 +42,6 @@ struct Cfg {
     static constexpr int kLdsW4 = 2 * kStage + 2 * kRaw + 2 * kSc;
 };
 
-// global_load_lds_dwordx4: lane i's 16 bytes land at LDS byte m0 + 16 i. Issued from inline asm so that the
-// compiler, which cannot tell these LDS writes from the stage the MFMAs read, does not wait for them before every
-// LDS read; the kernel waits for them itself (vmcnt) before the barrier that publishes the stage. An LDS DMA that
-// reads m0 needs one wait state after the scalar write of m0 (GFX9): the s_nop.
-// lds_dst: LDS byte address, wave-uniform
-__device__ __forceinline__ void dma16(const void* src, unsigned lds_dst) {
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
-}
-__device__ __forceinline__ void dma4(const void* src, unsigned lds_dst) {  // 4 bytes per lane
-    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
-}
-
 // MODE 0 split tiles: the tiles from `ndirect` on run as `ks` K ranges each (stream-K of the last, partly filled
 // round); their fp32 partials go to part [(tile - ndirect) * ks + split][BM][BN] and splitk_reduce_kernel adds them
 struct SplitArgs {
@@ -790,6 +778,10 @@ void moe_pf_gemm(int mode, const MoePfArgs& a, hipStream_t st) {
 void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st,
              bool tuned) {
     gemm_check(w.n, w.k, x, ldx, ldc, t, w.glu);
+    if (qe_config().gemm_h16) {  // the reference's fp16-accumulate numerics (its QE_GEMM_H16 with W4A8 off)
+        gemm_w4h(w, x, ldx, c, ldc, t, out_bf16, st);
+        return;
+    }
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
     if (w.sdt == kScaleF16) launch_gemm<kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, tuned, st);
     else launch_gemm<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, t, c, ldc, out, w.sdt, tuned, st);

@@ -13,9 +13,9 @@ const QeConfig& qe_config() { return g_cfg; }
 void qe_config_set(const QeConfig& c) {
     CHECK(c.skinny_min_m >= 1 && c.skinny_min_m <= kMaxGemvRows + 1 && c.w8_mfma_min_m >= 0 &&
               c.w8_mfma_min_m <= kMaxGemvRows + 1 && (c.batch_invariant == 0 || c.batch_invariant == 1) &&
-              (c.gemm_tune == 0 || c.gemm_tune == 1),
-          "config skinny_min_m %d w8_mfma_min_m %d batch_invariant %d gemm_tune %d", c.skinny_min_m, c.w8_mfma_min_m,
-          c.batch_invariant, c.gemm_tune);
+              (c.gemm_tune == 0 || c.gemm_tune == 1) && (c.gemm_h16 == 0 || c.gemm_h16 == 1),
+          "config skinny_min_m %d w8_mfma_min_m %d batch_invariant %d gemm_tune %d gemm_h16 %d", c.skinny_min_m,
+          c.w8_mfma_min_m, c.batch_invariant, c.gemm_tune, c.gemm_h16);
     g_cfg = c;
 }
 

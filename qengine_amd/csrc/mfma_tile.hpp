@@ -56,6 +56,18 @@ __device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, 
     *reinterpret_cast<uint32_t*>(wt + swz(row + 8, c0 + 1) + o0) = h8;
 }
 
+// global_load_lds_dwordx4: lane i's 16 bytes land at LDS byte m0 + 16 i. Issued from inline asm so that the
+// compiler, which cannot tell these LDS writes from the stage the MFMAs read, does not wait for them before every
+// LDS read; the kernel waits for them itself (vmcnt) before the barrier that publishes the stage. An LDS DMA that
+// reads m0 needs one wait state after the scalar write of m0 (GFX9): the s_nop.
+// lds_dst: LDS byte address, wave-uniform
+__device__ __forceinline__ void dma16(const void* src, unsigned lds_dst) {
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
+}
+__device__ __forceinline__ void dma4(const void* src, unsigned lds_dst) {  // 4 bytes per lane
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(lds_dst), "v"(src) : "memory", "m0");
+}
+
 // 32x32 MFMA C fragment: lane l holds column l % 32, rows 8 (r / 4) + 4 (l / 32) + r % 4 for r = 0..15
 __device__ __forceinline__ int c_row(int lane, int r) { return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3); }
 

@@ -82,6 +82,7 @@ struct QeConfig {
     int w8_mfma_min_m = 0;
     int batch_invariant = 0;
     int gemm_tune = 0;
+    int gemm_h16 = 0;
 };
 const QeConfig& qe_config();
 void qe_config_set(const QeConfig& c);
@@ -99,6 +100,9 @@ void gemm_w8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, b
 void gemm_w4_choice(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, int cfg, int ks,
                     hipStream_t st);
 bool gemm_split_applies(int cfg, int n, int k, int t, int ks);
+// the reference's fp16-accumulate prefill numerics (gemm_h.hip); gemm_h_reserve sizes its pre-pass buffer
+void gemm_w4h(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
+void gemm_h_reserve(int k, int t);
 void gemm_set_out_bf16(bool on);
 // reserve the split-K workspace of the current device (grown on demand otherwise, never during graph capture)
 void gemm_reserve(size_t bytes);

@@ -19,7 +19,7 @@ W8_PER_CHANNEL = 8
 class QeConfig(ctypes.Structure):
     """include/qe_kernels.h qe_config_t"""
     _fields_ = [("skinny_min_m", ctypes.c_int), ("w8_mfma_min_m", ctypes.c_int), ("batch_invariant", ctypes.c_int),
-                ("gemm_tune", ctypes.c_int), ("reserved", ctypes.c_int * 4)]
+                ("gemm_tune", ctypes.c_int), ("gemm_h16", ctypes.c_int), ("reserved", ctypes.c_int * 3)]
 
 
 def get_config():
@@ -27,7 +27,7 @@ def get_config():
     c = QeConfig()
     lib().qe_get_config(ctypes.byref(c))
     return {"skinny_min_m": c.skinny_min_m, "w8_mfma_min_m": c.w8_mfma_min_m, "batch_invariant": c.batch_invariant,
-            "gemm_tune": c.gemm_tune}
+            "gemm_tune": c.gemm_tune, "gemm_h16": c.gemm_h16}
 
 
 def set_config(**kw):
@@ -165,6 +165,16 @@ def gemm_w4(w: W4, x, out_bf16=False, y=None):
     assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
     y = _out(t, w.n, out_bf16, w.glu, x.device) if y is None else y
     call("qe_gemm_w4_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y
+
+
+def gemm_w4h(w: W4, x, out_bf16=False, y=None):
+    """prefill GEMM with the reference's fp16-accumulate numerics (qe_gemm_w4h_ex)"""
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, w.glu, x.device) if y is None else y
+    call("qe_gemm_w4h_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
          w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
     return y
 

@@ -1,0 +1,135 @@
+"""Prefill GEMM with the reference's fp16-accumulate numerics (qe_gemm_w4h_ex; the reference's gemm_h_kernel +
+x_to_h_kernel, src/kernels/gemm.cu:236-461) through the C-ABI vs the CPU oracle.
+
+* Integer-valued inputs (each token row holds one +-16, so xs = 1 and the fp16 activations are the inputs; small
+  integers elsewhere; power-of-two scales): every chunk partial is an integer below 2048, exact in fp16, so the
+  fp32 outputs equal the float64 product bit for bit. This pins the operand layouts, the flush, the scale and
+  token-scale indexing and the epilogue.
+* Random inputs: within one fp16 rounding per 64-k chunk of the oracle's emulation (oracle.gemm_h, which rounds
+  the exactly formed chunk partial once, as this kernel does after its fp32 MFMA sum), and within 1e-5 relative rms
+  of it; against the exact float64 product, the reference's own gate (tests/test_gemm.py:26-27,
+  max|err| / max|ref| < 1e-2).
+* GLU, bf16 outputs, fp16 / bf16 scales, ragged T and N, strided outputs; qe_config_t.gemm_h16 routes qe_gemm_w4*
+  here (bit-identical)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from qengine_amd import ops, synth
+from test_gemv_gpu import exact_w4, glu_act, out_f32
+
+pytestmark = pytest.mark.gpu
+
+
+def setup(n, k, sdt, seed, glu=False, q=None, s=None):
+    if q is None:
+        q, s = synth.w4_host(n, k, seed=seed, sdt=sdt)
+    if glu:
+        q, s = oracle.glu_rows(q, s, n, k)
+    w = ops.repack_w4(synth.to_dev(q), synth.to_dev(s, torch.float16 if sdt else torch.bfloat16), glu=glu)
+    return w, q, s
+
+
+def h_ref(xb, q, s, n, k, sdt):
+    xh, xs = oracle.x_to_h(xb)
+    wi = oracle.unpack_w4(q, n, k)
+    return oracle.gemm_h(xh, xs, wi, oracle.scale_to_f32(s, sdt).reshape(n, k // 128)), xh, xs, wi
+
+
+def chunk_bound(xh, xs, wi, s_f):
+    """sum over 64-k chunks of one fp16 ulp of the chunk's magnitude bound, at its scale, times the token scale"""
+    t, k = xh.shape
+    n = wi.shape[0]
+    mag = np.einsum("mci,nci->mcn", np.abs(xh).reshape(t, k // 64, 64), np.abs(wi).reshape(n, k // 64, 64))
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(mag, 2.0 ** -14))) - 10)
+    return (ulp * np.repeat(s_f, 2, axis=1).T[None]).sum(axis=1) * xs[:, None].astype(np.float64)
+
+
+@pytest.mark.parametrize("n,k,t,sdt", [(256, 640, 37, 1), (304, 1024, 130, 0), (512, 2048, 256, 1)])
+def test_gemm_h_exact_on_integer_inputs(dev, n, k, t, sdt):
+    rng = np.random.default_rng(n + t)
+    xf = rng.integers(-2, 3, (t, k)).astype(np.float32)
+    xf[np.arange(t), rng.integers(0, k, t)] = np.where(rng.random(t) < 0.5, 16.0, -16.0)
+    xb = synth.np_bf16(xf)
+    q, _ = synth.w4_host(n, k, seed=n)
+    sf = (2.0 ** rng.integers(-8, -5, (n, k // 128))).astype(np.float32)
+    s = sf.astype(np.float16).view(np.uint16) if sdt else synth.np_bf16(sf)
+    w, q, s = setup(n, k, sdt, 0, q=q, s=s)
+    y = ops.gemm_w4h(w, synth.to_dev(xb))
+    torch.cuda.synchronize()
+    want = xf.astype(np.float64) @ (oracle.unpack_w4(q, n, k).astype(np.float64) * np.repeat(sf, 128, axis=1)).T
+    assert np.array_equal(y.cpu().numpy().astype(np.float64), want)
+
+
+@pytest.mark.parametrize("n,k,t,sdt", [(128, 128, 1, 1), (256, 512, 37, 0), (512, 1024, 300, 1), (384, 2048, 129, 0),
+                                       (1040, 5120, 200, 1)])
+def test_gemm_h_parity(dev, n, k, t, sdt):
+    w, q, s = setup(n, k, sdt, seed=n + k + t)
+    xb = synth.x_host(t, k, seed=t)
+    ref, xh, xs, wi = h_ref(xb, q, s, n, k, sdt)
+    y = ops.gemm_w4h(w, synth.to_dev(xb))
+    torch.cuda.synchronize()
+    y = y.cpu().numpy().astype(np.float64)
+    s_f = oracle.scale_to_f32(s, sdt).reshape(n, k // 128).astype(np.float64)
+    assert np.all(np.abs(y - ref) <= chunk_bound(xh, xs, wi, s_f) + 1e-6 * np.abs(ref))
+    assert np.sqrt(np.mean((y - ref) ** 2) / np.mean(ref ** 2)) < 1e-5
+    exact = oracle.bf16_to_f32(xb).astype(np.float64) @ exact_w4(q, s, n, k, sdt).astype(np.float64).T
+    assert np.abs(y - exact).max() / np.abs(exact).max() < 1e-2  # the reference's gate
+    yb = out_f32(ops.gemm_w4h(w, synth.to_dev(xb), out_bf16=True))
+    assert np.all(np.abs(yb - y) <= 2.0 ** -8 * np.abs(y))  # bf16 output = RNE of the fp32 output
+
+
+def test_gemm_h_glu(dev):
+    n, k, t = 512, 1024, 77
+    w, q, s = setup(n, k, 1, seed=5, glu=True)
+    xb = synth.x_host(t, k, seed=6)
+    ref, _, _, _ = h_ref(xb, q, s, n, k, 1)
+    act = glu_act(ref)
+    y = out_f32(ops.gemm_w4h(w, synth.to_dev(xb)))
+    bound = 1e-4 * np.sqrt(np.mean(act ** 2)) + 2.0 ** -8 * np.abs(act)
+    assert np.all(np.abs(y - act) <= bound), float((np.abs(y - act) / bound).max())
+
+
+@pytest.mark.parametrize("glu", [False, True])
+def test_gemm_h_strided_output_and_config_route(dev, glu):
+    """outputs written at an odd offset inside a wider matrix equal the contiguous outputs; with
+    qe_config_t.gemm_h16 = 1 the qe_gemm_w4_ex entry point runs this kernel (bit-identical)"""
+    n, k, t = 512, 1024, 70
+    w, _, _ = setup(n, k, 0, seed=12, glu=glu)
+    x = synth.to_dev(synth.x_host(t, k, seed=13))
+    cols = n // 2 if glu else n
+    for out_bf16 in ((True,) if glu else (False, True)):
+        dt = torch.bfloat16 if (out_bf16 or glu) else torch.float32
+        iv = torch.int16 if dt == torch.bfloat16 else torch.int32
+        want = ops.gemm_w4h(w, x, out_bf16=out_bf16)
+        big = torch.full((t, cols + 7), float("nan"), dtype=dt, device=dev)
+        got = ops.gemm_w4h(w, x, out_bf16=out_bf16, y=big[:, 1:1 + cols])
+        torch.cuda.synchronize()
+        assert torch.equal(got.contiguous().view(iv), want.view(iv)), (glu, out_bf16)
+        assert torch.isnan(big[:, 0]).all() and torch.isnan(big[:, 1 + cols:]).all()
+        old = ops.set_config(gemm_h16=1)
+        try:
+            routed = ops.gemm_w4(w, x, out_bf16=out_bf16)
+            torch.cuda.synchronize()
+        finally:
+            ops.set_config(**old)
+        assert torch.equal(routed.view(iv), want.view(iv))
+        assert not torch.equal(ops.gemm_w4(w, x, out_bf16=out_bf16).view(iv), want.view(iv))  # the bf16 GEMM differs
+
+
+def test_gemm_h_baseline_shape_sampled(dev):
+    """C2's shape (M = 8192, K = 5120, N = 17408, fp16 scales, bf16 output): 24 sampled rows vs the oracle"""
+    n, k, t = 17408, 5120, 8192
+    qd, sd = synth.w4_dev(n, k, seed=21)
+    w = ops.repack_w4(qd, sd)
+    x = synth.x_dev(t, k, seed=22)
+    y = ops.gemm_w4h(w, x, out_bf16=True)
+    torch.cuda.synchronize()
+    rows = np.random.default_rng(3).choice(t, 24, replace=False)
+    q = qd.cpu().numpy()
+    s = synth.bits(sd)
+    ref, _, _, _ = h_ref(synth.bits(x[rows]), q, s, n, k, 1)
+    yb = out_f32(y[rows])
+    bound = 1e-4 * np.sqrt(np.mean(ref ** 2)) + 2.0 ** -8 * np.abs(ref)
+    assert np.all(np.abs(yb - ref) <= bound), float((np.abs(yb - ref) / bound).max())

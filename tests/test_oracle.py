@@ -395,3 +395,57 @@ def test_gemv_h16_within_one_fp16_rounding_per_chunk(wdiv):
     assert np.all(np.abs(got - exact) <= bound)
     assert not np.array_equal(got, exact)
     assert np.abs(got - exact).max() > 1e-3 * bound.max()
+
+
+def test_x_to_h_matches_torch():
+    """x_to_h against torch's float32 arithmetic and fp16 conversion; a zero row takes xs = 1, xh = 0; a row whose
+    amax is 16 keeps its values (xs = 1)"""
+    rng = np.random.default_rng(7)
+    t, k = 6, 384
+    xf = rng.standard_normal((t, k)).astype(np.float32) * np.exp(rng.standard_normal((t, 1))).astype(np.float32) * 5
+    xf[2] = 0
+    xf[3] = np.clip(np.round(xf[3]), -15, 15)
+    xf[3, 7] = -16
+    x = synth.np_bf16(xf)
+    xh, xs = oracle.x_to_h(x)
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).float()
+    amax = xt.abs().amax(1)
+    sc = torch.where(amax > 0, amax / 16, torch.ones_like(amax))
+    inv = 1.0 / sc
+    want = (xt * inv[:, None]).half().double().numpy()
+    assert np.array_equal(xs, sc.numpy()) and np.array_equal(xh, want)
+    assert xs[2] == 1 and not xh[2].any()
+    assert xs[3] == 1 and np.array_equal(xh[3], oracle.bf16_to_f32(x[3]).astype(np.float64))
+    assert np.abs(xh).max() <= 16
+
+
+def test_gemm_h_exact_on_integer_inputs():
+    """xh small integers, power-of-two scales and token scales: every chunk partial is an integer below 2048 (exact
+    in fp16), so gemm_h equals the float64 product exactly"""
+    rng = np.random.default_rng(3)
+    t, n, k = 5, 24, 640
+    xh = rng.integers(-3, 4, (t, k)).astype(np.float64)
+    xs = (2.0 ** rng.integers(-4, 3, t)).astype(np.float32)
+    w = rng.integers(-8, 8, (n, k))
+    s = 2.0 ** rng.integers(-12, -4, (n, k // 128))
+    got = oracle.gemm_h(xh, xs, w, s)
+    want = (xh * xs[:, None].astype(np.float64)) @ (w * np.repeat(s, 128, axis=1)).T
+    assert np.array_equal(got, want)
+
+
+def test_gemm_h_within_one_fp16_rounding_per_chunk():
+    """random activations through x_to_h: |gemm_h - exact| <= sum over chunks of half an fp16 ulp of the chunk's
+    magnitude bound at that chunk's scale (times the token scale); and the rounding really happens"""
+    rng = np.random.default_rng(11)
+    t, n, k = 4, 32, 1024
+    x = synth.np_bf16(rng.standard_normal((t, k)).astype(np.float32) * 3)
+    xh, xs = oracle.x_to_h(x)
+    w = rng.integers(-8, 8, (n, k))
+    s = np.abs(rng.standard_normal((n, k // 128))) * 0.01
+    got = oracle.gemm_h(xh, xs, w, s)
+    exact = (xh * xs[:, None].astype(np.float64)) @ (w * np.repeat(s, 128, axis=1)).T
+    mag = np.einsum("mci,nci->mcn", np.abs(xh).reshape(t, k // 64, 64), np.abs(w).reshape(n, k // 64, 64).astype(np.float64))
+    half_ulp = 2.0 ** (np.floor(np.log2(np.maximum(mag, 2.0 ** -14))) - 11)
+    bound = (half_ulp * np.repeat(s, 2, axis=1).T[None]).sum(axis=1) * xs[:, None]
+    assert np.all(np.abs(got - exact) <= bound)
+    assert not np.array_equal(got, exact)
