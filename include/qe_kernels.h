@@ -77,6 +77,22 @@ void qe_gemm_reserve(size_t bytes);
 void qe_gemm_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                     int flags, void* stream);
 void qe_gemm_h_reserve(int k, int t);
+/* W4A8 prefill GEMM, the reference's default prefill numerics (gemm_w4_i8 = x_to_i8_kernel + gemm_i8*_kernel,
+ * src/kernels/gemm.cu:463-594,4513-4518): activations quantized per (token, G-group), G = 32, 64 or 128, to int8
+ * with sx = amax / 127 (two lowest mantissa bits cleared) and q = rn(x / sx); weights as the exact int8 u - 8;
+ * int32 dot products per G-group on the int8 matrix cores, added at sx * sw in fp32. qe_gemm_w4_i8 replaces
+ * reference src/capi.cpp:104 (y fp32 [t][n], or bf16 after qe_gemm_set_out_bf16(1); bf16 scales), qe_gemm_w4_i8_glu
+ * src/capi.cpp:109 (act bf16 [t][n/2] of a GLU matrix); ci / ks (the reference's tile candidate and kernel variant)
+ * are accepted and ignored. qe_gemm_w4_i8_ex: strides, stream, flags QE_SCALE_F16 / QE_OUT_BF16 / QE_GLU. The
+ * pre-pass buffer (t * (k + k / 8) bytes) is the library's, grown on first use per device; qe_gemm_i8_reserve(k, t)
+ * sizes it before graph capture. */
+void qe_gemm_w4_i8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, int G, int ci,
+                   int ks);
+void qe_gemm_w4_i8_glu(const void* q, const void* s, int n, int k, const uint16_t* x, void* act, int t, int G, int ci,
+                       int ks);
+void qe_gemm_w4_i8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                      int G, int flags, void* stream);
+void qe_gemm_i8_reserve(int k, int t);
 /* test hook: qe_gemm_w4_ex with a given choice instead of the tuner's (cfg 0: 256 x 256 tiles, 1: 256 x 128; ks: K
  * ranges of the last partial round's tiles, 1 / 2 / 4); returns 1 if that split applies to the shape (else it runs
  * unsplit and returns 0). The reference's QE_GEMM_FORCE (src/kernels/gemm.cu:4376-4394). */

@@ -29,6 +29,9 @@ Parity pins (each function is checked against something other than itself in tes
                     implementation), known answers (zero row, amax = 16)
   gemm_h            exact on integer-valued inputs (equal to the float64 product), and elsewhere within the
                     closed-form bound of one fp16 rounding per 64-k chunk of the float64 product
+  x_to_i8           the reference test's own torch emulation (tests/test_gemm_i8.py:52-61 quant_emul) restated in
+                    torch, known answers (zero group, amax = 127 * 2^e)
+  gemm_i8           float64 product of the dequantized int8 operands: brute force on tiny shapes
 """
 import ctypes
 import os
@@ -359,3 +362,33 @@ def gemm_h(xh, xs, w, s):
         part = xh[:, 64 * c:64 * c + 64] @ np.asarray(w[:, 64 * c:64 * c + 64], np.float64).T
         acc += part.astype(np.float16).astype(np.float64) * sf[:, c // 2][None, :]
     return acc * np.asarray(xs, np.float64)[:, None]
+
+
+# ---------------------------------------------------------------- W4A8 prefill GEMM (gemm_w4_i8)
+def x_to_i8(x, G):
+    """bf16 bits [t][k] -> (q int8 [t][k] in natural k order, sx float32 [t][k/G]) of the reference's x_to_i8_kernel
+    (gemm.cu:540-594): per (token, G-group) amax; sx = bits(amax / 127) & ~3 in fp32 (1 for a zero group),
+    inv = fp32(1 / sx) (0 for a zero group), q = rn(x * inv) clamped to [-127, 127]"""
+    xf = bf16_to_f32(np.asarray(x, np.uint16))
+    t, k = xf.shape
+    xg = xf.reshape(t, k // G, G)
+    amax = np.abs(xg).max(axis=2)
+    sx = ((amax / np.float32(127)).astype(np.float32).view(np.uint32) & np.uint32(0xFFFFFFFC)).view(np.float32)
+    sx = np.where(amax > 0, sx, np.float32(1)).astype(np.float32)
+    inv = np.where(amax > 0, np.float32(1) / sx, np.float32(0)).astype(np.float32)
+    prod = (xg * inv[:, :, None]).astype(np.float32)
+    q = np.clip(np.rint(prod), -127, 127).astype(np.int8)
+    return q.reshape(t, k), sx
+
+
+def gemm_i8(q, sx, w, s, G):
+    """the W4A8 product of the dequantized operands in float64: sum_k (q sx)[t][k] (w s)[n][k], q / sx from x_to_i8,
+    w [n][k] the exact integer weights u - 8, s [n][k/128] the group scales (float); the reference's test
+    emulation (tests/test_gemm_i8.py:52-61,124-129)"""
+    t, k = q.shape
+    xq = (np.asarray(q, np.float64).reshape(t, k // G, G) * np.asarray(sx, np.float64)[:, :, None]).reshape(t, k)
+    out = np.zeros((t, w.shape[0]))
+    sf = np.asarray(s, np.float64)
+    for g in range(k // 128):  # the weights are converted group by group (full-size matrices stay integer)
+        out += xq[:, 128 * g:128 * g + 128] @ (np.asarray(w[:, 128 * g:128 * g + 128], np.float64) * sf[:, g:g + 1]).T
+    return out

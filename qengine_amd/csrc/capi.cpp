@@ -79,6 +79,27 @@ void qe_gemm_tune_clear(void) { gemm_table_clear(); }
 int qe_gemm_tune_entries(void) { return (int)gemm_table_size(); }
 void qe_gemm_reserve(size_t bytes) { gemm_reserve(bytes); }
 void qe_gemm_h_reserve(int k, int t) { gemm_h_reserve(k, t); }
+void qe_gemm_i8_reserve(int k, int t) { gemm_i8_reserve(k, t); }
+
+// W4A8 (reference src/capi.cpp:104-113): ci (tile candidate) and ks (kernel variant) select among the reference's
+// CUDA kernels; this build has one kernel per activation group and ignores them
+void qe_gemm_w4_i8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, int G, int ci,
+                   int ks) {
+    (void)ci;
+    (void)ks;
+    gemm_w4_i8(mk_w4(q, s, n, k, false, kScaleBF16), x, k, y, n, t, G, gemm_out_bf16(), 0);
+}
+void qe_gemm_w4_i8_glu(const void* q, const void* s, int n, int k, const uint16_t* x, void* act, int t, int G, int ci,
+                       int ks) {
+    (void)ci;
+    (void)ks;
+    gemm_w4_i8(mk_w4(q, s, n, k, true, kScaleBF16), x, k, act, n / 2, t, G, false, 0);
+}
+void qe_gemm_w4_i8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
+                      int G, int flags, void* st) {
+    gemm_w4_i8(mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y,
+               ldy, t, G, (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
 
 int qe_gemm_w4_choice(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                       int flags, int cfg, int ks, void* stream) {

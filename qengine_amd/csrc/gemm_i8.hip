@@ -1,0 +1,399 @@
+// W4A8 prefill GEMM, the reference's default prefill numerics (reference gemm_w4_i8: x_to_i8_kernel +
+// gemm_i8*_kernel, src/kernels/gemm.cu:463-594,4513-4518): C[t][n] = sum_k X[t][k] W[n][k] where
+//   * the activations are quantized per (token, group of G k), G in {32, 64, 128}: sx = amax / 127 with the two
+//     lowest mantissa bits cleared (1 for a zero group), q = rn(x * fp32(1 / sx)) as int8 (x_to_i8_kernel,
+//     gemm.cu:540-594);
+//   * the weights enter as the exact signed int8 u - 8;
+//   * each G-group's integer dot product (exact, int32) is converted to fp32, multiplied by sx and added at sw
+//     (the 128-k weight group scale) into fp32 accumulators.
+// The reference flushes per G-group into a per-128-k partial and scales that by sw; both are within fp32 rounding
+// of the float64 product of the dequantized int8 operands (the reference's gate, tests/test_gemm_i8.py:125-135:
+// relative rms below 1e-5 against that emulation).
+//
+// v_mfma_i32_32x32x32_i8 (gfx950) with W as A and X as B, so a lane of the 32 x 32 result holds one token (column
+// l % 32): one activation scale per lane and tile per G-group, the weight scales of its 16 rows from LDS (4 rows per
+// 8-byte read). Block: 512 threads = 8 waves in 2 (tokens) x 4 (weight rows), tile BM = 128 tokens x BN = 256 rows,
+// one 128-k weight group per step (128 B per LDS row, the bf16 kernels' swizzled tile). Pipeline as in the bf16
+// prefill GEMM: X (int8, from the pre-pass) by LDS DMA one step ahead, the two raw W4 chunks of a step by DMA two
+// steps ahead, the next step's int8 W tile unpacked between the MFMA rows (order pinned), the weight and activation
+// scales by DMA into small double buffers. Within each 16-k block the weight bytes come out of a W4 word in the
+// order k0, k0 + 8, k0 + 1, k0 + 9 (k0 = 2 t, words t = 0..3); the pre-pass stores the activations in that same
+// order, so the dot products pair matching k (the same permutation as the reference's pre-pass, forced by the
+// W4 layout).
+#include "mfma_tile.hpp"
+
+#include <mutex>
+#include <type_traits>
+#include <vector>
+
+namespace {
+
+using namespace qe_tile;
+
+typedef int i32x4_v __attribute__((ext_vector_type(4)));
+typedef int i32x16_v __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 128, BN = 256, BK = 128, NTH = 512, WMT = 2, WNT = 2;
+constexpr int kStage = (BM + BN) * BK;       // X [BM][128] and W [BN][128] int8
+constexpr int kRaw = BN * 64;                // two 64-k W4 chunks of BN / 16 tiles x 512 B
+constexpr int kSc = BN * 2;                  // [BN / 16][16] weight scales of one group
+constexpr int kSx = BM * 4 * 4;              // [BM][128 / G] activation scales, G >= 32
+constexpr int kLds = 2 * kStage + 2 * kRaw + 2 * kSc + 2 * kSx;
+enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
+
+// byte p of a 16-k block holds k offset kPerm(p) = 2 (p / 4) + {0, 8, 1, 9}[p % 4]
+__device__ __forceinline__ int k_perm(int p) { return 2 * (p >> 2) + ((p & 1) ? 8 : 0) + ((p >> 1) & 1); }
+
+// one block per token; thread j quantizes the 16-k block j (reference x_to_i8_kernel, gemm.cu:540-594): the amax of
+// its G-group over the G / 16 lanes that share it, sx = bits(amax / 127) & ~3 (1 for a zero group), inv =
+// fp32(1 / sx) (0 for a zero group), q = rn(x * inv); bytes stored in the W4 word order of the block
+template <int G>
+__global__ void __launch_bounds__(256) x_to_i8_kernel(const uint16_t* __restrict__ x, int ldx, int K,
+                                                      int8_t* __restrict__ xq, float* __restrict__ sx) {
+    constexpr int L = G / 16;
+    const int t = blockIdx.x;
+    const uint16_t* r = x + (size_t)t * ldx;
+    for (int j0 = 0; j0 < K / 16; j0 += blockDim.x) {
+        const int j = j0 + threadIdx.x;
+        const bool live = j < K / 16;
+        float v[16];
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            v[i] = live ? bf16_to_f32(r[16 * j + i]) : 0.f;
+            mx = fmaxf(mx, fabsf(v[i]));
+        }
+#pragma unroll
+        for (int o = 1; o < L; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // the G / 16 lanes of a group
+        const float sc = mx > 0.f ? __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mx / 127.f) & ~3u) : 1.f;
+        const float inv = mx > 0.f ? 1.f / sc : 0.f;
+        if (!live) continue;
+        uint32_t o[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            uint32_t wv = 0;
+#pragma unroll
+            for (int b = 0; b < 4; b++) {
+                const float qf = fminf(fmaxf(__builtin_rintf(v[k_perm(4 * u + b)] * inv), -127.f), 127.f);
+                wv |= ((uint32_t)(int)qf & 0xFFu) << (8 * b);
+            }
+            o[u] = wv;
+        }
+        *reinterpret_cast<u32x4_v*>(xq + (size_t)t * K + 16 * j) = u32x4_v{o[0], o[1], o[2], o[3]};
+        if (j % L == 0) sx[(size_t)t * (K / G) + (16 * j) / G] = sc;
+    }
+}
+
+// 4 nibbles u (one per byte) -> 4 signed bytes u - 8
+__device__ __forceinline__ uint32_t nib_s8(uint32_t u) { return ((u | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
+
+template <int G, int SDT, int OUT>
+__global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
+                                                      int N, int K, const int8_t* __restrict__ xq,
+                                                      const float* __restrict__ sxg, int T, void* __restrict__ c,
+                                                      int ldc, int nbn, int ntiles) {
+    constexpr int NGS = BK / G;   // activation groups per step
+    constexpr int KPG = G / 32;   // k32 MFMA steps per activation group
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const unsigned lds32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds);
+    const int per = (ntiles + 7) >> 3, b = blockIdx.x;
+    const int tile = (b & 7) * per + (b >> 3);
+    if (tile >= ntiles) return;
+    const int n0 = (tile % nbn) * BN, t0 = (tile / nbn) * BM;
+    const int G128 = K >> 7, KT = K / BK;
+    const int ntile_last = (N >> 4) - 1;
+
+    auto dma_x = [&](int kt, unsigned xt) {  // 8 rows of 128 B per wave instruction
+#pragma unroll
+        for (int i = 0; i < BM / 64; i++) {
+            const int r0 = (wave * (BM / 64) + i) * 8, row = r0 + (lane >> 3);
+            const int ch = (lane & 7) ^ swz_f(row);
+            const int tok = t0 + row < T ? t0 + row : T - 1;
+            dma16(xq + (size_t)tok * K + kt * BK + ch * 16, lds32 + xt + r0 * 128);
+        }
+    };
+    // the step's two raw 64-k W4 chunks: lane i of wave w < 8 loads record (tile 2 w + (i / 8) % 2, g = i % 8,
+    // t = i / 16) of chunk 2 kt (waves 0..7) and 2 kt + 1 (waves 8..15 = the same waves again)
+    auto dma_w4 = [&](int kt, unsigned raw) {
+        if (wave < BN / 32) {
+            const int tl = min((n0 >> 4) + 2 * wave + ((lane >> 3) & 1), ntile_last);
+            const uint4* src = q + ((size_t)tl * (K >> 6) + 2 * kt) * 32 + 4 * (lane & 7) + (lane >> 4);
+            dma16(src, lds32 + raw + wave * 1024);
+            dma16(src + 32, lds32 + raw + BN * 32 + wave * 1024);
+        }
+    };
+    auto dma_sc = [&](int grp, unsigned sc) {
+        if (wave < BN / 128) {
+            const int tl = min((n0 >> 4) + 8 * wave + (lane >> 3), ntile_last);
+            dma4(s + ((size_t)tl * G128 + grp) * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
+        }
+    };
+    // activation scales of the step: [BM tokens][NGS] floats, 4 bytes per lane
+    auto dma_sx = [&](int kt, unsigned sxo) {
+        constexpr int NW = BM * NGS / 64;  // wave instructions
+        if (wave < NW) {
+            const int i = wave * 64 + lane, row = i / NGS, gi = i % NGS;
+            const int tok = t0 + row < T ? t0 + row : T - 1;
+            dma4(sxg + (size_t)tok * (K / G) + kt * NGS + gi, lds32 + sxo + wave * 256);
+        }
+    };
+    const int jj = tid & 3, jg = (tid >> 2) & 7, jtr = tid >> 5;
+    static_assert(BN * 2 == NTH, "one unpack job per thread");
+
+    constexpr unsigned kRawOff = 2 * kStage, kScOff = kRawOff + 2 * kRaw, kSxOff = kScOff + 2 * kSc;
+    const int wm = wave >> 2, wn = wave & 3;
+    f32x16_v acc[WMT][WNT];
+    i32x16_v dsum[WMT][WNT];
+#pragma unroll
+    for (int a = 0; a < WMT; a++)
+#pragma unroll
+        for (int bb = 0; bb < WNT; bb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[a][bb][r] = 0.f;
+    int lane_off[BK / 32];  // k32 step ks: 16 bytes at chunk 2 ks + l / 32 of row l % 32
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ks++) lane_off[ks] = swz(lane & 31, 2 * ks + (lane >> 5));
+
+    // unpack unit (ch, h, t): word t of raw chunk ch, row half h -> 4 signed bytes; after t = 3 the 16-byte chunk
+    // (row jtr * 16 + jg + 8 h, 16-k block 4 ch + jj) is stored
+    uint32_t wd[2][4], ob[4];
+    auto unit = [&](char* wtile, int ch, int h, int t) {
+        const uint32_t u = (h ? wd[ch][t] >> 4 : wd[ch][t]) & nib_mask();
+        ob[t] = nib_s8(u);
+        if (t == 3) {
+            const int row = jtr * 16 + jg + 8 * h;
+            *reinterpret_cast<u32x4_v*>(wtile + swz(row, 4 * ch + jj)) = u32x4_v{ob[0], ob[1], ob[2], ob[3]};
+        }
+    };
+    auto read_words = [&](const char* rawb) {
+#pragma unroll
+        for (int ch = 0; ch < 2; ch++) {
+            const uint32_t* rw = reinterpret_cast<const uint32_t*>(rawb + ch * BN * 32 + (jtr >> 1) * 1024) +
+                                 (8 * (jtr & 1) + jg) * 4 + jj;
+#pragma unroll
+            for (int t = 0; t < 4; t++) wd[ch][t] = rw[64 * t];
+        }
+    };
+
+    dma_x(0, 0);
+    dma_w4(0, kRawOff);
+    if (KT > 1) dma_w4(1, kRawOff + kRaw);
+    dma_sc(0, kScOff);
+    dma_sx(0, kSxOff);
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+    read_words(lds + kRawOff);
+#pragma unroll
+    for (int ch = 0; ch < 2; ch++)
+#pragma unroll
+        for (int h = 0; h < 2; h++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) unit(lds + BM * BK, ch, h, t);
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+    // step kt: DMA X (kt + 1), the raw W, weight scales and activation scales of kt + 1 / kt + 2; MFMAs of step kt
+    // with the unpack of step kt + 1 (two units after each MFMA row); each activation group's sums flushed after its
+    // last k32 step: acc += float(sum) * sx * sw
+    auto kstep = [&](int kt, auto more) {
+        constexpr bool MORE = decltype(more)::value;
+        char* wnext = lds + ((kt + 1) & 1) * kStage + BM * BK;
+        if (MORE) {
+            dma_x(kt + 1, ((kt + 1) & 1) * kStage);
+            dma_sc(kt + 1, kScOff + ((kt + 1) & 1) * kSc);
+            dma_sx(kt + 1, kSxOff + ((kt + 1) & 1) * kSx);
+        }
+        if (kt + 2 < KT) dma_w4(kt + 2, kRawOff + (kt & 1) * kRaw);
+        const char* xt = lds + (kt & 1) * kStage;
+        const char* wt = xt + BM * BK;
+        i32x4_v af[2][WMT], bfr[2][WNT];  // af: X (B operand), bfr: W (A operand)
+        auto read_frags = [&](int ks, int buf) {
+#pragma unroll
+            for (int a = 0; a < WMT; a++)
+                af[buf][a] = *reinterpret_cast<const i32x4_v*>(xt + lane_off[ks] + (wm * 32 * WMT + a * 32) * 128);
+#pragma unroll
+            for (int bb = 0; bb < WNT; bb++)
+                bfr[buf][bb] = *reinterpret_cast<const i32x4_v*>(wt + lane_off[ks] + (wn * 32 * WNT + bb * 32) * 128);
+        };
+        read_frags(0, 0);
+        if constexpr (MORE) read_words(lds + kRawOff + ((kt + 1) & 1) * kRaw);
+        // weight scales of this lane's rows (4 consecutive rows per register quad, one 8-byte read) for the step
+        const uint16_t* scb = reinterpret_cast<const uint16_t*>(lds + kScOff + (kt & 1) * kSc);
+        const float* sxb = reinterpret_cast<const float*>(lds + kSxOff + (kt & 1) * kSx);
+        float swf[WNT][16];
+#pragma unroll
+        for (int bb = 0; bb < WNT; bb++)
+#pragma unroll
+            for (int rq = 0; rq < 4; rq++) {
+                const uint2 sp = *reinterpret_cast<const uint2*>(scb + wn * 32 * WNT + bb * 32 + 8 * rq + 4 * (lane >> 5));
+                swf[bb][4 * rq] = scale_to_f32<SDT>((uint16_t)(sp.x & 0xFFFFu));
+                swf[bb][4 * rq + 1] = scale_to_f32<SDT>((uint16_t)(sp.x >> 16));
+                swf[bb][4 * rq + 2] = scale_to_f32<SDT>((uint16_t)(sp.y & 0xFFFFu));
+                swf[bb][4 * rq + 3] = scale_to_f32<SDT>((uint16_t)(sp.y >> 16));
+            }
+        __builtin_amdgcn_sched_barrier(0);
+        int slot = 0;
+#pragma unroll
+        for (int ks = 0; ks < BK / 32; ks++) {
+            if (ks + 1 < BK / 32) read_frags(ks + 1, (ks + 1) & 1);
+#pragma unroll
+            for (int a = 0; a < WMT; a++) {
+#pragma unroll
+                for (int bb = 0; bb < WNT; bb++) {
+                    const i32x16_v cin = ks % KPG == 0 ? i32x16_v{} : dsum[a][bb];
+                    dsum[a][bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfr[ks & 1][bb], af[ks & 1][a], cin, 0, 0, 0);
+                }
+                if constexpr (MORE) {
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        const int un = 2 * slot + e;  // 16 units over 8 rows
+                        unit(wnext, un >> 3, (un >> 2) & 1, un & 3);
+                    }
+                }
+                slot++;
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            if (ks % KPG == KPG - 1) {  // flush activation group ks / KPG: acc += (float(sum) * sx) * sw
+                const int gi = ks / KPG;
+#pragma unroll
+                for (int a = 0; a < WMT; a++) {
+                    const float sxa = sxb[(wm * 32 * WMT + a * 32 + (lane & 31)) * NGS + gi];
+#pragma unroll
+                    for (int bb = 0; bb < WNT; bb++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++)
+                            acc[a][bb][r] = fmaf((float)dsum[a][bb][r] * sxa, swf[bb][r], acc[a][bb][r]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    };
+    static_assert((BK / 32) * WMT * 2 == 16, "16 unpack units per step, two per MFMA row");
+    for (int kt = 0; kt + 1 < KT; kt++) kstep(kt, std::true_type{});
+    kstep(KT - 1, std::false_type{});
+
+    // epilogue: lane = token l % 32, register r = weight row 8 (r / 4) + 4 (l / 32) + r % 4 of its tile
+    const int cj = lane & 31, ci = 4 * (lane >> 5);
+    const bool vec = ((ldc & 3) == 0 && ((uintptr_t)c & (OUT == kOutF32 ? 15u : 7u)) == 0);
+#pragma unroll
+    for (int a = 0; a < WMT; a++)
+#pragma unroll
+        for (int bb = 0; bb < WNT; bb++) {
+            const int tok = t0 + wm * 32 * WMT + a * 32 + cj;
+            if (tok >= T) continue;
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) {
+                const int n = n0 + wn * 32 * WNT + bb * 32 + 8 * rb + ci;  // first of 4 consecutive rows
+                if (n >= N) continue;
+                const f32x16_v& v = acc[a][bb];
+                if constexpr (OUT == kOutGLU) {
+                    if (rb & 1) continue;  // rows 8 (rb + 1) + ..: the up rows of this gate block
+                    uint16_t* p = reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + (n >> 4) * 8 + (n & 7);
+                    float g[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j++) g[j] = silu_f32(v[4 * rb + j]) * v[4 * rb + 4 + j];
+                    if (vec) {
+                        *reinterpret_cast<uint2*>(p) = uint2{pack_bf16x2(g[0], g[1]), pack_bf16x2(g[2], g[3])};
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) p[j] = f32_to_bf16(g[j]);
+                    }
+                } else if constexpr (OUT == kOutBF16) {
+                    uint16_t* p = reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + n;
+                    if (vec) {
+                        *reinterpret_cast<uint2*>(p) =
+                            uint2{pack_bf16x2(v[4 * rb], v[4 * rb + 1]), pack_bf16x2(v[4 * rb + 2], v[4 * rb + 3])};
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) p[j] = f32_to_bf16(v[4 * rb + j]);
+                    }
+                } else {
+                    float* p = reinterpret_cast<float*>(c) + (size_t)tok * ldc + n;
+                    if (vec) {
+                        *reinterpret_cast<f32x4_v*>(p) = f32x4_v{v[4 * rb], v[4 * rb + 1], v[4 * rb + 2], v[4 * rb + 3]};
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; j++) p[j] = v[4 * rb + j];
+                    }
+                }
+            }
+        }
+}
+
+// ---- library-owned pre-pass buffers (xq [t][k] int8, sx [t][k / G] fp32), one per device, grown outside graph
+//      capture, outgrown buffers kept (a graph captured earlier may still read them)
+constexpr int kMaxDev = 64;
+std::mutex g_mu;
+struct I8Ws {
+    void* p = nullptr;
+    size_t bytes = 0;
+    std::vector<void*> retired;
+} g_ws[kMaxDev];
+
+void* i8_ws(size_t bytes, hipStream_t st) {
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    CHECK(dev >= 0 && dev < kMaxDev, "device %d", dev);
+    std::lock_guard<std::mutex> lk(g_mu);
+    I8Ws& w = g_ws[dev];
+    if (w.bytes >= bytes) return w.p;
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    HIP_CHECK(hipStreamIsCapturing(st, &cs));
+    CHECK(cs == hipStreamCaptureStatusNone,
+          "gemm_w4_i8: the pre-pass buffer (%zu bytes) must be sized by an eager call or qe_gemm_i8_reserve before capture",
+          bytes);
+    void* np = nullptr;
+    HIP_CHECK(hipMalloc(&np, bytes));
+    if (w.p) w.retired.push_back(w.p);
+    w.p = np;
+    w.bytes = bytes;
+    return np;
+}
+
+size_t xq_bytes(int k, int t) { return ((size_t)t * k + 255) / 256 * 256; }
+size_t i8_ws_bytes(int k, int t) { return xq_bytes(k, t) + (size_t)t * (k / 32) * 4; }  // sx sized for G = 32
+
+template <int G>
+void run_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int out, hipStream_t st) {
+    char* ws = static_cast<char*>(i8_ws(i8_ws_bytes(w.k, t), st));
+    int8_t* xq = reinterpret_cast<int8_t*>(ws);
+    float* sx = reinterpret_cast<float*>(ws + xq_bytes(w.k, t));
+    x_to_i8_kernel<G><<<dim3((unsigned)t), dim3(256), 0, st>>>(x, ldx, w.k, xq, sx);
+    HIP_CHECK(hipGetLastError());
+    const int nbn = (w.n + BN - 1) / BN, nbt = (t + BM - 1) / BM, ntiles = nbn * nbt;
+    const unsigned blocks = (unsigned)(8 * ((ntiles + 7) / 8));
+#define QE_GI(SDT_, OUT_)                                                                                            \
+    gemm_i8_kernel<G, SDT_, OUT_><<<dim3(blocks), dim3(NTH), kLds, st>>>(w.q, w.s, w.n, w.k, xq, sx, t, c, ldc, nbn, \
+                                                                          ntiles)
+    if (w.sdt == kScaleF16) {
+        if (out == kOutGLU) QE_GI(kScaleF16, kOutGLU);
+        else if (out == kOutBF16) QE_GI(kScaleF16, kOutBF16);
+        else QE_GI(kScaleF16, kOutF32);
+    } else {
+        if (out == kOutGLU) QE_GI(kScaleBF16, kOutGLU);
+        else if (out == kOutBF16) QE_GI(kScaleBF16, kOutBF16);
+        else QE_GI(kScaleBF16, kOutF32);
+    }
+#undef QE_GI
+    HIP_CHECK(hipGetLastError());
+}
+
+}  // namespace
+
+void gemm_i8_reserve(int k, int t) {
+    if (k > 0 && t > 0) i8_ws(i8_ws_bytes(k, t), 0);
+}
+
+void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int G, bool out_bf16,
+                hipStream_t st) {
+    CHECK(w.n > 0 && w.n % 16 == 0 && w.k >= 128 && w.k % 128 == 0, "gemm_w4_i8: n = %d, k = %d", w.n, w.k);
+    CHECK(G == 32 || G == 64 || G == 128, "gemm_w4_i8: activation group G = %d (32, 64 or 128)", G);
+    CHECK(t > 0, "gemm_w4_i8: t = %d", t);
+    CHECK(ldx >= w.k && ((uintptr_t)x & 1) == 0, "gemm_w4_i8: ldx = %d < k", ldx);
+    CHECK(ldc >= (w.glu ? w.n / 2 : w.n), "gemm_w4_i8: ldc = %d", ldc);
+    const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    if (G == 32) run_i8<32>(w, x, ldx, c, ldc, t, out, st);
+    else if (G == 64) run_i8<64>(w, x, ldx, c, ldc, t, out, st);
+    else run_i8<128>(w, x, ldx, c, ldc, t, out, st);
+}

@@ -179,6 +179,16 @@ def gemm_w4h(w: W4, x, out_bf16=False, y=None):
     return y
 
 
+def gemm_w4_i8(w: W4, x, G=64, out_bf16=False, y=None):
+    """W4A8 prefill GEMM, activation group G (qe_gemm_w4_i8_ex)"""
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, w.glu, x.device) if y is None else y
+    call("qe_gemm_w4_i8_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t, G,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y
+
+
 def gemm_w4_choice(w: W4, x, cfg, ks, out_bf16=False, y=None):
     """prefill GEMM with a given (tile configuration, split) instead of the tuner's; returns (y, split applied)"""
     t = x.shape[0]

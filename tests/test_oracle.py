@@ -449,3 +449,43 @@ def test_gemm_h_within_one_fp16_rounding_per_chunk():
     bound = (half_ulp * np.repeat(s, 2, axis=1).T[None]).sum(axis=1) * xs[:, None]
     assert np.all(np.abs(got - exact) <= bound)
     assert not np.array_equal(got, exact)
+
+
+@pytest.mark.parametrize("G", [32, 64, 128])
+def test_x_to_i8_matches_reference_emulation(G):
+    """x_to_i8 against the reference test's torch emulation (tests/test_gemm_i8.py:52-61, restated: amax, / 127.0,
+    the low two mantissa bits cleared, 1 / sc, round, clamp); a zero group gives sx = 1, q = 0; a group whose
+    amax is 127 * 2^e has sx = 2^e and q = x / 2^e exactly"""
+    rng = np.random.default_rng(G)
+    t, k = 5, 512
+    xf = rng.standard_normal((t, k)).astype(np.float32) * np.exp(rng.standard_normal((t, 1))).astype(np.float32) * 4
+    xf[1, :G] = 0
+    xf[2, :G] = np.clip(np.round(xf[2, :G] * 10), -100, 100) * np.float32(0.25)
+    xf[2, 3] = 127 * 0.25
+    x = synth.np_bf16(xf)
+    q, sx = oracle.x_to_i8(x, G)
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16).float().reshape(t, k // G, G)
+    amax = xt.abs().amax(-1, keepdim=True)
+    sc = (amax / 127.0).view(torch.int32) & ~3
+    sc = torch.where(amax > 0, sc.view(torch.float32), torch.ones_like(amax))
+    inv = torch.where(amax > 0, 1.0 / sc, torch.zeros_like(amax))
+    want = torch.round(xt * inv).clamp(-127, 127).reshape(t, k).numpy().astype(np.int8)
+    assert np.array_equal(q, want) and np.array_equal(sx, sc.reshape(t, k // G).numpy())
+    assert sx[1, 0] == 1 and not q[1, :G].any()
+    assert sx[2, 0] == 0.25 and np.array_equal(q[2, :G].astype(np.float32) * 0.25, oracle.bf16_to_f32(x[2, :G]))
+
+
+def test_gemm_i8_brute_force():
+    """gemm_i8 = the scalar triple loop over the dequantized int8 operands on a tiny shape"""
+    rng = np.random.default_rng(1)
+    t, n, k, G = 3, 5, 256, 64
+    q = rng.integers(-127, 128, (t, k)).astype(np.int8)
+    sx = rng.random((t, k // G)).astype(np.float32)
+    w = rng.integers(-8, 8, (n, k))
+    s = rng.random((n, k // 128))
+    got = oracle.gemm_i8(q, sx, w, s, G)
+    want = np.zeros((t, n))
+    for i in range(t):
+        for j in range(n):
+            want[i, j] = sum(float(q[i, kk]) * float(sx[i, kk // G]) * float(w[j, kk]) * s[j, kk // 128] for kk in range(k))
+    assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
