@@ -168,9 +168,10 @@ def bench_read_floor(args, n=17408, k=5120, steps=None, warmup=None):
             "working_set": rec * args.copies}
 
 
-def bench_gemm(m, n, k, steps=10, warmup=3, copies=2, h16=False):
+def bench_gemm(m, n, k, steps=10, warmup=3, copies=2, h16=False, i8=0):
     """prefill GEMM (BASELINE config 2): TFLOP/s from the kernel's mean duration (events around each launch);
-    h16: the fp16-accumulate numerics (qe_gemm_w4h_ex, its activation pre-pass included in the time)"""
+    h16: the fp16-accumulate numerics (qe_gemm_w4h_ex), i8 = G: the W4A8 numerics with activation group G
+    (qe_gemm_w4_i8_ex); their activation pre-pass is included in the time"""
     import torch
     from qengine_amd import ops, synth
     ws = []
@@ -180,7 +181,9 @@ def bench_gemm(m, n, k, steps=10, warmup=3, copies=2, h16=False):
         del q, s
     x = synth.x_dev(m, k, seed=2)
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
-    if h16:
+    if i8:
+        fn = lambda i: ops.gemm_w4_i8(ws[i], x, G=i8, out_bf16=True, y=y)  # noqa: E731
+    elif h16:
         fn = lambda i: ops.gemm_w4h(ws[i], x, out_bf16=True, y=y)  # noqa: E731
     else:
         fn = lambda i: ops.gemm_w4(ws[i], x, out_bf16=True, y=y)  # noqa: E731
@@ -348,7 +351,9 @@ def main():
     if args.only:
         fns = {"prefill": lambda: {"k5120_n17408": bench_gemm(8192, 17408, 5120),
                                    "k17408_n5120": bench_gemm(8192, 5120, 17408),
-                                   "h16_k5120_n17408": bench_gemm(8192, 17408, 5120, h16=True)},
+                                   "h16_k5120_n17408": bench_gemm(8192, 17408, 5120, h16=True),
+                                   "w4a8_g64_k5120_n17408": bench_gemm(8192, 17408, 5120, i8=64),
+                                   "w4a8_g128_k5120_n17408": bench_gemm(8192, 17408, 5120, i8=128)},
                "w8": lambda: {"m1": bench_w8(1), "m4096": bench_w8(4096)},
                "moe": lambda: bench_moe(),
                "skinny": lambda: {f"m{m}_n{n}": (lambda r: {"us": round(r["kernel_ms_mean"] * 1e3, 2),
@@ -384,6 +389,7 @@ def main():
         secondary["prefill_k5120_n17408"] = bench_gemm(8192, 17408, 5120)
         secondary["prefill_k17408_n5120"] = bench_gemm(8192, 5120, 17408)
         secondary["prefill_h16_k5120_n17408"] = bench_gemm(8192, 17408, 5120, h16=True)
+        secondary["prefill_w4a8_g64_k5120_n17408"] = bench_gemm(8192, 17408, 5120, i8=64)
         secondary["w8_gemv_m1_k2048_n8192"] = bench_w8(1)
         secondary["w8_gemm_m4096_k2048_n8192"] = bench_w8(4096)
         secondary["moe_e512_top10_h2048_i512"] = bench_moe()
