@@ -41,6 +41,11 @@ def test_library_exports_every_declared_symbol():
     ("lib.qe_tile_w8(None, None, 16, 100, 1, None, None, None)", "tile_w8 16 100"),
     ("lib.qe_dequant_w4(None, None, 16, 64, 0, None, None)", "dequant_w4 16 64"),
     ("lib.qe_set_config(ctypes.byref((ctypes.c_int * 8)(2, 0, 5, 0, 0, 0, 0, 0)))", "batch_invariant 5"),
+    ("lib.qe_set_config(ctypes.byref((ctypes.c_int * 8)(2, 0, 0, 0, 3, 0, 0, 0)))", "gemm_h16 3"),
+    ("lib.qe_set_config(ctypes.byref((ctypes.c_int * 8)(2, 0, 0, 0, 0, 0, 7, 0)))", "reserved fields must be 0"),
+    # the reduced-precision prefill paths check their shapes and the activation group on the host
+    ("lib.qe_gemm_w4_i8_ex(None, None, 256, 512, None, 512, None, 256, 8, 48, 0, None)", "activation group G = 48"),
+    ("lib.qe_gemm_w4h_ex(None, None, 250, 512, None, 512, None, 256, 8, 0, None)", "gemm_w4h: n = 250"),
     # the allocation-free MoE layer rejects a workspace above its scratch array before touching the GPU
     ("lib.qe_moe_w4_noalloc(None, None, None, 100000, 512, 10, 2048, 512, None, 0, None)",
      "qe_moe_w4_noalloc: T 100000"),

@@ -376,4 +376,4 @@ def test_batch_invariant_w8(dev, batch_invariant):
 
 def test_config_defaults_and_checks(dev):
     c = ops.get_config()
-    assert c == {"skinny_min_m": 2, "w8_mfma_min_m": 0, "batch_invariant": 0, "gemm_tune": 0}
+    assert c == {"skinny_min_m": 2, "w8_mfma_min_m": 0, "batch_invariant": 0, "gemm_tune": 0, "gemm_h16": 0}
