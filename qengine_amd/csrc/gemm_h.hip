@@ -38,14 +38,35 @@ constexpr float kXTarget = 16.f;
 enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
 
 // one block per token (reference x_to_h_kernel, gemm.cu:262-289): the row's amax, xs = amax / 16 (1 for a zero
-// row), xh = fp16_rn(x * (1 / xs)) with the product rounded to fp32 first
+// row), xh = fp16_rn(x * (1 / xs)) with the product rounded to fp32 first. VEC: 16-byte aligned rows, 8 values per
+// load and store
+template <bool VEC>
 __global__ void __launch_bounds__(256) x_to_h_kernel(const uint16_t* __restrict__ x, int ldx, int K,
                                                      uint16_t* __restrict__ xh, float* __restrict__ xs) {
     const int t = blockIdx.x;
     const uint16_t* r = x + (size_t)t * ldx;
+    constexpr int V = VEC ? 8 : 2;
+    auto load = [&](int k, float (&f)[V]) {
+        if constexpr (VEC) {
+            const u32x4_v a = *reinterpret_cast<const u32x4_v*>(r + k);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t wa = a[i];
+                f[2 * i] = __builtin_bit_cast(float, wa << 16);
+                f[2 * i + 1] = __builtin_bit_cast(float, wa & 0xFFFF0000u);
+            }
+        } else {
+            f[0] = bf16_to_f32(r[k]);
+            f[1] = bf16_to_f32(r[k + 1]);
+        }
+    };
     float mx = 0.f;
-    for (int k = threadIdx.x * 2; k < K; k += blockDim.x * 2)
-        mx = fmaxf(mx, fmaxf(fabsf(bf16_to_f32(r[k])), fabsf(bf16_to_f32(r[k + 1]))));
+    for (int k = threadIdx.x * V; k < K; k += blockDim.x * V) {
+        float f[V];
+        load(k, f);
+#pragma unroll
+        for (int i = 0; i < V; i++) mx = fmaxf(mx, fabsf(f[i]));
+    }
     __shared__ float red[4];
     for (int o = 32; o; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
@@ -55,12 +76,20 @@ __global__ void __launch_bounds__(256) x_to_h_kernel(const uint16_t* __restrict_
     const float inv = 1.f / sc;
     if (threadIdx.x == 0) xs[t] = sc;
     uint16_t* o = xh + (size_t)t * K;
-    for (int k = threadIdx.x * 2; k < K; k += blockDim.x * 2) {
-        const float a = bf16_to_f32(r[k]) * inv, b = bf16_to_f32(r[k + 1]) * inv;
-        // the products are fp32 values first (no fused convert): the reference rounds twice
-        const float av = __builtin_amdgcn_fmed3f(a, a, a), bv = __builtin_amdgcn_fmed3f(b, b, b);
-        const f16x2_v h = {(_Float16)av, (_Float16)bv};
-        *reinterpret_cast<uint32_t*>(o + k) = __builtin_bit_cast(uint32_t, h);
+    for (int k = threadIdx.x * V; k < K; k += blockDim.x * V) {
+        float f[V];
+        load(k, f);
+        uint32_t hv[V / 2];
+#pragma unroll
+        for (int i = 0; i < V / 2; i++) {
+            // the products are fp32 values first (med3 of one value keeps the compiler from fusing the multiply into
+            // the fp16 conversion): the reference rounds twice
+            const float a = f[2 * i] * inv, b = f[2 * i + 1] * inv;
+            const f16x2_v h = {(_Float16)__builtin_amdgcn_fmed3f(a, a, a), (_Float16)__builtin_amdgcn_fmed3f(b, b, b)};
+            hv[i] = __builtin_bit_cast(uint32_t, h);
+        }
+        if constexpr (VEC) *reinterpret_cast<u32x4_v*>(o + k) = u32x4_v{hv[0], hv[1], hv[2], hv[3]};
+        else *reinterpret_cast<uint32_t*>(o + k) = hv[0];
     }
 }
 
@@ -293,12 +322,13 @@ void gemm_h_reserve(int k, int t) {
 void gemm_w4h(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st) {
     CHECK(w.n > 0 && w.n % 16 == 0 && w.k >= 128 && w.k % 128 == 0, "gemm_w4h: n = %d, k = %d", w.n, w.k);
     CHECK(t > 0, "gemm_w4h: t = %d", t);
-    CHECK(ldx >= w.k && ((uintptr_t)x & 3) == 0 && ldx % 2 == 0, "gemm_w4h: x must be 4-byte aligned, ldx >= k");
+    CHECK(ldx >= w.k, "gemm_w4h: ldx = %d < k", ldx);
     CHECK(ldc >= (w.glu ? w.n / 2 : w.n), "gemm_w4h: ldc = %d", ldc);
     char* ws = static_cast<char*>(h_ws(h_ws_bytes(w.k, t), st));
     uint16_t* xh = reinterpret_cast<uint16_t*>(ws);
     float* xs = reinterpret_cast<float*>(ws + ((size_t)t * w.k * 2 + 255) / 256 * 256);
-    x_to_h_kernel<<<dim3((unsigned)t), dim3(256), 0, st>>>(x, ldx, w.k, xh, xs);
+    if (((uintptr_t)x & 15) == 0 && ldx % 8 == 0) x_to_h_kernel<true><<<dim3((unsigned)t), dim3(256), 0, st>>>(x, ldx, w.k, xh, xs);
+    else x_to_h_kernel<false><<<dim3((unsigned)t), dim3(256), 0, st>>>(x, ldx, w.k, xh, xs);
     HIP_CHECK(hipGetLastError());
     const int nbn = (w.n + BN - 1) / BN, nbt = (t + BM - 1) / BM, ntiles = nbn * nbt;
     const unsigned blocks = (unsigned)(8 * ((ntiles + 7) / 8));

@@ -44,44 +44,56 @@ enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
 // byte p of a 16-k block holds k offset kPerm(p) = 2 (p / 4) + {0, 8, 1, 9}[p % 4]
 __device__ __forceinline__ int k_perm(int p) { return 2 * (p >> 2) + ((p & 1) ? 8 : 0) + ((p >> 1) & 1); }
 
-// one block per token; thread j quantizes the 16-k block j (reference x_to_i8_kernel, gemm.cu:540-594): the amax of
-// its G-group over the G / 16 lanes that share it, sx = bits(amax / 127) & ~3 (1 for a zero group), inv =
-// fp32(1 / sx) (0 for a zero group), q = rn(x * inv); bytes stored in the W4 word order of the block
-template <int G>
-__global__ void __launch_bounds__(256) x_to_i8_kernel(const uint16_t* __restrict__ x, int ldx, int K,
+// thread = one 16-k block of one token (the flattened (token, block) index; reference x_to_i8_kernel,
+// gemm.cu:540-594): the amax of its G-group over the G / 16 consecutive lanes that share it, sx = bits(amax / 127) &
+// ~3 (1 for a zero group), inv = fp32(1 / sx) (0 for a zero group), q = rn(x * inv); bytes stored in the W4 word
+// order of the block. VEC: x rows 16-byte aligned (two 16-byte loads per thread)
+template <int G, bool VEC>
+__global__ void __launch_bounds__(256) x_to_i8_kernel(const uint16_t* __restrict__ x, int ldx, int K, int T,
                                                       int8_t* __restrict__ xq, float* __restrict__ sx) {
     constexpr int L = G / 16;
-    const int t = blockIdx.x;
-    const uint16_t* r = x + (size_t)t * ldx;
-    for (int j0 = 0; j0 < K / 16; j0 += blockDim.x) {
-        const int j = j0 + threadIdx.x;
-        const bool live = j < K / 16;
-        float v[16];
-        float mx = 0.f;
+    const int jpr = K / 16;  // blocks per row, a multiple of L: a group never straddles two tokens
+    const long id = (long)blockIdx.x * 256 + threadIdx.x;
+    const bool live = id < (long)T * jpr;
+    const int t = live ? (int)(id / jpr) : 0, j = live ? (int)(id % jpr) : 0;
+    const uint16_t* r = x + (size_t)t * ldx + 16 * j;
+    float v[16];
+    if constexpr (VEC) {
+        const u32x4_v a = live ? *reinterpret_cast<const u32x4_v*>(r) : u32x4_v{0u, 0u, 0u, 0u};
+        const u32x4_v b = live ? *reinterpret_cast<const u32x4_v*>(r + 8) : u32x4_v{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int i = 0; i < 16; i++) {
-            v[i] = live ? bf16_to_f32(r[16 * j + i]) : 0.f;
-            mx = fmaxf(mx, fabsf(v[i]));
+        for (int i = 0; i < 4; i++) {
+            const uint32_t wa = a[i], wb = b[i];
+            v[2 * i] = __builtin_bit_cast(float, wa << 16);
+            v[2 * i + 1] = __builtin_bit_cast(float, wa & 0xFFFF0000u);
+            v[8 + 2 * i] = __builtin_bit_cast(float, wb << 16);
+            v[8 + 2 * i + 1] = __builtin_bit_cast(float, wb & 0xFFFF0000u);
         }
+    } else {
 #pragma unroll
-        for (int o = 1; o < L; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // the G / 16 lanes of a group
-        const float sc = mx > 0.f ? __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mx / 127.f) & ~3u) : 1.f;
-        const float inv = mx > 0.f ? 1.f / sc : 0.f;
-        if (!live) continue;
-        uint32_t o[4];
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-            uint32_t wv = 0;
-#pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const float qf = fminf(fmaxf(__builtin_rintf(v[k_perm(4 * u + b)] * inv), -127.f), 127.f);
-                wv |= ((uint32_t)(int)qf & 0xFFu) << (8 * b);
-            }
-            o[u] = wv;
-        }
-        *reinterpret_cast<u32x4_v*>(xq + (size_t)t * K + 16 * j) = u32x4_v{o[0], o[1], o[2], o[3]};
-        if (j % L == 0) sx[(size_t)t * (K / G) + (16 * j) / G] = sc;
+        for (int i = 0; i < 16; i++) v[i] = live ? bf16_to_f32(r[i]) : 0.f;
     }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+    for (int o = 1; o < L; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // the G / 16 lanes of a group
+    if (!live) return;
+    const float sc = mx > 0.f ? __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mx / 127.f) & ~3u) : 1.f;
+    const float inv = mx > 0.f ? 1.f / sc : 0.f;
+    uint32_t o[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            const float qf = fminf(fmaxf(__builtin_rintf(v[k_perm(4 * u + bb)] * inv), -127.f), 127.f);
+            wv |= ((uint32_t)(int)qf & 0xFFu) << (8 * bb);
+        }
+        o[u] = wv;
+    }
+    *reinterpret_cast<u32x4_v*>(xq + (size_t)t * K + 16 * j) = u32x4_v{o[0], o[1], o[2], o[3]};
+    if (j % L == 0) sx[(size_t)t * (K / G) + (16 * j) / G] = sc;
 }
 
 // 4 nibbles u (one per byte) -> 4 signed bytes u - 8
@@ -359,7 +371,9 @@ void run_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, in
     char* ws = static_cast<char*>(i8_ws(i8_ws_bytes(w.k, t), st));
     int8_t* xq = reinterpret_cast<int8_t*>(ws);
     float* sx = reinterpret_cast<float*>(ws + xq_bytes(w.k, t));
-    x_to_i8_kernel<G><<<dim3((unsigned)t), dim3(256), 0, st>>>(x, ldx, w.k, xq, sx);
+    const unsigned pb = (unsigned)(((long)t * (w.k / 16) + 255) / 256);
+    if (((uintptr_t)x & 15) == 0 && ldx % 8 == 0) x_to_i8_kernel<G, true><<<dim3(pb), dim3(256), 0, st>>>(x, ldx, w.k, t, xq, sx);
+    else x_to_i8_kernel<G, false><<<dim3(pb), dim3(256), 0, st>>>(x, ldx, w.k, t, xq, sx);
     HIP_CHECK(hipGetLastError());
     const int nbn = (w.n + BN - 1) / BN, nbt = (t + BM - 1) / BM, ntiles = nbn * nbt;
     const unsigned blocks = (unsigned)(8 * ((ntiles + 7) / 8));

@@ -133,3 +133,18 @@ def test_gemm_h_baseline_shape_sampled(dev):
     yb = out_f32(y[rows])
     bound = 1e-4 * np.sqrt(np.mean(ref ** 2)) + 2.0 ** -8 * np.abs(ref)
     assert np.all(np.abs(yb - ref) <= bound), float((np.abs(yb - ref) / bound).max())
+
+
+def test_gemm_h_unaligned_activations(dev):
+    """activation rows that are not 16-byte aligned (offset 1, row stride k + 9) take the pre-pass's scalar-load
+    path; the results equal those of the aligned copy bit for bit"""
+    n, k, t = 512, 1024, 45
+    w, _, _ = setup(n, k, 1, seed=31)
+    xa = synth.to_dev(synth.x_host(t, k, seed=32))
+    big = torch.zeros(t, k + 9, dtype=torch.bfloat16, device=dev)
+    big[:, 1:1 + k] = xa
+    xu = big[:, 1:1 + k]
+    want = ops.gemm_w4h(w, xa)
+    got = ops.gemm_w4h(w, xu)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)

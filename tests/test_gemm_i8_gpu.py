@@ -125,3 +125,18 @@ def test_gemm_i8_baseline_shape_sampled(dev):
     rows = np.random.default_rng(3).choice(t, 24, replace=False)
     ref = i8_ref(synth.bits(x[rows]), qd.cpu().numpy(), synth.bits(sd), n, k, 1, G)
     assert relrms(y[rows].cpu().numpy(), ref) < 1e-5
+
+
+def test_gemm_i8_unaligned_activations(dev):
+    """activation rows that are not 16-byte aligned (offset 1, row stride k + 9) take the pre-pass's scalar-load
+    path; the results equal those of the aligned copy bit for bit"""
+    n, k, t = 512, 1024, 45
+    w, _, _ = setup(n, k, 1, seed=31)
+    xa = synth.to_dev(synth.x_host(t, k, seed=32))
+    big = torch.zeros(t, k + 9, dtype=torch.bfloat16, device=dev)
+    big[:, 1:1 + k] = xa
+    xu = big[:, 1:1 + k]
+    want = ops.gemm_w4_i8(w, xa, G=64)
+    got = ops.gemm_w4_i8(w, xu, G=64)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
