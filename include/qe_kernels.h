@@ -188,9 +188,10 @@ void qe_glu_rows8(const int32_t* q, const uint16_t* s, int n, int k, int32_t* dq
 void qe_gemv_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu, int h16,
                 void* xh_ws, void* yh);
 
-/* prefill GEMM of a Q8 matrix (bf16 MFMA on bf16_rn(w * s) tiles), y fp32 [t][n] (or bf16 after
- * qe_gemm_set_out_bf16(1); glu: the bf16 activation [t][n/2]). Replaces reference src/capi.cpp:41. G / ci select the
- * reference's W8A8 activation grouping and kernel candidate; this build has one numerics for every value. */
+/* prefill GEMM of a Q8 matrix, y fp32 [t][n] (or bf16 after qe_gemm_set_out_bf16(1); glu: the bf16 activation
+ * [t][n/2]). Replaces reference src/capi.cpp:41. G > 0: W8A8 with activation group G (32, 64, 128; the reference's
+ * gemm_w4_i8 on a Q8 matrix: int8 activations per (token, G-group) as in qe_gemm_w4_i8, the Q8 bytes as the int8
+ * weights); G = 0: the bf16 MFMA GEMM on bf16_rn(w * s) tiles. ci (the reference's tile candidate) is ignored. */
 void qe_gemm_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, int glu, int G, int ci);
 
 /* ---- build-defined entry points (no reference counterpart; BASELINE workloads: fp16 scales, bf16 out) ---- */

@@ -238,8 +238,12 @@ void qe_gemv_q8(const void* q, const void* s, int n, int k, const uint16_t* x, f
 }
 
 void qe_gemm_q8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, int glu, int G, int ci) {
-    (void)G;
     (void)ci;
+    if (G > 0) {  // W8A8 with activation group G (the reference's gemm_w4_i8 on a Q8 matrix)
+        gemm_w4_i8(mk_w4(q, s, n, k, glu != 0, kScaleBF16), x, k, y, glu ? n / 2 : n, t, G, !glu && gemm_out_bf16(), 0,
+                   true);
+        return;
+    }
     W8 w = mk_w8(q, s, n, k, false, kScaleBF16);
     w.q8 = true;
     w.glu = glu != 0;

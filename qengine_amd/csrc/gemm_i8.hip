@@ -99,7 +99,11 @@ __global__ void __launch_bounds__(256) x_to_i8_kernel(const uint16_t* __restrict
 // 4 nibbles u (one per byte) -> 4 signed bytes u - 8
 __device__ __forceinline__ uint32_t nib_s8(uint32_t u) { return ((u | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 
-template <int G, int SDT, int OUT>
+// Q8: the weights are the Q8 layout's signed bytes (W8A8 of an INT8 matrix, reference gemm_q8_dispatch,
+// gemm.cu:4516): a row's 16-k block is word 2 s + h of the 4 records (lanes 4 g + t, t = 0..3) of its 32-k slab, in
+// the same byte order as a W4 word, so the W tile is gathered straight into LDS by 4-byte DMAs (one dword of a record
+// per lane, no unpack) one step ahead, like the activations
+template <int G, int SDT, int OUT, bool Q8>
 __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                       int N, int K, const int8_t* __restrict__ xq,
                                                       const float* __restrict__ sxg, int T, void* __restrict__ c,
@@ -134,6 +138,20 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
             const uint4* src = q + ((size_t)tl * (K >> 6) + 2 * kt) * 32 + 4 * (lane & 7) + (lane >> 4);
             dma16(src, lds32 + raw + wave * 1024);
             dma16(src + 32, lds32 + raw + BN * 32 + wave * 1024);
+        }
+    };
+    // Q8 W tile of step kt: 128 wave instructions of 256 B (two 128-B rows), 16 per wave; lane l fills dword l % 4 of
+    // chunk position (l / 4) % 8 of row 2 u + l / 32: logical chunk c = position ^ swz_f(row) = 16-k block c % 2 of
+    // 32-k slab c / 2; the dword is word 2 (c % 2) + h of record lane 4 g + (l % 4) (g = row % 8, h = (row % 16) / 8)
+    auto dma_wq8 = [&](int kt, unsigned wtile) {
+        const uint32_t* q32 = reinterpret_cast<const uint32_t*>(q);
+#pragma unroll
+        for (int i = 0; i < BN / 16; i++) {
+            const int u = wave * (BN / 16) + i, row = 2 * u + (lane >> 5);
+            const int cl = ((lane >> 2) & 7) ^ swz_f(row);
+            const int tl = min((n0 + row) >> 4, ntile_last), g = row & 7, h = (row >> 3) & 1;
+            const size_t rec = ((size_t)tl * (K >> 5) + kt * 4 + (cl >> 1)) * 32 + g * 4 + (lane & 3);
+            dma4(q32 + rec * 4 + 2 * (cl & 1) + h, lds32 + wtile + u * 256);
         }
     };
     auto dma_sc = [&](int grp, unsigned sc) {
@@ -190,19 +208,25 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
     };
 
     dma_x(0, 0);
-    dma_w4(0, kRawOff);
-    if (KT > 1) dma_w4(1, kRawOff + kRaw);
+    if constexpr (Q8) {
+        dma_wq8(0, BM * BK);
+    } else {
+        dma_w4(0, kRawOff);
+        if (KT > 1) dma_w4(1, kRawOff + kRaw);
+    }
     dma_sc(0, kScOff);
     dma_sx(0, kSxOff);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    read_words(lds + kRawOff);
+    if constexpr (!Q8) {
+        read_words(lds + kRawOff);
 #pragma unroll
-    for (int ch = 0; ch < 2; ch++)
+        for (int ch = 0; ch < 2; ch++)
 #pragma unroll
-        for (int h = 0; h < 2; h++)
+            for (int h = 0; h < 2; h++)
 #pragma unroll
-            for (int t = 0; t < 4; t++) unit(lds + BM * BK, ch, h, t);
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+                for (int t = 0; t < 4; t++) unit(lds + BM * BK, ch, h, t);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    }
 
     // step kt: DMA X (kt + 1), the raw W, weight scales and activation scales of kt + 1 / kt + 2; MFMAs of step kt
     // with the unpack of step kt + 1 (two units after each MFMA row); each activation group's sums flushed after its
@@ -212,10 +236,13 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         char* wnext = lds + ((kt + 1) & 1) * kStage + BM * BK;
         if (MORE) {
             dma_x(kt + 1, ((kt + 1) & 1) * kStage);
+            if constexpr (Q8) dma_wq8(kt + 1, ((kt + 1) & 1) * kStage + BM * BK);
             dma_sc(kt + 1, kScOff + ((kt + 1) & 1) * kSc);
             dma_sx(kt + 1, kSxOff + ((kt + 1) & 1) * kSx);
         }
-        if (kt + 2 < KT) dma_w4(kt + 2, kRawOff + (kt & 1) * kRaw);
+        if constexpr (!Q8) {
+            if (kt + 2 < KT) dma_w4(kt + 2, kRawOff + (kt & 1) * kRaw);
+        }
         const char* xt = lds + (kt & 1) * kStage;
         const char* wt = xt + BM * BK;
         i32x4_v af[2][WMT], bfr[2][WNT];  // af: X (B operand), bfr: W (A operand)
@@ -228,7 +255,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
                 bfr[buf][bb] = *reinterpret_cast<const i32x4_v*>(wt + lane_off[ks] + (wn * 32 * WNT + bb * 32) * 128);
         };
         read_frags(0, 0);
-        if constexpr (MORE) read_words(lds + kRawOff + ((kt + 1) & 1) * kRaw);
+        if constexpr (MORE && !Q8) read_words(lds + kRawOff + ((kt + 1) & 1) * kRaw);
         // weight scales of this lane's rows (4 consecutive rows per register quad, one 8-byte read) for the step
         const uint16_t* scb = reinterpret_cast<const uint16_t*>(lds + kScOff + (kt & 1) * kSc);
         const float* sxb = reinterpret_cast<const float*>(lds + kSxOff + (kt & 1) * kSx);
@@ -255,7 +282,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
                     const i32x16_v cin = ks % KPG == 0 ? i32x16_v{} : dsum[a][bb];
                     dsum[a][bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfr[ks & 1][bb], af[ks & 1][a], cin, 0, 0, 0);
                 }
-                if constexpr (MORE) {
+                if constexpr (MORE && !Q8) {
 #pragma unroll
                     for (int e = 0; e < 2; e++) {
                         const int un = 2 * slot + e;  // 16 units over 8 rows
@@ -366,7 +393,7 @@ void* i8_ws(size_t bytes, hipStream_t st) {
 size_t xq_bytes(int k, int t) { return ((size_t)t * k + 255) / 256 * 256; }
 size_t i8_ws_bytes(int k, int t) { return xq_bytes(k, t) + (size_t)t * (k / 32) * 4; }  // sx sized for G = 32
 
-template <int G>
+template <int G, bool Q8>
 void run_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int out, hipStream_t st) {
     char* ws = static_cast<char*>(i8_ws(i8_ws_bytes(w.k, t), st));
     int8_t* xq = reinterpret_cast<int8_t*>(ws);
@@ -378,7 +405,7 @@ void run_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, in
     const int nbn = (w.n + BN - 1) / BN, nbt = (t + BM - 1) / BM, ntiles = nbn * nbt;
     const unsigned blocks = (unsigned)(8 * ((ntiles + 7) / 8));
 #define QE_GI(SDT_, OUT_)                                                                                            \
-    gemm_i8_kernel<G, SDT_, OUT_><<<dim3(blocks), dim3(NTH), kLds, st>>>(w.q, w.s, w.n, w.k, xq, sx, t, c, ldc, nbn, \
+    gemm_i8_kernel<G, SDT_, OUT_, Q8><<<dim3(blocks), dim3(NTH), kLds, st>>>(w.q, w.s, w.n, w.k, xq, sx, t, c, ldc, nbn, \
                                                                           ntiles)
     if (w.sdt == kScaleF16) {
         if (out == kOutGLU) QE_GI(kScaleF16, kOutGLU);
@@ -400,14 +427,20 @@ void gemm_i8_reserve(int k, int t) {
 }
 
 void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int G, bool out_bf16,
-                hipStream_t st) {
+                hipStream_t st, bool q8) {
     CHECK(w.n > 0 && w.n % 16 == 0 && w.k >= 128 && w.k % 128 == 0, "gemm_w4_i8: n = %d, k = %d", w.n, w.k);
     CHECK(G == 32 || G == 64 || G == 128, "gemm_w4_i8: activation group G = %d (32, 64 or 128)", G);
     CHECK(t > 0, "gemm_w4_i8: t = %d", t);
     CHECK(ldx >= w.k && ((uintptr_t)x & 1) == 0, "gemm_w4_i8: ldx = %d < k", ldx);
     CHECK(ldc >= (w.glu ? w.n / 2 : w.n), "gemm_w4_i8: ldc = %d", ldc);
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
-    if (G == 32) run_i8<32>(w, x, ldx, c, ldc, t, out, st);
-    else if (G == 64) run_i8<64>(w, x, ldx, c, ldc, t, out, st);
-    else run_i8<128>(w, x, ldx, c, ldc, t, out, st);
+    if (q8) {
+        if (G == 32) run_i8<32, true>(w, x, ldx, c, ldc, t, out, st);
+        else if (G == 64) run_i8<64, true>(w, x, ldx, c, ldc, t, out, st);
+        else run_i8<128, true>(w, x, ldx, c, ldc, t, out, st);
+    } else {
+        if (G == 32) run_i8<32, false>(w, x, ldx, c, ldc, t, out, st);
+        else if (G == 64) run_i8<64, false>(w, x, ldx, c, ldc, t, out, st);
+        else run_i8<128, false>(w, x, ldx, c, ldc, t, out, st);
+    }
 }

@@ -104,7 +104,9 @@ bool gemm_split_applies(int cfg, int n, int k, int t, int ks);
 void gemm_w4h(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
 void gemm_h_reserve(int k, int t);
 // the reference's W4A8 prefill numerics (gemm_i8.hip): activation group G in {32, 64, 128}
-void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int G, bool out_bf16, hipStream_t st);
+// q8: the matrix is in the Q8 layout (signed int8 weights, W8A8)
+void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int G, bool out_bf16, hipStream_t st,
+                bool q8 = false);
 void gemm_i8_reserve(int k, int t);
 void gemm_set_out_bf16(bool on);
 // reserve the split-K workspace of the current device (grown on demand otherwise, never during graph capture)

@@ -140,3 +140,33 @@ def test_gemm_i8_unaligned_activations(dev):
     got = ops.gemm_w4_i8(w, xu, G=64)
     torch.cuda.synchronize()
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("G", [32, 64, 128])
+@pytest.mark.parametrize("glu", [False, True])
+def test_gemm_q8_w8a8(dev, G, glu):
+    """qe_gemm_q8 with G > 0 (the reference's W8A8 on a Q8 matrix, src/capi.cpp:41-44): the Q8 bytes are the int8
+    weights; within 1e-5 relative rms of the float64 emulation (int8 activations x int8 weights x both scales)"""
+    n, k, t = 512, 1024, 70
+    rng = np.random.default_rng(G + glu)
+    u = rng.integers(0, 256, (n, k))  # stored u = w + 128 (compressed-tensors 8-bit)
+    q = (u[:, 0::4] | (u[:, 1::4] << 8) | (u[:, 2::4] << 16) | (u[:, 3::4] << 24)).astype(np.uint32).view(np.int32)
+    s = synth.np_bf16((np.abs(rng.standard_normal((n, k // 128))) * 0.003).astype(np.float32))
+    if glu:
+        q, s = oracle.glu_rows(q, s, n, k, bits=8)
+    dq, ds = oracle.repack_q8(q, s, n, k)
+    xb = outlier_x(t, k, seed=G)
+    xq, sx = oracle.x_to_i8(xb, G)
+    wi = (np.stack([(q.view(np.uint32) >> (8 * b)) & 0xFF for b in range(4)], axis=2).reshape(n, k).astype(np.int64) - 128)
+    ref = oracle.gemm_i8(xq, sx, wi, oracle.bf16_to_f32(s).reshape(n, k // 128), G)
+    cols = n // 2 if glu else n
+    y = torch.zeros(t, cols, dtype=torch.bfloat16 if glu else torch.float32, device=dev)
+    call("qe_gemm_q8", synth.to_dev(dq.view(np.int8)), synth.to_dev(ds), n, k, synth.to_dev(xb), y, t, int(glu), G, 0)
+    torch.cuda.synchronize()
+    if glu:
+        act = glu_act(ref)
+        yb = out_f32(y)
+        bound = 1e-4 * np.sqrt(np.mean(act ** 2)) + 2.0 ** -8 * np.abs(act)
+        assert np.all(np.abs(yb - act) <= bound), float((np.abs(yb - act) / bound).max())
+    else:
+        assert relrms(y.cpu().numpy(), ref) < 1e-5
