@@ -13,10 +13,10 @@ void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     gemv_check(w.n, w.k, x, ldx, ldy, m, w.glu);
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
     const QeConfig& cfg = qe_config();
-    const bool aligned = ((uintptr_t)x & 15) == 0 && ldx % 8 == 0;
-    if (m == 1 && !(cfg.batch_invariant && aligned) && gemv1_w4(w, x, y, out, st)) return;
-    // the skinny kernel loads activations as 16-byte pieces; unaligned rows take the decode GEMV for every m
-    if ((m >= cfg.skinny_min_m || cfg.batch_invariant) && aligned) {
+    if (m == 1 && !cfg.batch_invariant && gemv1_w4(w, x, y, out, st)) return;  // 16-byte aligned x only
+    // the matrix-core kernel for m >= skinny_min_m (every m with batch_invariant); rows that are not 16-byte aligned
+    // take its 4-dword activation loads
+    if (m >= cfg.skinny_min_m || cfg.batch_invariant) {
         skinny_w4_mfma(w, x, ldx, y, ldy, m, out, st);
         return;
     }

@@ -20,8 +20,8 @@ void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     CHECK(ldy >= (w.glu ? w.n / 2 : w.n), "gemv_w8 ldy %d", ldy);
     CHECK(!w.glu || w.q8, "gemv_w8: GLU is for Q8 matrices");
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
-    // 16-byte aligned activation rows: the matrix-core kernel from w8_mfma_min_m rows; unaligned rows: the VALU GEMV
-    if (m >= w8_mfma_min_m(w.n, w.k) && ((uintptr_t)x & 15) == 0 && ldx % 8 == 0) {
+    // the matrix-core kernel from w8_mfma_min_m rows (rows that are not 16-byte aligned take its 4-dword loads)
+    if (m >= w8_mfma_min_m(w.n, w.k)) {
         skinny_w8_mfma(w, x, ldx, y, ldy, m, out, st);
         return;
     }

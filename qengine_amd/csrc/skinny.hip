@@ -75,7 +75,8 @@ constexpr int skinny_wsz() {  // dwords of LDS per wave: xl [UPX ? NGM : 2][MT][
 // H16: the reference's fp16 decode numerics (XH activations x / 16 in fp16 already in class-major order, weights as
 // exact integers in fp16 (Q8: w / 16), f16 MFMAs, every 64-k chunk's partial rounded to fp16 and flushed into fp32
 // with the group scale x 16 (Q8 x 256)); W4 and Q8 only
-template <int MT, int SDT, int NG, int RT, int FMT, bool H16 = false, int D = skinny_d<MT, NG, RT, FMT>(),
+// UA: activation rows only 4-byte aligned (x or ldx not 16-byte aligned): each 16-byte piece is loaded as 4 dwords
+template <int MT, int SDT, int NG, int RT, int FMT, bool H16 = false, bool UA = false, int D = skinny_d<MT, NG, RT, FMT>(),
           int WPE = skinny_wpe<MT, NG, RT, FMT>()>
 __global__ void __launch_bounds__(64 * (NG > 0 ? kMaxWaves : kMaxWavesGeneric))
 __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
@@ -108,16 +109,19 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     // (2 x kXStride = 8 banks mod 64, so the 4 rows' spans are disjoint); rows 1 apart would overlap by 4 banks.
     constexpr int XP = MT >= 4 ? MT / 4 : 1;
     auto xrow_of = [&](int e) { return MT >= 8 ? (e & 1) + 2 * (L >> 4) + 8 * (e >> 1) : (L >> 4) + 4 * e; };
-    const u32x4_v* xq[XP];
+    auto ld16 = [&](const uint32_t* p) -> u32x4_v {
+        if constexpr (UA) return u32x4_v{p[0], p[1], p[2], p[3]};
+        else return *reinterpret_cast<const u32x4_v*>(p);
+    };
+    const uint32_t* xq[XP];  // dword pointers of this lane's pieces (16-byte aligned unless UA)
 #pragma unroll
     for (int e = 0; e < XP; e++) {
         const int tp = xrow_of(e);
-        xq[e] = reinterpret_cast<const u32x4_v*>(reinterpret_cast<const uint32_t*>(x) + (size_t)(tp < m ? tp : m - 1) * xs +
-                                                 (size_t)gb * 64) + (L & 15);
+        xq[e] = reinterpret_cast<const uint32_t*>(x) + (size_t)(tp < m ? tp : m - 1) * xs + (size_t)gb * 64 + 4 * (L & 15);
     }
     auto ldxg = [&](u32x4_v* dst, int ii) {
 #pragma unroll
-        for (int e = 0; e < XP; e++) dst[e] = xq[e][ii * 16];
+        for (int e = 0; e < XP; e++) dst[e] = ld16(xq[e] + ii * 64);
     };
     auto stxg = [&](const u32x4_v* src, int buf) {
 #pragma unroll
@@ -168,9 +172,9 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             const int lc = L + 64 * pr < XL ? L + 64 * pr : XL - 1;  // lanes past the slice reload its last piece
 #pragma unroll
             for (int tok = 0; tok < MT; tok++) {
-                const u32x4_v* src = reinterpret_cast<const u32x4_v*>(xs0 + (tok < m ? tok : m - 1) * xs) + 2 * lc;
-                xv[pr][tok][0] = src[0];
-                xv[pr][tok][1] = src[1];
+                const uint32_t* src = xs0 + (tok < m ? tok : m - 1) * xs + 8 * lc;
+                xv[pr][tok][0] = ld16(src);
+                xv[pr][tok][1] = ld16(src + 4);
             }
         }
 #pragma unroll
@@ -397,7 +401,7 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
     }
 }
 
-template <int FMT, int SDT, bool H16 = false>
+template <int FMT, int SDT, bool H16 = false, bool UA = false>
 void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
             int out, int sdt, hipStream_t st, uint16_t* yh = nullptr, int ldyh = 0) {
     // the K slices of the m = 1 matrix-core kernel where they divide K, else the generic uneven slices; they depend
@@ -416,11 +420,11 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     do {                                                                                                            \
         constexpr int RT_ = skinny_rt<MT_, NG_, FMT>();                                                             \
         if (RT_ == 2 && rt2)                                                                                        \
-            skinny_kernel<MT_, SDT, NG_, RT_, FMT, H16><<<dim3((unsigned)(n / (16 * RT_))), block,                  \
+            skinny_kernel<MT_, SDT, NG_, RT_, FMT, H16, UA><<<dim3((unsigned)(n / (16 * RT_))), block,                  \
                                          (size_t)sc.S * skinny_wsz<MT_, NG_, RT_>() * 4, st>>>(                    \
                 q, s, n, k, x, ldx, y, ldy, m, out, sdt, yh, ldyh);                                                 \
         else                                                                                                        \
-            skinny_kernel<MT_, SDT, NG_, 1, FMT, H16><<<dim3((unsigned)(n / 16)), block,                            \
+            skinny_kernel<MT_, SDT, NG_, 1, FMT, H16, UA><<<dim3((unsigned)(n / 16)), block,                            \
                                               (size_t)sc.S * skinny_wsz<MT_, NG_, 1>() * 4, st>>>(                 \
                     q, s, n, k, x, ldx, y, ldy, m, out, sdt, yh, ldyh);                                             \
     } while (0)
@@ -439,7 +443,7 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     else if (mt == 4) QE_SK_NG(4);
     else if (mt == 8) QE_SK_NG(8);
     else if (mt == 16) QE_SK_NG(16);
-    else if constexpr (FMT == qe_gemv::kFmtW4 && !H16) {
+    else if constexpr (FMT == qe_gemv::kFmtW4 && !H16 && !UA) {
         // 32 rows: even slices only (the uneven-slice variant's 16 waves x 32 staged rows exceed the LDS); else two
         // launches of 16 and m - 16 rows (the same sums per row)
         if (sc.ng == 0) {
@@ -464,8 +468,15 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
 }  // namespace qe_skinny
 
 void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
-    if (w.sdt == kScaleF16) qe_skinny::launch<qe_gemv::kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
-    else qe_skinny::launch<qe_gemv::kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    using qe_gemv::kFmtW4;
+    if (((uintptr_t)x & 15) != 0 || ldx % 8 != 0) {  // rows 4-byte aligned only (the caller checked that much)
+        CHECK(m <= kMaxGemvRows, "skinny: unaligned activations take up to 16 rows per launch (m = %d)", m);
+        if (w.sdt == kScaleF16) qe_skinny::launch<kFmtW4, kScaleF16, false, true>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+        else qe_skinny::launch<kFmtW4, kScaleBF16, false, true>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+        return;
+    }
+    if (w.sdt == kScaleF16) qe_skinny::launch<kFmtW4, kScaleF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+    else qe_skinny::launch<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }
 
 // 17..32 activation rows in one pass over the weights (two 16-row B blocks per MFMA A operand)
@@ -504,6 +515,13 @@ void skinny_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q
 
 // INT8 (W8 layout with per-channel or group scales, or the Q8 layout; the scale dtype a run-time value)
 void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st) {
+    if (((uintptr_t)x & 15) != 0 || ldx % 8 != 0) {  // rows 4-byte aligned only
+        CHECK(m <= kMaxGemvRows, "skinny: unaligned activations take up to 16 rows per launch (m = %d)", m);
+        if (w.q8) qe_skinny::launch<qe_gemv::kFmtQ8, -1, false, true>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+        else if (w.per_channel) qe_skinny::launch<qe_gemv::kFmtW8C, -1, false, true>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+        else qe_skinny::launch<qe_gemv::kFmtW8G, -1, false, true>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
+        return;
+    }
     if (w.q8) qe_skinny::launch<qe_gemv::kFmtQ8, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else if (w.per_channel) qe_skinny::launch<qe_gemv::kFmtW8C, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
     else qe_skinny::launch<qe_gemv::kFmtW8G, -1>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);

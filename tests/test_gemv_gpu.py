@@ -308,23 +308,28 @@ def _unaligned_rows(xh, mode):
 @pytest.mark.parametrize("mode", ["offset", "stride"])
 @pytest.mark.parametrize("n,k", [(1024, 5120), (256, 1280)])
 def test_gemv_unaligned_activations(dev, mode, n, k):
-    """activation rows that are only 4-byte aligned take the VALU GEMV (even K slices, every group's activations
-    staged at once for m = 1 / 2): W4 and W8 against the oracle"""
+    """activation rows that are only 4-byte aligned: m = 1 takes the VALU GEMV, m >= 2 the matrix-core kernel with
+    4-dword activation loads, whose rows equal those of the aligned copy bit for bit; W4 and W8 against the oracle"""
     w, q, s = setup_w4(n, k, 1, seed=n + 3 * k)
-    xh = synth.x_host(2, k, seed=k + 7)
+    xh = synth.x_host(16, k, seed=k + 7)
     x = _unaligned_rows(xh, mode)
+    xa = synth.to_dev(xh)
     ref_ex = matmul_f64(xh, exact_w4(q, s, n, k, 1))
-    for m in (1, 2):
+    for m in (1, 2, 8, 16):
         y = ops.gemv_w4(w, x[:m])
         torch.cuda.synchronize()
         assert err_ratio(y.cpu().numpy(), ref_ex[:m]) <= 1e-4, (mode, m)
+        if m >= 2:
+            assert torch.equal(y, ops.gemv_w4(w, xa[:m])), (mode, m)
     q8, s8 = synth.w8_host(n, k, seed=n + k, per_channel=True)
     w8 = ops.tile_w8(synth.to_dev(q8), synth.to_dev(s8, torch.float16), True)
     ref8 = matmul_f64(xh, exact_w8(q8, s8, n, k, True))
-    for m in (1, 2):
+    for m in (1, 2, 16):
         y = ops.gemv_w8(w8, x[:m])
         torch.cuda.synchronize()
         assert err_ratio(y.cpu().numpy(), ref8[:m]) <= 1e-4, (mode, m)
+        if m >= 2:
+            assert torch.equal(y, ops.gemv_w8(w8, xa[:m])), (mode, m)
 
 
 # the reference's row counts for its skinny == GEMV test (reference tests/test_skinny.py:13), with the 33..64 rows of
