@@ -42,7 +42,7 @@ struct Cfg {
     static constexpr int kLdsW4 = 2 * kStage + 2 * kRaw + 2 * kSc;
 };
 
-// MODE 0 split tiles: the tiles from `ndirect` on run as `ks` K ranges each (stream-K of the last, partly filled
+// Split tiles: the tiles from `ndirect` on run as `ks` K ranges each (stream-K of the last, partly filled
 // round); their fp32 partials go to part [(tile - ndirect) * ks + split][BM][BN] and splitk_reduce_kernel adds them
 struct SplitArgs {
     int ndirect = 1 << 30;
@@ -50,19 +50,14 @@ struct SplitArgs {
     float* part = nullptr;
 };
 
-// MODE 0: the dense GEMM. MODE 1 / 2: the MoE grouped gate_up / down GEMMs (MoePfArgs), INT4 only: block
-// (job, n tile) with the job's rows gathered (gate_up: x rows of the slots' tokens, down: act rows of the slots),
-// the W tile from the job's expert records (gate_up: the 256 GLU rows of record n tile, K = H; down: H rows, K = I,
-// 128 k per record), and the epilogue into the slot rows.
-template <int FMT, int SDT, int WMT, int WNT, int MODE = 0>
+template <int FMT, int SDT, int WMT, int WNT>
 __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                    int N, int K, const uint16_t* __restrict__ x, int ldx, int T,
                                                    void* __restrict__ c, int ldc, int out, int sdt, int nbn, int nbt,
-                                                   MoePfArgs ma, SplitArgs sp) {
+                                                   SplitArgs sp) {
     using C = Cfg<WMT, WNT>;
     constexpr int BM = C::BM, BN = C::BN;
     constexpr bool W4 = FMT == kFmtW4;
-    static_assert(MODE == 0 || (W4 && BN == 256), "MoE modes: INT4, 256-row tiles (one gate_up record)");
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -70,72 +65,38 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     // XCD-aware tile order: block b runs on XCD b % 8; XCD j takes tiles [j * per, (j + 1) * per) of the
     // n-major tile sequence (consecutive tiles share the X tile, a band of them shares W tiles)
     int n0, t0;
-    int e = 0, slot0 = 0, nt = 0;
     int kt0 = 0, KTL = K / BK;  // this block's k steps [kt0, kt0 + KTL)
     int split_slot = -1;        // >= 0: a split tile's part, stored raw to sp.part
-    if constexpr (MODE == 0) {
-        // tiles [0, sp.ndirect): whole K, XCD bands; tiles [sp.ndirect, ntiles): split into sp.ks K ranges whose
-        // fp32 partials splitk_reduce_kernel sums (the blocks of the otherwise partly idle last round)
-        const int ntiles = nbn * nbt, per = (sp.ndirect + 7) >> 3;
-        const int b = blockIdx.x;
-        int tile;
-        if (b < 8 * per) {
-            tile = (b & 7) * per + (b >> 3);
-            if (tile >= sp.ndirect) return;
-        } else {
-            const int j = b - 8 * per;
-            tile = sp.ndirect + j / sp.ks;
-            if (tile >= ntiles) return;
-            KTL = K / BK / sp.ks;
-            kt0 = (j % sp.ks) * KTL;
-            split_slot = j;
-        }
-        n0 = (tile % nbn) * BN;
-        t0 = (tile / nbn) * BM;
+    // tiles [0, sp.ndirect): whole K, XCD bands; tiles [sp.ndirect, ntiles): split into sp.ks K ranges whose
+    // fp32 partials splitk_reduce_kernel sums (the blocks of the otherwise partly idle last round)
+    const int ntiles = nbn * nbt, per = (sp.ndirect + 7) >> 3;
+    const int b = blockIdx.x;
+    int tile;
+    if (b < 8 * per) {
+        tile = (b & 7) * per + (b >> 3);
+        if (tile >= sp.ndirect) return;
     } else {
-        // block b runs on XCD b % 8: the n tiles of a job run there one after another (they share its gathered
-        // rows in that L2) and the jobs, job % 8 = XCD, spread over all XCDs whatever the job count
-        const int b = blockIdx.x, r = b >> 3;
-        nt = r % nbn;
-        const int job = (r / nbn) * 8 + (b & 7);
-        if (job >= *ma.njobs) return;
-        e = ma.jobs[2 * job];
-        slot0 = ma.off[e] + ma.jobs[2 * job + 1];
-        T = min(BM, ma.off[e + 1] - slot0);  // rows of the job
-        n0 = MODE == 1 ? 0 : nt * BN;
-        t0 = 0;
-        if constexpr (MODE == 1) {  // the record's GLU rows: a 256 x H W4 matrix
-            const char* rp = ma.recs + ((size_t)e * ma.ngrp + nt) * ma.rec;
-            q = reinterpret_cast<const uint4*>(rp);
-            s = reinterpret_cast<const uint16_t*>(rp + ma.gg_q);
-        }
+        const int j = b - 8 * per;
+        tile = sp.ndirect + j / sp.ks;
+        if (tile >= ntiles) return;
+        KTL = K / BK / sp.ks;
+        kt0 = (j % sp.ks) * KTL;
+        split_slot = j;
     }
+    n0 = (tile % nbn) * BN;
+    t0 = (tile / nbn) * BM;
     const int G = K >> 7;
 
     // ---- X (every format): LDS DMA (global_load_lds_dwordx4), 1 KB = 8 rows per wave instruction. Lane i lands at
     //      LDS slot i of the 8-row block, so it loads the chunk that the swizzle puts there. Rows past T re-read
     //      row T - 1 (their outputs are not stored).
-    // (MoE: the gathered row of each of this lane's DMA rows, fixed for the block)
-    const uint16_t* xrow[MODE == 0 ? 1 : C::XDMA];
-    if constexpr (MODE != 0) {
-#pragma unroll
-        for (int i = 0; i < C::XDMA; i++) {
-            const int row = (wave * C::XDMA + i) * 8 + (lane >> 3);
-            const int sl = slot0 + (row < T ? row : T - 1);
-            xrow[i] = ma.a + (MODE == 1 ? (size_t)ma.slot_tok[sl] * ma.H : (size_t)sl * ma.I);
-        }
-    }
     auto dma_x = [&](int kt, unsigned xt) {  // xt: LDS offset of the X tile from lds[]
 #pragma unroll
         for (int i = 0; i < C::XDMA; i++) {
             const int r0 = (wave * C::XDMA + i) * 8, row = r0 + (lane >> 3);
             const int ch = (lane & 7) ^ swz_f(row);
-            if constexpr (MODE == 0) {
-                const int tok = t0 + row < T ? t0 + row : T - 1;
-                dma16(x + (size_t)tok * ldx + kt * BK + ch * 8, lds32 + xt + r0 * 128);
-            } else {
-                dma16(xrow[i] + kt * BK + ch * 8, lds32 + xt + r0 * 128);
-            }
+            const int tok = t0 + row < T ? t0 + row : T - 1;
+            dma16(x + (size_t)tok * ldx + kt * BK + ch * 8, lds32 + xt + r0 * 128);
         }
     };
     // ---- W, INT4 path. Raw records go to LDS by DMA: a 1 KB wave load covers two 16-row tiles; lane i holds record
@@ -146,24 +107,9 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     const bool jactive = tid < NJOB;
     const int jj = tid & 3, jg = (tid >> 2) & 7, jtr = tid >> 5;
     const int ntile_last = (N >> 4) - 1;
-    // record (tile tl, 64-k step kt) and scales (tile tl, group grp); MoE down: 128 k per record, in the record's
-    // [H / 16][2][32][4] down layout with [H / 16][16] scales
-    auto w_rec = [&](int tl, int kt) -> const uint4* {
-        if constexpr (MODE == 2) {
-            const char* rp = ma.recs + ((size_t)e * ma.ngrp + (kt >> 1)) * ma.rec + ma.gg_q + ma.gg_s;
-            return reinterpret_cast<const uint4*>(rp) + ((size_t)tl * 2 + (kt & 1)) * 32;
-        } else {
-            return q + ((size_t)tl * (K >> 6) + kt) * 32;
-        }
-    };
-    auto w_sc = [&](int tl, int grp) -> const uint16_t* {
-        if constexpr (MODE == 2) {
-            const char* rp = ma.recs + ((size_t)e * ma.ngrp + grp) * ma.rec + ma.gg_q + ma.gg_s + ma.gd_q;
-            return reinterpret_cast<const uint16_t*>(rp) + (size_t)tl * 16;
-        } else {
-            return s + ((size_t)tl * G + grp) * 16;
-        }
-    };
+    // record (tile tl, 64-k step kt) and scales (tile tl, group grp)
+    auto w_rec = [&](int tl, int kt) -> const uint4* { return q + ((size_t)tl * (K >> 6) + kt) * 32; };
+    auto w_sc = [&](int tl, int grp) -> const uint16_t* { return s + ((size_t)tl * G + grp) * 16; };
     auto dma_w4 = [&](int kt, unsigned raw) {  // raw: LDS offset of the raw record buffer
         if (wave < BN / 32) {
             const int tl = min((n0 >> 4) + 2 * wave + ((lane >> 3) & 1), ntile_last);
@@ -292,13 +238,6 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[a][bb][r] = 0.f;
 
-    // MoE jobs: 32-row MFMA tiles of this wave that hold a row of the job (bit a); the others skip their fragment
-    // reads and MFMAs (their outputs are not stored). Wave-uniform.
-    const unsigned alive = __builtin_amdgcn_readfirstlane(MODE == 0 ? ~0u : [&] {
-        unsigned mk = 0;
-        for (int a = 0; a < WMT; a++) mk |= (wm * 32 * WMT + a * 32 < T ? 1u : 0u) << a;
-        return mk;
-    }());
     // one k step: MFMAs on stage kt % 2 while the next step's tiles go into the other stage
     int lane_off[BK / 16];  // swz(l % 32, 2 ks + l / 32) of this lane
 #pragma unroll
@@ -319,8 +258,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             const char* wl = wt + lane_off[ks];
 #pragma unroll
             for (int a = 0; a < WMT; a++)
-                if (MODE == 0 || (alive >> a) & 1)
-                    af[buf][a] = *reinterpret_cast<const bf16x8_v*>(xl + (wm * 32 * WMT + a * 32) * 128);
+                af[buf][a] = *reinterpret_cast<const bf16x8_v*>(xl + (wm * 32 * WMT + a * 32) * 128);
 #pragma unroll
             for (int bb = 0; bb < WNT; bb++)
                 bfr[buf][bb] = *reinterpret_cast<const bf16x8_v*>(wl + (wn * 32 * WNT + bb * 32) * 128);
@@ -338,8 +276,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             for (int a = 0; a < WMT; a++) {
 #pragma unroll
                 for (int bb = 0; bb < WNT; bb++)
-                    if (MODE == 0 || (alive >> a) & 1)
-                        acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][bb], af[ks & 1][a], acc[a][bb], 0, 0, 0);
+                    acc[a][bb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][bb], af[ks & 1][a], acc[a][bb], 0, 0, 0);
                 between(ks * WMT + a);
                 fence();
             }
@@ -446,7 +383,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
     //      ldc / c are not aligned for them. GLU: gate row g and up row g + 8 of a 16-row tile are registers r and
     //      r + 4 of the same lane.
     const int cj = lane & 31, ci = 4 * (lane >> 5);
-    if (MODE == 0 && split_slot >= 0) {
+    if (split_slot >= 0) {
         // raw fp32 partial of the whole BM x BN tile, [token][row] (rows past N / tokens past T included)
         float* pp = sp.part + (size_t)split_slot * BM * BN;
 #pragma unroll
@@ -462,7 +399,7 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
                 }
         return;
     }
-    const bool vec = MODE != 0 || ((ldc & 3) == 0 && ((uintptr_t)c & (out == kOutF32 ? 15u : 7u)) == 0);
+    const bool vec = (ldc & 3) == 0 && ((uintptr_t)c & (out == kOutF32 ? 15u : 7u)) == 0;
     auto st4 = [&](uint16_t* p, float v0, float v1, float v2, float v3) {  // 4 consecutive bf16
         if (vec) {
             *reinterpret_cast<uint2*>(p) = uint2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)};
@@ -483,25 +420,14 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
             for (int rb = 0; rb < 4; rb++) {
                 const int n = n0 + wn * 32 * WNT + bb * 32 + 8 * rb + ci;  // first of the 4 columns
                 const f32x16_v& v = acc[a][bb];
-                const bool glu = MODE == 1 || (MODE == 0 && out == kOutGLU);
-                if (glu) {
+                if (out == kOutGLU) {
                     if (rb & 1) continue;  // rows 8 (rb + 1) + ..: the up rows of this gate block
                     float g[4];
 #pragma unroll
                     for (int j = 0; j < 4; j++) g[j] = silu_f32(v[4 * rb + j]) * v[4 * rb + 4 + j];
-                    if constexpr (MODE == 1) {
-                        // the record's 256 GLU rows are act columns 128 nt .. + 128; times the slot's routing weight
-                        const float sw = ma.slot_w[slot0 + tok];
-                        st4(ma.out + (size_t)(slot0 + tok) * ma.I + nt * 128 + (n >> 4) * 8 + (n & 7), g[0] * sw,
-                            g[1] * sw, g[2] * sw, g[3] * sw);
-                    } else if (n < N) {
+                    if (n < N)
                         st4(reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + (n >> 4) * 8 + (n & 7), g[0], g[1],
                             g[2], g[3]);
-                    }
-                } else if constexpr (MODE == 2) {
-                    if (n < N)
-                        st4(ma.out + (size_t)(slot0 + tok) * ma.H + n, v[4 * rb], v[4 * rb + 1], v[4 * rb + 2],
-                            v[4 * rb + 3]);
                 } else if (n < N) {
                     if (out == kOutBF16) {
                         st4(reinterpret_cast<uint16_t*>(c) + (size_t)tok * ldc + n, v[4 * rb], v[4 * rb + 1],
@@ -648,7 +574,7 @@ void launch_cfg(const uint4* q, const uint16_t* s, int n, int k, const uint16_t*
     const int per = (g.ndirect + 7) / 8;
     const unsigned blocks = (unsigned)(8 * per + g.nsplit * g.ks);
     gemm_kernel<FMT, SDT, WMT, WNT><<<dim3(blocks), dim3(NTH), FMT == kFmtW4 ? C::kLdsW4 : 2 * C::kStage, st>>>(
-        q, s, n, k, x, ldx, t, c, ldc, out, sdt, g.nbn, g.nbt, MoePfArgs{}, sp);
+        q, s, n, k, x, ldx, t, c, ldc, out, sdt, g.nbn, g.nbt, sp);
     HIP_CHECK(hipGetLastError());
     if (g.nsplit > 0) {
         const size_t threads = (size_t)g.nsplit * C::BM * (C::BN / 16);
@@ -757,23 +683,6 @@ void gemm_check(int n, int k, const void* x, int ldx, int ldc, int t, bool glu) 
 }
 
 }  // namespace
-
-// MoE grouped prefill GEMMs: 128 rows (a job) x 256 weight rows (gate_up: one record) per block, 8 waves of
-// 64 x 64; grid = 8 XCD lanes x ceil(max_jobs / 8) job groups x n tiles (blocks past the job count exit)
-void moe_pf_gemm(int mode, const MoePfArgs& a, hipStream_t st) {
-    using C = Cfg<2, 2>;
-    static_assert(C::BM == kMoePfRows && C::BN == 256, "MoE prefill tile");
-    CHECK(a.H % 256 == 0 && a.I % 128 == 0 && a.max_jobs >= 1, "moe_pf H %d I %d", a.H, a.I);
-    const int nbn = mode == 1 ? a.ngrp : a.H / C::BN;
-    const unsigned grid = 8u * (unsigned)((a.max_jobs + 7) / 8) * (unsigned)nbn;
-    if (mode == 1)
-        gemm_kernel<kFmtW4, kScaleF16, 2, 2, 1><<<dim3(grid), dim3(NTH), C::kLdsW4, st>>>(
-            nullptr, nullptr, 256, a.H, nullptr, 0, 0, nullptr, 0, kOutGLU, kScaleF16, nbn, 0, a, SplitArgs{});
-    else
-        gemm_kernel<kFmtW4, kScaleF16, 2, 2, 2><<<dim3(grid), dim3(NTH), C::kLdsW4, st>>>(
-            nullptr, nullptr, a.H, a.I, nullptr, 0, 0, nullptr, 0, kOutBF16, kScaleF16, nbn, 0, a, SplitArgs{});
-    HIP_CHECK(hipGetLastError());
-}
 
 void gemm_w4(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st,
              bool tuned) {

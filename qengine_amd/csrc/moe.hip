@@ -16,7 +16,8 @@
 //
 // Decode (T <= 32): the grouped GEMVs reuse the decode GEMV tile (gemv_impl.hpp) with gathered activation rows,
 // jobs = (expert, chunk of <= 2 rows). Prefill: grouped MFMA GEMMs over (expert, 128-row tile) jobs, one block per
-// (job, 256 weight rows): every expert's weights are read once per 128 of its rows.
+// (job, 512 weight rows), the weights dequantized in registers (moe_pf.hip): every expert's weights are read once
+// per 128 of its rows.
 #include "gemv_impl.hpp"
 #include "../../include/qe_kernels.h"
 
@@ -652,7 +653,7 @@ __global__ void __launch_bounds__(64 * 16) moe_dec_down_combine_kernel(
 }
 
 // ------------------------------------------------------------------ prefill grouped GEMMs
-// (expert, 128-row) jobs on the prefill GEMM's W4 pipeline: moe_pf_gemm in gemm.hip
+// (expert, 128-row) jobs: moe_pf_gemm in moe_pf.hip
 
 // ------------------------------------------------------------------ combine: out[t] = sum_k slot_out[inv[t, k]]
 // block t, H / 8 threads: each thread's 8 columns of every slot of the token are one 16-byte load, all issued

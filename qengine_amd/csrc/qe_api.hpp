@@ -120,7 +120,7 @@ int qe_num_cus();
 // device address of the MoE scratch array on the current device (moe.hip; resolved once per device)
 void* moe_scratch_ptr();
 
-// ---- grouped prefill GEMMs of the MoE layer on the prefill GEMM's W4 pipeline (gemm.hip) ----
+// ---- grouped prefill GEMMs of the MoE layer (moe_pf.hip: weights dequantized in registers) ----
 // Jobs are (expert, first row) pairs over the expert-sorted slots, kMoePfRows rows each (moe.hip's segmentation).
 // mode 1, gate_up: act[slot][I] = bf16(silu(gate) * up * slot_w[slot]) from the records' GLU rows over x[token];
 // mode 2, down: slot_out[slot][H] = bf16(act[slot] . down) over the records' down columns.
