@@ -45,8 +45,8 @@ __device__ __forceinline__ uint32_t nib_mask_hi() {
 
 // MODE 1: gate_up, N = 2 I GLU rows (records of 256 rows x K = H), epilogue act[slot][I] = silu(gate) up w_slot.
 // MODE 2: down, N = H rows, K = I over the expert's records (128 k each), epilogue slot_out[slot][H].
-// NA: 32-row token tiles holding a row of the job (the others are not computed).
-template <int MODE, int NA>
+// NA: 32-row token tiles holding a row of the job (the others are not computed). SHORT: K = 128 (two k steps).
+template <int MODE, int NA, bool SHORT>
 __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, int e, int slot0, int T) {
     constexpr int NS = 2 * NA;  // MFMAs per k16 step
     const int tid = threadIdx.x, lane = tid & 63;
@@ -56,6 +56,7 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
     const int KT = K / BK, G = K >> 7;
     const int wrow = nt * BN + 64 * wave;  // first weight row of this wave
     const bool wact = wrow < N;            // wave-uniform: N is a multiple of 64
+    const int drow = wact ? wrow : N - 64;  // rows whose records a wave loads (waves past N: loaded, not used)
     const int m = lane & 31, kh = lane >> 5, g = m & 7;
     const int tl = (wrow >> 4) + (m >> 3);  // the lane's 16-row tile among the expert's N rows
 
@@ -63,9 +64,9 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
     // LDS slot 64 d + i = 32 t + m (m = i % 32: the row pair of A row m)
     const int dt = (lane >> 3) & 3;  // wave tile of this lane's DMA record
     auto w_at = [&](int kt) -> const uint4* {
-        const int t2 = (wrow >> 4) + dt;
+        const int t2 = (drow >> 4) + dt;
         if constexpr (MODE == 1) {
-            const char* rp = ma.recs + ((size_t)e * ma.ngrp + (wrow >> 8)) * ma.rec;
+            const char* rp = ma.recs + ((size_t)e * ma.ngrp + (drow >> 8)) * ma.rec;
             return reinterpret_cast<const uint4*>(rp) + ((size_t)(t2 & 15) * (K >> 6) + kt) * 32 + 4 * g + kh;
         } else {
             const char* rp = ma.recs + ((size_t)e * ma.ngrp + (kt >> 1)) * ma.rec + ma.gg_q + ma.gg_s;
@@ -75,9 +76,9 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
     // scale dword (rows 2 d, 2 d + 1) of wave tile q for group grp; DMA lane l fetches q = (l / 8) % 4, d = l % 8
     const int sq = (lane >> 3) & 3, sd = lane & 7;
     auto s_at = [&](int grp) -> const uint16_t* {
-        const int t = (wrow >> 4) + sq;
+        const int t = (drow >> 4) + sq;
         if constexpr (MODE == 1) {
-            const char* rp = ma.recs + ((size_t)e * ma.ngrp + (wrow >> 8)) * ma.rec + ma.gg_q;
+            const char* rp = ma.recs + ((size_t)e * ma.ngrp + (drow >> 8)) * ma.rec + ma.gg_q;
             return reinterpret_cast<const uint16_t*>(rp) + ((size_t)(t & 15) * G + grp) * 16 + 2 * sd;
         } else {
             const char* rp = ma.recs + ((size_t)e * ma.ngrp + grp) * ma.rec + ma.gg_q + ma.gg_s + ma.gd_q;
@@ -85,51 +86,32 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
         }
     };
     // gathered activation rows: wave w stages rows 16 w .. 16 w + 15 (two 1 KB DMAs of 8 rows; lane i lands at slot i
-    // of its 8-row block, so it loads the chunk the swizzle puts there). Rows past T are not loaded: they feed only
-    // output columns (tokens) that are not stored. An 8-row block with no row below T issues no DMA; one with some
-    // has lane 0 active, so its DMA is always issued (the waits count DMAs).
-    const bool xb0 = wave * 16 < T, xb1 = wave * 16 + 8 < T;  // wave-uniform
+    // of its 8-row block, so it loads the chunk the swizzle puts there); rows past T re-read row T - 1 (their outputs
+    // are not stored)
     const uint16_t* xrow[2];
-    bool xlane[2];
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int row = wave * 16 + i * 8 + (lane >> 3);
-        xlane[i] = row < T;
         const int sl = slot0 + (row < T ? row : T - 1);
         xrow[i] = ma.a + (MODE == 1 ? (size_t)ma.slot_tok[sl] * ma.H : (size_t)sl * ma.I) + ((lane & 7) ^ swz_f(row)) * 8;
     }
-    // step kt's DMAs into buffer kt % 4: the activation rows (2 per wave), this wave's records (2) and scales (1)
+    // step kt's 5 DMAs per wave into buffer kt % 4: the activation rows (2), the wave's records (2) and scales (1).
+    // Every wave issues the same 5, so a wait for all but the last `after` steps is vmcnt(5 after).
     auto dma_step = [&](int kt) {
         const int buf = kt % NBUF;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            if (i ? xb1 : xb0) {
-                if (xlane[i]) dma16(xrow[i] + kt * BK, lds32 + buf * kXStage + (wave * 16 + i * 8) * 128);
-            }
-        }
-        if (wact) {
-            const uint4* p = w_at(kt);
-            const unsigned dst = lds32 + kRawOff + (buf * 8 + wave) * kRawWave;
-            dma16(p, dst);          // t = 0, 1
-            dma16(p + 2, dst + 1024);  // t = 2, 3
-            dma4(s_at(kt >> 1), lds32 + kScOff + (buf * 8 + wave) * kScWave);
-        }
+        for (int i = 0; i < 2; i++) dma16(xrow[i] + kt * BK, lds32 + buf * kXStage + (wave * 16 + i * 8) * 128);
+        const uint4* p = w_at(kt);
+        const unsigned dst = lds32 + kRawOff + (buf * 8 + wave) * kRawWave;
+        dma16(p, dst);             // t = 0, 1
+        dma16(p + 2, dst + 1024);  // t = 2, 3
+        dma4(s_at(kt >> 1), lds32 + kScOff + (buf * 8 + wave) * kScWave);
     };
-    // wait until the DMAs of all but the `after` most recently issued steps have landed (a wave issues `per` DMAs a
-    // step: vmcnt counts them in issue order)
-    const int per = (xb0 ? 1 : 0) + (xb1 ? 1 : 0) + (wact ? 3 : 0);
-    auto wait_dma = [&](int after) {
-        switch (after * per) {
-            case 1: asm volatile("s_waitcnt vmcnt(1)" ::: "memory"); break;
-            case 2: asm volatile("s_waitcnt vmcnt(2)" ::: "memory"); break;
-            case 3: asm volatile("s_waitcnt vmcnt(3)" ::: "memory"); break;
-            case 4: asm volatile("s_waitcnt vmcnt(4)" ::: "memory"); break;
-            case 5: asm volatile("s_waitcnt vmcnt(5)" ::: "memory"); break;
-            case 6: asm volatile("s_waitcnt vmcnt(6)" ::: "memory"); break;
-            case 8: asm volatile("s_waitcnt vmcnt(8)" ::: "memory"); break;
-            case 10: asm volatile("s_waitcnt vmcnt(10)" ::: "memory"); break;
-            default: asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); break;
-        }
+    auto wait_dma = [&](auto after) {
+        constexpr int A = decltype(after)::value;
+        if constexpr (A == 2) asm volatile("s_waitcnt vmcnt(10)" ::: "memory");
+        else if constexpr (A == 1) asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+        else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     };
 
     f32x16_v acc[NA][2];
@@ -180,12 +162,17 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
-
-    // prologue: DMAs of steps 0, 1, 2 (KT >= 2), wait for step 0, its first operands
+    using P2 = std::integral_constant<int, 2>;
+    using PM1 = std::integral_constant<int, -1>;
+    // prologue: DMAs of steps 0, 1, 2 (0, 1 if SHORT), wait for step 0, its first operands
     dma_step(0);
     dma_step(1);
-    if (KT > 2) dma_step(2);
-    wait_dma(KT > 2 ? 2 : 1);
+    if constexpr (SHORT) {
+        wait_dma(P1{});
+    } else {
+        dma_step(2);
+        wait_dma(P2{});
+    }
     __builtin_amdgcn_s_barrier();
     if (wact) {
         load_step(0, P0{});
@@ -199,16 +186,15 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
         for (int a = 0; a < NA; a++) xf[buf][a] = *reinterpret_cast<const bf16x8_v*>(xt + xo[ks] + a * 32 * 128);
     };
 
-    // step kt (set = kt % 2): DMAs of kt + 3; per k16 step ks the 2 NA MFMAs on the current operands, each followed
-    // by its share of the 8 units that build the next operands (ks + 1 from this step's set, or step kt + 1's first
-    // from the other set: its records are read at ks = 2, after the wait for its DMAs). Nothing is scheduled across
-    // the fences, so the units keep their place.
-    auto kstep = [&](int kt, auto more, auto set) {
+    // step kt (set = kt % 2): DMAs of kt + 3 (DMA); per k16 step ks the 2 NA MFMAs on the current operands, each
+    // followed by its share of the 8 units that build the next operands (ks + 1 from this step's set, or step kt + 1's
+    // first from the other set: its records are read at ks = 2, after the wait for its DMAs; AFTER: steps issued
+    // after kt + 1). Nothing is scheduled across the fences, so the units keep their place.
+    auto kstep = [&](int kt, auto more, auto set, auto dma, auto after) {
         constexpr bool MORE = decltype(more)::value;
         constexpr int S = decltype(set)::value;
         using SN = std::integral_constant<int, S ^ 1>;
-        if (kt + 3 < KT) dma_step(kt + 3);
-        const int after = min(KT - kt - 2, 2);  // steps issued after kt + 1
+        if constexpr (decltype(dma)::value) dma_step(kt + 3);
         if (wact) {
             const char* xt = lds + (kt % NBUF) * kXStage;
             read_x(xt, 0, 0);
@@ -241,16 +227,26 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
                 }
             }
         }
-        wait_dma(max(after, 0));
+        wait_dma(after);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     };
-    // KT is even (K is a multiple of 128): pairs of steps, the last pair without a next step
-    for (int kt = 0; kt + 2 < KT; kt += 2) {
-        kstep(kt, std::true_type{}, P0{});
-        kstep(kt + 1, std::true_type{}, P1{});
+    // KT even, >= 4: pairs of steps with DMAs three ahead, then the last four (DMA of the last step, none); SHORT:
+    // the two steps
+    using T_ = std::true_type;
+    using F_ = std::false_type;
+    if constexpr (SHORT) {
+        kstep(0, T_{}, P0{}, F_{}, P0{});
+        kstep(1, F_{}, P1{}, F_{}, PM1{});
+    } else {
+        for (int kt = 0; kt + 4 < KT; kt += 2) {
+            kstep(kt, T_{}, P0{}, T_{}, P2{});
+            kstep(kt + 1, T_{}, P1{}, T_{}, P2{});
+        }
+        kstep(KT - 4, T_{}, P0{}, T_{}, P2{});
+        kstep(KT - 3, T_{}, P1{}, F_{}, P1{});
+        kstep(KT - 2, T_{}, P0{}, F_{}, P0{});
+        kstep(KT - 1, F_{}, P1{}, F_{}, PM1{});
     }
-    kstep(KT - 2, std::true_type{}, P0{});
-    kstep(KT - 1, std::false_type{}, P1{});
 
     if (!wact) return;
     // epilogue: lane l holds token a * 32 + l % 32; register r = 4 q + j is row pair g = 4 (l / 32) + j of tile q
@@ -299,10 +295,19 @@ __global__ void __launch_bounds__(NTH) moe_rw_kernel(MoePfArgs ma, int nbn) {
     const int slot0 = ma.off[e] + ma.jobs[2 * job + 1];
     const int T = min(BM, ma.off[e + 1] - slot0);  // rows of the job, >= 1
     const int na = __builtin_amdgcn_readfirstlane((T + 31) >> 5);
-    if (na >= 4) rw_body<MODE, 4>(ma, lds, nt, e, slot0, T);
-    else if (na == 3) rw_body<MODE, 3>(ma, lds, nt, e, slot0, T);
-    else if (na == 2) rw_body<MODE, 2>(ma, lds, nt, e, slot0, T);
-    else rw_body<MODE, 1>(ma, lds, nt, e, slot0, T);
+    if ((MODE == 1 ? ma.H : ma.I) == 128) {
+        if constexpr (MODE == 2) {  // (gate_up: K = H, a multiple of 512)
+            if (na >= 4) rw_body<MODE, 4, true>(ma, lds, nt, e, slot0, T);
+            else if (na == 3) rw_body<MODE, 3, true>(ma, lds, nt, e, slot0, T);
+            else if (na == 2) rw_body<MODE, 2, true>(ma, lds, nt, e, slot0, T);
+            else rw_body<MODE, 1, true>(ma, lds, nt, e, slot0, T);
+        }
+        return;
+    }
+    if (na >= 4) rw_body<MODE, 4, false>(ma, lds, nt, e, slot0, T);
+    else if (na == 3) rw_body<MODE, 3, false>(ma, lds, nt, e, slot0, T);
+    else if (na == 2) rw_body<MODE, 2, false>(ma, lds, nt, e, slot0, T);
+    else rw_body<MODE, 1, false>(ma, lds, nt, e, slot0, T);
 }
 
 }  // namespace qe_moe_rw
@@ -311,7 +316,9 @@ __global__ void __launch_bounds__(NTH) moe_rw_kernel(MoePfArgs ma, int nbn) {
 void moe_pf_gemm(int mode, const MoePfArgs& a, hipStream_t st) {
     using namespace qe_moe_rw;
     const int N = mode == 1 ? 2 * a.I : a.H, K = mode == 1 ? a.H : a.I;
-    CHECK(N % 64 == 0 && K % 128 == 0 && a.max_jobs >= 1, "moe_pf_rw mode %d N %d K %d", mode, N, K);
+    // K = 128 runs the two-step variant; the others need an even number of 64-k steps, at least 4
+    CHECK(N % 64 == 0 && K % 128 == 0 && (mode == 2 || K >= 512) && a.max_jobs >= 1, "moe_pf mode %d N %d K %d", mode,
+          N, K);
     const int nbn = (N + BN - 1) / BN;
     const unsigned grid = 8u * (unsigned)((a.max_jobs + 7) / 8) * (unsigned)nbn;
     if (mode == 1) moe_rw_kernel<1><<<grid, NTH, kLds, st>>>(a, nbn);
