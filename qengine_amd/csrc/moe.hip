@@ -85,10 +85,11 @@ __device__ __forceinline__ void route_step(uint64_t& k) {
     k = k2 > k ? k2 : k;
 }
 
-// Lane l holds the keys of experts l + 64 i (i < PER = ceil(E / 64); missing experts key 0). Each of the topk rounds
-// takes the lane's largest unselected key, reduces the lanes' candidates to the wave's largest key by DPP (quad
-// swaps, row rotations by 4 and 8, row broadcasts 15 and 31: lane 63 holds it) and the lane that held it marks that
-// key selected: no LDS traffic, no barriers, one 64-bit compare per step. Keys are distinct, so the order is total.
+// Lane l holds the keys of experts l + 64 i (i < PER = ceil(E / 64); missing experts key 0), sorted descending in
+// its registers (a bitonic network, no cross-lane dependence). Each of the topk rounds reduces the lanes' heads to the
+// wave's largest key by DPP (quad swaps, row rotations by 4 and 8, row broadcasts 15 and 31: lane 63 holds it), and
+// the lane whose head it was shifts its list by one: no LDS traffic, no barriers, one 64-bit compare per step. Keys
+// are distinct, so the order is total and exactly one lane wins each round.
 // one token t by the calling wave; sel / w: the token's topk outputs (global or LDS)
 template <int PER>
 __device__ __forceinline__ void route_token(const float* __restrict__ logits, int t, int E, int topk, int32_t* sel,
@@ -104,19 +105,25 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, in
         const int e = lane + 64 * i;
         k[i] = route_key(v[i], e) & (0ull - (uint64_t)(e < E));  // missing experts: key 0 (no branch)
     }
-    unsigned avail = (1u << PER) - 1u;  // bit i: key i not yet selected (missing experts hold key 0, never selected)
-    uint64_t mine = 0;                   // lane r keeps round r's key
-    for (int r = 0; r < topk; r++) {
-        // the lane's largest available key (selects over the PER keys, no branches)
-        uint64_t lk = 0;
-        int li = 0;
+    // bitonic sort, descending (PER is a power of two)
 #pragma unroll
-        for (int i = 0; i < PER; i++) {
-            const bool better = (((avail >> i) & 1u) != 0u) & (k[i] > lk);  // no short circuit
-            lk = better ? k[i] : lk;
-            li = better ? i : li;
-        }
-        uint64_t bk = lk;
+    for (int size = 2; size <= PER; size <<= 1)
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1)
+#pragma unroll
+            for (int i = 0; i < PER; i++) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const bool swap = desc ? k[j] > k[i] : k[i] > k[j];
+                    const uint64_t a = k[i], b = k[j];
+                    k[i] = swap ? b : a;
+                    k[j] = swap ? a : b;
+                }
+            }
+    uint64_t mine = 0;  // lane r keeps round r's key
+    for (int r = 0; r < topk; r++) {
+        uint64_t bk = k[0];
         route_step<0xB1>(bk);        // quad_perm [1,0,3,2]
         route_step<0x4E>(bk);        // quad_perm [2,3,0,1]
         route_step<0x124>(bk);       // row_ror:4
@@ -125,7 +132,13 @@ __device__ __forceinline__ void route_token(const float* __restrict__ logits, in
         route_step<0x143, 0xC>(bk);  // row_bcast:31 into rows 2 and 3: lane 63 holds the wave's largest
         const uint64_t best = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(bk >> 32), 63) << 32) |
                               (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bk, 63);
-        avail &= ~((lk == best ? 1u : 0u) << li);
+        // the winning lane's shift as bit-field merges with an all-ones / zero mask (the empty asm keeps the compiler
+        // from rewriting the shift into a register-indexed select over every key)
+        uint64_t wm = 0ull - (uint64_t)(k[0] == best);
+        asm volatile("" : "+v"(wm));
+#pragma unroll
+        for (int i = 0; i + 1 < PER; i++) k[i] = (k[i + 1] & wm) | (k[i] & ~wm);
+        k[PER - 1] &= ~wm;
         mine = lane == r ? best : mine;
     }
     // weights exp(l_k - l_max) / sum, the sum in k order
