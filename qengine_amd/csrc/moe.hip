@@ -611,6 +611,45 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
     }
 }
 
+// T <= kDecRouteFused, T * topk <= 64 (followed by the fused down + combine): routing and gate_up in one launch.
+// Every block routes the T tokens itself (route_token into LDS, one token per wave), so no launch waits for a routing
+// kernel and nothing is segmented: block (pair p = t * topk + k, record g * 16 + tile) multiplies expert sel[p]'s
+// tile by token t's row into act slot p. Block (0, 0) stores sel, w and inv (inv[p] = p) for the down + combine.
+// Same arithmetic as moe_dec_gate_up_kernel with one row per job.
+template <int PER, int NG>
+__global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_route_gate_up_kernel(
+    const float* __restrict__ logits, int T, int E, int topk, const char* __restrict__ recs, MoeShape sh,
+    const uint16_t* __restrict__ x, int32_t* __restrict__ sel, float* __restrict__ w, int32_t* __restrict__ inv,
+    uint16_t* __restrict__ act) {
+    extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
+    __shared__ int32_t ssel[kDecRouteFused * 16];
+    __shared__ float sw[kDecRouteFused * 16];
+    const int S = blockDim.x >> 6, wv = threadIdx.x >> 6;
+    for (int tt = wv; tt < T; tt += S) route_token<PER>(logits, tt, E, topk, ssel + tt * topk, sw + tt * topk);
+    __syncthreads();
+    const int p = blockIdx.x, t = p / topk;
+    if (blockIdx.x == 0 && blockIdx.y == 0) {
+        for (int q = threadIdx.x; q < T * topk; q += blockDim.x) {
+            sel[q] = ssel[q];
+            w[q] = sw[q];
+            inv[q] = q;
+        }
+    }
+    const int e = ssel[p];
+    const int g = blockIdx.y >> 4, tile = blockIdx.y & 15;
+    const int G = sh.H >> 7, gb = wv * NG;
+    const char* rp = rec_ptr(recs, sh, e, g);
+    const uint4* qp = reinterpret_cast<const uint4*>(rp) + ((size_t)tile * (sh.H >> 6) + 2 * gb) * 32;
+    const uint16_t* sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q) + ((size_t)tile * G + gb) * 16;
+    const uint32_t* xw[1] = {reinterpret_cast<const uint32_t*>(x + (size_t)t * sh.H) + gb * 64};
+    const float* red = mfma_dec_tile<1, NG>(lds, qp, sp, xw, 1, 64, 8);
+    if (threadIdx.x < 8) {
+        const int gg = threadIdx.x;
+        const float v = silu_f32(rsum<1>(red, S, 0, gg)) * rsum<1>(red, S, 0, gg + 8) * sw[p];
+        act[(size_t)p * sh.I + g * 128 + tile * 8 + gg] = f32_to_bf16(v);
+    }
+}
+
 // down: block = one wave = (job, 16-row tile of H), all NGRP records of the expert (K = I = 128 per record): the
 // wave streams NGRP KB and no K slice is reduced across waves
 template <int MT, int NGRP>
@@ -872,6 +911,26 @@ size_t qe_moe_record_bytes(int H, int I) { return moe_shape(1, 1, H, I).rec * (s
 
 namespace {
 
+// the fused decode down + combine (T * topk <= 64, I / 128 <= 8)
+void launch_down_combine(const char* recs, const MoeShape& sh, const uint16_t* act, const int32_t* sel,
+                         const int32_t* inv, int T, int topk, int H, void* out, int flags, hipStream_t st) {
+#define QE_DOWN_COMBINE(NGRP_)                                                                                 \
+    moe_dec_down_combine_kernel<NGRP_><<<dim3(H / 16, T), 64 * topk, gemv_lds_bytes<1, NGRP_, true>(topk), st>>>( \
+        recs, sh, act, sel, inv, topk, out, (flags & QE_OUT_BF16) ? 1 : 0)
+    switch (sh.ngrp) {
+        case 1: QE_DOWN_COMBINE(1); break;
+        case 2: QE_DOWN_COMBINE(2); break;
+        case 3: QE_DOWN_COMBINE(3); break;
+        case 4: QE_DOWN_COMBINE(4); break;
+        case 5: QE_DOWN_COMBINE(5); break;
+        case 6: QE_DOWN_COMBINE(6); break;
+        case 7: QE_DOWN_COMBINE(7); break;
+        default: QE_DOWN_COMBINE(8); break;
+    }
+#undef QE_DOWN_COMBINE
+    HIP_CHECK(hipGetLastError());
+}
+
 // the layer on a workspace of moe_ws(T, ...).bytes at `workspace` (checked by the callers)
 void moe_run(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
              void* out, int flags, void* workspace, hipStream_t st) {
@@ -884,6 +943,35 @@ void moe_run(const float* logits, const uint16_t* x, const void* records, int T,
     const int chunk = decode ? kDecRows : kMoePfRows;
     const int mj = max_jobs(T, E, topk, chunk);
 
+    // a few decode tokens: routing + gate_up in one launch, then the fused down + combine (two launches in all)
+    if (T <= kDecRouteFused && T * topk <= 64 && sh.ngrp <= 8) {
+        const int G = H / 128, per = (E + 63) / 64;
+        const int ng = (G % 2 == 0 && G / 2 <= kMaxWaves) ? 2 : (G % 4 == 0 && G / 4 <= kMaxWaves) ? 4 : 8;
+        CHECK(G % ng == 0 && G / ng <= kMaxWaves, "moe decode H %d", H);
+        const size_t lds = ng == 2 ? gemv_lds_bytes<1, 2, true>(G / 2)
+                           : ng == 4 ? gemv_lds_bytes<1, 4, true>(G / 4)
+                                     : gemv_lds_bytes<1, 8, true>(G / 8);
+        const dim3 grid((unsigned)(T * topk), (unsigned)(sh.ngrp * 16)), block((unsigned)(64 * (G / ng)));
+#define QE_RGU(PER_, NG_)                                                                                     \
+    moe_dec_route_gate_up_kernel<PER_, NG_><<<grid, block, lds, st>>>(logits, T, E, topk, recs, sh, x, ws.sel, ws.w, \
+                                                                       ws.inv, ws.act)
+#define QE_RGU_NG(PER_)                      \
+    do {                                     \
+        if (ng == 2) QE_RGU(PER_, 2);        \
+        else if (ng == 4) QE_RGU(PER_, 4);   \
+        else QE_RGU(PER_, 8);                \
+    } while (0)
+        if (per <= 1) QE_RGU_NG(1);
+        else if (per <= 2) QE_RGU_NG(2);
+        else if (per <= 4) QE_RGU_NG(4);
+        else if (per <= 8) QE_RGU_NG(8);
+        else QE_RGU_NG(16);
+#undef QE_RGU_NG
+#undef QE_RGU
+        HIP_CHECK(hipGetLastError());
+        launch_down_combine(recs, sh, ws.act, ws.sel, ws.inv, T, topk, H, out, flags, st);
+        return;
+    }
     if (T > kDecTokens) launch_route(logits, T, E, topk, ws.sel, ws.w, st);
     if (T <= kDecTokens) {
         launch_route_segment(logits, T, E, topk, chunk, ws.sel, ws.w, ws.off, ws.slot_pair, ws.slot_tok, ws.slot_w,
@@ -922,21 +1010,7 @@ void moe_run(const float* logits, const uint16_t* x, const void* records, int T,
                 recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
         HIP_CHECK(hipGetLastError());
         if (few && sh.ngrp <= 8) {
-#define QE_DOWN_COMBINE(NGRP_)                                                                                 \
-    moe_dec_down_combine_kernel<NGRP_><<<dim3(H / 16, T), 64 * topk, gemv_lds_bytes<1, NGRP_, true>(topk), st>>>( \
-        recs, sh, ws.act, ws.sel, ws.inv, topk, out, (flags & QE_OUT_BF16) ? 1 : 0)
-            switch (sh.ngrp) {
-                case 1: QE_DOWN_COMBINE(1); break;
-                case 2: QE_DOWN_COMBINE(2); break;
-                case 3: QE_DOWN_COMBINE(3); break;
-                case 4: QE_DOWN_COMBINE(4); break;
-                case 5: QE_DOWN_COMBINE(5); break;
-                case 6: QE_DOWN_COMBINE(6); break;
-                case 7: QE_DOWN_COMBINE(7); break;
-                default: QE_DOWN_COMBINE(8); break;
-            }
-#undef QE_DOWN_COMBINE
-            HIP_CHECK(hipGetLastError());
+            launch_down_combine(recs, sh, ws.act, ws.sel, ws.inv, T, topk, H, out, flags, st);
             return;
         }
 #define QE_DOWN(NGRP_)                                                                                         \
