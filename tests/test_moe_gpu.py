@@ -131,6 +131,24 @@ def pipeline_ref(lg, xh, gq, gs, dq, ds, topk, H, I):
     return bf(out)
 
 
+def test_moe_decode_fused_route_gate_up_bit_exact(dev):
+    """T <= 4 routes inside the gate_up blocks (no segmentation: slot = pair), T = 5 routes, segments and runs the
+    grouped gate_up; with T * topk <= 64 both take the same gate_up K slicing and the fused down + combine, and every
+    value is per (token, k), so the first 4 tokens of a 5-token call equal a 4-token call bit for bit"""
+    E, topk, H, I = 64, 10, 2048, 512
+    gq, gs, dq, ds = synth.moe_host(E, H, I, seed=41)
+    moe = ops.MoE.pack(synth.to_dev(gq), synth.to_dev(gs, torch.float16), synth.to_dev(dq),
+                       synth.to_dev(ds, torch.float16), topk=topk)
+    lg = torch.from_numpy(synth.logits_host(5, E, seed=42)).to(dev)
+    x = synth.to_dev(synth.x_host(5, H, seed=43))
+    for out_bf16 in (True, False):
+        y5 = moe(lg, x, out_bf16=out_bf16)
+        y4 = moe(lg[:4].contiguous(), x[:4].contiguous(), out_bf16=out_bf16)
+        torch.cuda.synchronize()
+        iv = torch.int16 if out_bf16 else torch.int32
+        assert torch.equal(y4.view(iv), y5[:4].contiguous().view(iv)), out_bf16
+
+
 @pytest.mark.parametrize("T,E", [(300, 8), (700, 4)])
 def test_moe_layer_multi_job(dev, T, E):
     """prefill experts with more rows than one job (128 rows): ~150 and 700 rows per expert. Against the layer's own
