@@ -19,6 +19,7 @@
 // (job, 512 weight rows), the weights dequantized in registers (moe_pf.hip): every expert's weights are read once
 // per 128 of its rows.
 #include "gemv_impl.hpp"
+#include "mfma_tile.hpp"
 #include "../../include/qe_kernels.h"
 
 #include <mutex>
@@ -491,12 +492,13 @@ __global__ void __launch_bounds__(kSegThreads) moe_seg_place_kernel(const int32_
 // ------------------------------------------------------------------ decode grouped GEMVs (gemv_tile)
 constexpr int kDecRows = 2;  // rows per decode job
 
-// Matrix-core decode tile (W4, fp16 scales, slices of NG <= 8 groups, MT <= 4 gathered activation rows): the
-// arithmetic of the skinny GEMM kernel (skinny.hip) behind gemv_tile's interface. Lane 16 q + i holds A row i of the
-// 16-row tile (its half of the records (g = i % 8, t = q): t = (w >> 4 (i / 8)) & 0x0F0F0F0F, byte permutes with 0x43
-// give the bf16 pairs 128 + u) and B column i = activation row i (class-major staged activations, one ds_read_b128
-// per MFMA); the bias by one more MFMA with A = -136; acc += s * C per group. Activations, scales and every group's
-// records are loaded before any wait. Returns red in gemv_tile's layout [S][2][MT][16] (half 1 zero) for rsum().
+// Matrix-core decode tile (W4, fp16 scales, slices of NG <= 8 groups, MT <= 4 gathered activation rows) behind
+// gemv_tile's interface. Lane 16 q + i holds A row i of the 16-row tile (its half of the records (g = i % 8, t = q):
+// t = (w >> 4 (i / 8)) & 0x0F0F0F0F) and B column i = activation row i (class-major staged activations, one
+// ds_read_b128 per MFMA). The A values are the reference's weight operand bf16_rn((u - 8) s), s the row's group scale
+// (the prefill GEMMs' operand too, so a token gets the same weights at every T), accumulated across the groups by the
+// MFMAs in fp32. Activations, scales and every group's records are loaded before any wait. Returns red in gemv_tile's
+// layout [S][2][MT][16] (half 1 zero) for rsum().
 template <int MT, int NG>
 __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __restrict__ qp,
                                                const uint16_t* __restrict__ sp, const uint32_t* const* xw, int m,
@@ -545,12 +547,13 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
-    // 3. per group: 4 k steps of a weight MFMA and a bias MFMA, then the group scale
-    const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{0xC308C308u, 0xC308C308u, 0xC308C308u, 0xC308C308u});
+    // 3. per group: the row's scale, 4 k steps of one MFMA on the dequantized weights (pairs of bytes 0 / 2 and 1 / 3
+    //    of the nibble words: k, k + 1 and k + 8, k + 9 of the record's byte order)
     f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ii = 0; ii < NG; ii++) {
-        f32x4_v c = {0.f, 0.f, 0.f, 0.f};
+        const float sc = scale_to_f32<kScaleF16>(sl16[ii * 16 + i]);
+        const float bias = -8.f * sc;
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
             u32x4_v b = *reinterpret_cast<const u32x4_v*>(
@@ -559,16 +562,13 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
             const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
             const u32x4_v rec = wv[ii][mm >> 1];
             const int j0 = 2 * (mm & 1);
-            const uint32_t t0 = (rec[j0] >> sh) & kNib, t1 = (rec[j0 + 1] >> sh) & kNib;
-            const u32x4_v a = {bf16x2_b02(t0), bf16x2_b13(t0), bf16x2_b02(t1), bf16x2_b13(t1)};
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, c, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb, c, 0, 0, 0);
+            const uint32_t t0 = (rec[j0] >> sh) & qe_tile::nib_mask(), t1 = (rec[j0 + 1] >> sh) & qe_tile::nib_mask();
+            const u32x4_v a = {pack_bf16x2(fmaf(qe_tile::cvt_ubyte<0>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t0), sc, bias)),
+                               pack_bf16x2(fmaf(qe_tile::cvt_ubyte<1>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t0), sc, bias)),
+                               pack_bf16x2(fmaf(qe_tile::cvt_ubyte<0>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t1), sc, bias)),
+                               pack_bf16x2(fmaf(qe_tile::cvt_ubyte<1>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t1), sc, bias))};
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, acc, 0, 0, 0);
         }
-        const uint2 sv = *reinterpret_cast<const uint2*>(&sl16[ii * 16 + 4 * qg]);
-        acc[0] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.x & 0xffffu)), c[0], acc[0]);
-        acc[1] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.x >> 16)), c[1], acc[1]);
-        acc[2] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.y & 0xffffu)), c[2], acc[2]);
-        acc[3] = fmaf(scale_to_f32<kScaleF16>((uint16_t)(sv.y >> 16)), c[3], acc[3]);
     }
     // 4. lane (q, i < MT) holds rows 4 q .. 4 q + 3 of activation row i
     if (i < MT) {
@@ -669,13 +669,22 @@ __global__ void __launch_bounds__(64) moe_dec_down_kernel(
 #pragma unroll
     for (int r = 0; r < MT; r++)
         xw[r] = reinterpret_cast<const uint32_t*>(act + (size_t)(slot0 + (r < m ? r : 0)) * sh.I);
-    const float* red = NGRP <= 8 ? mfma_dec_tile<MT, NGRP <= 8 ? NGRP : 8>(lds, qp, sp, xw, m, sh.rec / 16, sh.rec / 4)
-                                  : gemv_tile<MT, kFmtW4, kScaleF16, NGRP, true>(lds, qp, sp, xw, m, NGRP, kScaleF16,
-                                                                                 sh.rec / 16, sh.rec / 4);
-    for (int idx = threadIdx.x; idx < m * 16; idx += blockDim.x) {
-        const int r = idx >> 4, rr = idx & 15;
-        slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_bf16(rsum<MT>(red, 1, r, rr));
+    // NGRP = 16 (I = 2048): two tiles of 8 groups, each thread keeping its sums of the first (m * 16 <= 64 outputs,
+    // one per thread) before the second reuses the LDS
+    constexpr int NH = NGRP <= 8 ? NGRP : 8;
+    static_assert(NGRP <= 8 || NGRP == 16, "moe decode down: I / 128 in 1..8 or 16");
+    const int idx = threadIdx.x, r = idx >> 4, rr = idx & 15;
+    const float* red = mfma_dec_tile<MT, NH>(lds, qp, sp, xw, m, sh.rec / 16, sh.rec / 4);
+    float v = idx < m * 16 ? rsum<MT>(red, 1, r, rr) : 0.f;
+    if constexpr (NGRP == 16) {
+        __syncthreads();
+        const uint32_t* xw2[MT];
+#pragma unroll
+        for (int q = 0; q < MT; q++) xw2[q] = xw[q] + 8 * 64;  // activations of groups 8..15
+        red = mfma_dec_tile<MT, 8>(lds, qp + 8 * (sh.rec / 16), sp + 8 * (sh.rec / 2), xw2, m, sh.rec / 16, sh.rec / 4);
+        v += idx < m * 16 ? rsum<MT>(red, 1, r, rr) : 0.f;
     }
+    if (idx < m * 16) slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_bf16(v);
 }
 
 // T * topk <= 64 (decode, few pairs), I / 128 <= 8: the down GEMV and the combine in one launch. Block (16-row tile
