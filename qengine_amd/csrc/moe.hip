@@ -549,11 +549,14 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
 
     // 3. per group: the row's scale, 4 k steps of one MFMA on the dequantized weights (pairs of bytes 0 / 2 and 1 / 3
     //    of the nibble words: k, k + 1 and k + 8, k + 9 of the record's byte order)
+    // rows g + 8 (lanes i >= 8) keep their high nibbles in place (16 u) and take s / 16: the same fma, no shift
+    const uint32_t lmask = sh ? 0xF0F0F0F0u : qe_tile::nib_mask();
+    const float lscale = sh ? 0.0625f : 1.f;
     f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ii = 0; ii < NG; ii++) {
-        const float sc = scale_to_f32<kScaleF16>(sl16[ii * 16 + i]);
-        const float bias = -8.f * sc;
+        const float s_row = scale_to_f32<kScaleF16>(sl16[ii * 16 + i]);
+        const float sc = s_row * lscale, bias = -8.f * s_row;
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
             u32x4_v b = *reinterpret_cast<const u32x4_v*>(
@@ -562,7 +565,7 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
             const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
             const u32x4_v rec = wv[ii][mm >> 1];
             const int j0 = 2 * (mm & 1);
-            const uint32_t t0 = (rec[j0] >> sh) & qe_tile::nib_mask(), t1 = (rec[j0 + 1] >> sh) & qe_tile::nib_mask();
+            const uint32_t t0 = rec[j0] & lmask, t1 = rec[j0 + 1] & lmask;
             const u32x4_v a = {pack_bf16x2(fmaf(qe_tile::cvt_ubyte<0>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t0), sc, bias)),
                                pack_bf16x2(fmaf(qe_tile::cvt_ubyte<1>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t0), sc, bias)),
                                pack_bf16x2(fmaf(qe_tile::cvt_ubyte<0>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t1), sc, bias)),
