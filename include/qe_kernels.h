@@ -231,6 +231,20 @@ void qe_gemv_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x
 void qe_gemm_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                    int flags, void* stream);
 
+/* W8A8 row GEMM of a W8 matrix, the reference's prefill numerics for INT8 matrices (k_x_to_r8 + k_rows_qt,
+ * src/flash/flash_pfq.cuh:473-651): the activations are quantized per (row, 128-k group), sx = amax / 127 with the
+ * two lowest mantissa bits cleared (1 for a zero group), q = rn(x * fp32(1 / sx)); each group's int8 x int8 dot
+ * product is summed exactly in int32 and y = fma(rn(float(sum) * sx), sw, y) over the groups in k order, the
+ * reference's arithmetic to the bit. Group-128 or per-channel (QE_W8_PER_CHANNEL) scales, QE_SCALE_F16,
+ * QE_OUT_BF16; any m >= 1, k % 128 == 0. The pre-pass buffer (m * (k + k / 8) bytes) is the one of qe_gemm_w4_i8
+ * (qe_gemm_i8_reserve sizes it). qe_rows8 is the reference's dispatch, Worker::rows8 (src/flash/flash.cu:369-411):
+ * W8A8 for m >= 64, k <= 4096 and ldx % 8 == 0, else the W8A16 GEMM of qe_gemm_w8_ex for 16-byte aligned rows and
+ * the W8A16 GEMV of qe_gemv_w8_ex (blocks of 16 rows) otherwise; y fp32. */
+void qe_gemm_w8a8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                     int flags, void* stream);
+void qe_rows8(const void* q, const void* s, int n, int k, int flags, const uint16_t* x, int ldx, float* y, int ldy,
+              int m, void* stream);
+
 /* ---- MoE grouped INT4 expert layer (one GPU, every expert local). No reference C-ABI exists for it: it replaces
  * Worker::moe (reference src/flash/flash.cu:4842-5020) and its kernels k_topk_rows / k_jobs_pf / k_moe_* with the
  * expert weights in the Flash-Next group-record format (src/flash/flash.h:203-218, fp16 scales): record (e, g) =

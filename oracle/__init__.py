@@ -32,6 +32,9 @@ Parity pins (each function is checked against something other than itself in tes
   x_to_i8           the reference test's own torch emulation (tests/test_gemm_i8.py:52-61 quant_emul) restated in
                     torch, known answers (zero group, amax = 127 * 2^e)
   gemm_i8           float64 product of the dequantized int8 operands: brute force on tiny shapes
+  rows_w8a8         brute force on tiny shapes in exact rational arithmetic (integer sums, one float32 rounding
+                    of the product, one of the fused multiply-add, ties to even, written independently of libm's
+                    fmaf), and the float64 product exactly on integer-valued inputs
 """
 import ctypes
 import os
@@ -149,6 +152,23 @@ def matmul_bf16(x, w, nthreads=0):
     n = w.shape[0]
     y = np.empty((m, n), np.float32)
     lib().or_matmul_bf16(_p(x), _p(w), m, n, k, _p(y), int(nthreads))
+    return y
+
+
+def rows_w8a8(xq, sx, w, sw, per_channel, nthreads=0):
+    """the reference's W8A8 row GEMM (k_rows_qt, src/flash/flash_pfq.cuh:520-651): xq int8 [m][k] in natural k
+    order and sx float32 [m][k/128] from x_to_i8(x, 128) (k_x_to_r8's arithmetic), w int8 [n][k], sw float32
+    [n][k/128] (per_channel: [n]) -> fp32 [m][n], per 128-k group in k order y = fma(rn(float(sum) sx), sw, y)"""
+    xq = _c(xq, np.int8)
+    sx = _c(sx, np.float32)
+    w = _c(w, np.int8)
+    sw = _c(sw, np.float32)
+    m, k = xq.shape
+    n = w.shape[0]
+    assert k % 128 == 0 and w.shape[1] == k and sx.shape == (m, k // 128)
+    assert sw.shape == ((n,) if per_channel else (n, k // 128))
+    y = np.empty((m, n), np.float32)
+    lib().or_rows_w8a8(_p(xq), _p(sx), _p(w), _p(sw), int(bool(per_channel)), m, n, k, _p(y), int(nthreads))
     return y
 
 

@@ -295,5 +295,36 @@ void or_moe_segment(const int32_t* sel, int T, int E, int topk, int32_t* cnt, in
     free(fill);
 }
 
+/* W8A8 row GEMM (reference k_rows_qt, src/flash/flash_pfq.cuh:520-651; the activations quantized by the caller as
+ * k_x_to_r8, :473-518, does): per (token t, row r) and 128-k group g in k order, sum = the exact integer dot product
+ * of xq[t] and w[r] over the group, p = rn_f32((float)sum * sx[t][g]) and y = fmaf(p, sw[r][g], y). The reference
+ * computes p as fma(M + sum, sx, -M sx) with M = 1.5 * 2^23 (an int32 accumulator started at M's bit pattern):
+ * M sx is exact (sx has 22 significant bits) and (M + sum) sx - M sx = sum sx before the one rounding, so p is the
+ * same. sw: [n][k/128] floats, or [n] with per_channel (the same scale in every group). nthreads <= 0: all. */
+void or_rows_w8a8(const int8_t* xq, const float* sx, const int8_t* w, const float* sw, int per_channel, int m, int n,
+                  int k, float* y, int nthreads) {
+#ifdef _OPENMP
+    if (nthreads > 0) omp_set_num_threads(nthreads);
+#else
+    (void)nthreads;
+#endif
+    const int ng = k / 128;
+#pragma omp parallel for schedule(static)
+    for (int r = 0; r < n; r++) {
+        const int8_t* wr = w + (size_t)r * k;
+        for (int t = 0; t < m; t++) {
+            const int8_t* xr = xq + (size_t)t * k;
+            float acc = 0.f;
+            for (int g = 0; g < ng; g++) {
+                int32_t sum = 0;
+                for (int c = 128 * g; c < 128 * g + 128; c++) sum += (int32_t)xr[c] * (int32_t)wr[c];
+                const float p = (float)sum * sx[(size_t)t * ng + g];
+                acc = fmaf(p, per_channel ? sw[r] : sw[(size_t)r * ng + g], acc);
+            }
+            y[(size_t)t * n + r] = acc;
+        }
+    }
+}
+
 /* silu(a) * b in fp32 */
 float or_silu_mul(float a, float b) { return a / (1.f + expf(-a)) * b; }

@@ -6,6 +6,7 @@
 #include "gemm_tune.hpp"
 #include "../../include/qe_kernels.h"
 
+#include <algorithm>
 #include <atomic>
 
 [[noreturn]] void qe_fatal_check() {
@@ -304,6 +305,32 @@ void qe_gemm_w8_ex(const void* q, const void* s, int n, int k, const uint16_t* x
     const bool pc = (flags & QE_W8_PER_CHANNEL) != 0;
     gemm_w8(mk_w8(q, s, n, k, pc, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y, ldy, t,
             (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+void qe_gemm_w8a8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int m,
+                     int flags, void* st) {
+    const bool pc = (flags & QE_W8_PER_CHANNEL) != 0;
+    gemm_w8a8(mk_w8(q, s, n, k, pc, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16), x, ldx, y, ldy, m,
+              (flags & QE_OUT_BF16) != 0, as_stream(st));
+}
+
+// Worker::rows8 (reference src/flash/flash.cu:369-411): W8A8 for m >= 64 rows, k <= 4096 (the reference pre-pass's
+// row staging limit, RQ_KMAX) and 8-element row strides, else its gemv_w8_rows (flash.cu:351-366): the W8A16 row GEMM
+// for 16-byte aligned rows, else the W8A16 GEMV over blocks of up to 16 rows; fp32 out
+void qe_rows8(const void* q, const void* s, int n, int k, int flags, const uint16_t* x, int ldx, float* y, int ldy,
+              int m, void* st) {
+    const bool pc = (flags & QE_W8_PER_CHANNEL) != 0;
+    const W8 w = mk_w8(q, s, n, k, pc, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16);
+    CHECK(m >= 1, "rows8: m = %d", m);
+    if (m >= 64 && k <= 4096 && ldx % 8 == 0) {
+        gemm_w8a8(w, x, ldx, y, ldy, m, false, as_stream(st));
+    } else if (ldx % 8 == 0 && ((uintptr_t)x & 15) == 0) {
+        gemm_w8(w, x, ldx, y, ldy, m, false, as_stream(st));
+    } else {
+        for (int r0 = 0; r0 < m; r0 += kMaxGemvRows)
+            gemv_w8(w, x + (size_t)r0 * ldx, ldx, y + (size_t)r0 * ldy, ldy, std::min(kMaxGemvRows, m - r0), false,
+                    as_stream(st));
+    }
 }
 
 }  // extern "C"

@@ -96,20 +96,90 @@ __global__ void __launch_bounds__(256) x_to_i8_kernel(const uint16_t* __restrict
     if (j % L == 0) sx[(size_t)t * (K / G) + (16 * j) / G] = sc;
 }
 
+// W8A8 pre-pass (reference k_x_to_r8, src/flash/flash_pfq.cuh:473-518, the activations of the row GEMM k_rows_qt):
+// thread = one 32-k block of one token; the same per-(token, 128-k group) scale and rounding as x_to_i8_kernel (the
+// 4 lanes of a group share the amax). Byte p of the block holds k = k_perm8(p): a W8 record lane holds a row's bytes
+// as pairs (k, k + 1) at k = 16 kb + 8 half + 2 t (record dword 2 kb + half, record lane 4 g + t), and the GEMM
+// takes two consecutive record lanes per 16-byte operand, so both operands pair matching k
+__device__ __forceinline__ int k_perm8(int p) { return 16 * ((p >> 2) & 1) + 8 * ((p >> 1) & 1) + 2 * (p >> 3) + (p & 1); }
+
+template <bool VEC>
+__global__ void __launch_bounds__(256) x_to_r8_kernel(const uint16_t* __restrict__ x, int ldx, int K, int T,
+                                                      int8_t* __restrict__ xq, float* __restrict__ sx) {
+    const int jpr = K / 32;  // blocks per row, a multiple of 4: a group never straddles two tokens
+    const long id = (long)blockIdx.x * 256 + threadIdx.x;
+    const bool live = id < (long)T * jpr;
+    const int t = live ? (int)(id / jpr) : 0, j = live ? (int)(id % jpr) : 0;
+    const uint16_t* r = x + (size_t)t * ldx + 32 * j;
+    float v[32];
+    if constexpr (VEC) {
+#pragma unroll
+        for (int h = 0; h < 4; h++) {
+            const u32x4_v a = live ? *reinterpret_cast<const u32x4_v*>(r + 8 * h) : u32x4_v{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t wa = a[i];
+                v[8 * h + 2 * i] = __builtin_bit_cast(float, wa << 16);
+                v[8 * h + 2 * i + 1] = __builtin_bit_cast(float, wa & 0xFFFF0000u);
+            }
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = live ? bf16_to_f32(r[i]) : 0.f;
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) mx = fmaxf(mx, fabsf(v[i]));
+    mx = fmaxf(mx, __shfl_xor(mx, 1));
+    mx = fmaxf(mx, __shfl_xor(mx, 2));
+    if (!live) return;
+    const float sc = mx > 0.f ? __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, mx / 127.f) & ~3u) : 1.f;
+    const float inv = mx > 0.f ? 1.f / sc : 0.f;
+    uint32_t o[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+        uint32_t wv = 0;
+#pragma unroll
+        for (int bb = 0; bb < 4; bb++) {
+            const float qf = fminf(fmaxf(__builtin_rintf(v[k_perm8(4 * u + bb)] * inv), -127.f), 127.f);
+            wv |= ((uint32_t)(int)qf & 0xFFu) << (8 * bb);
+        }
+        o[u] = wv;
+    }
+    u32x4_v* dst = reinterpret_cast<u32x4_v*>(xq + (size_t)t * K + 32 * j);
+    dst[0] = u32x4_v{o[0], o[1], o[2], o[3]};
+    dst[1] = u32x4_v{o[4], o[5], o[6], o[7]};
+    if ((j & 3) == 0) sx[(size_t)t * (K / 128) + (j >> 2)] = sc;
+}
+
 // 4 nibbles u (one per byte) -> 4 signed bytes u - 8
 __device__ __forceinline__ uint32_t nib_s8(uint32_t u) { return ((u | 0x80808080u) - 0x08080808u) ^ 0x80808080u; }
 
-// Q8: the weights are the Q8 layout's signed bytes (W8A8 of an INT8 matrix, reference gemm_q8_dispatch,
-// gemm.cu:4516): a row's 16-k block is word 2 s + h of the 4 records (lanes 4 g + t, t = 0..3) of its 32-k slab, in
-// the same byte order as a W4 word, so the W tile is gathered straight into LDS by 4-byte DMAs (one dword of a record
-// per lane, no unpack) one step ahead, like the activations
-template <int G, int SDT, int OUT, bool Q8>
+// Weight formats (WF):
+// kW4: W4 records, raw chunks by DMA two steps ahead, unpacked to signed int8 between the MFMA rows.
+// kQ8: the weights are the Q8 layout's signed bytes (W8A8 of an INT8 matrix, reference gemm_q8_dispatch,
+//   gemm.cu:4516): a row's 16-k block is word 2 s + h of the 4 records (lanes 4 g + t, t = 0..3) of its 32-k slab, in
+//   the same byte order as a W4 word, so the W tile is gathered straight into LDS by 4-byte DMAs (one dword of a
+//   record per lane, no unpack) one step ahead, like the activations.
+// kW8: the W8 layout's signed bytes (the reference's W8A8 row GEMM k_rows_qt, src/flash/flash_pfq.cuh:520-651, with
+//   group-128 or per-channel (PC) weight scales). Every record dword holds two k of row g and the same two of row
+//   g + 8, so the tile is stored as pair lines (rows g and g + 8 of a 16-row tile: the 4 consecutive records 4 g + t of
+//   each 32-k block, 256 B per step) by 16-byte DMAs one step ahead, and the A operands of both rows come out of one
+//   line read by 4 byte permutes each: the wave's two 32-row MFMA tiles are the rows g and the rows g + 8 of its four
+//   16-row tiles. The activations arrive in the matching order (x_to_r8_kernel). G = 128, so every step flushes once:
+//   acc = fma(rn(float(sum) sx), sw, acc), the reference's per-stage arithmetic (its magic-number accumulator gives
+//   the same rn(sum sx)), so the result is fixed to the bit.
+enum Wf : int { kW4 = 0, kQ8 = 1, kW8 = 2 };
+
+template <int G, int SDT, int OUT, int WF, bool PC>
 __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                       int N, int K, const int8_t* __restrict__ xq,
                                                       const float* __restrict__ sxg, int T, void* __restrict__ c,
                                                       int ldc, int nbn, int ntiles) {
     constexpr int NGS = BK / G;   // activation groups per step
     constexpr int KPG = G / 32;   // k32 MFMA steps per activation group
+    static_assert(WF != kW8 || G == 128, "W8A8: activation groups of 128");
+    static_assert(!PC || WF == kW8, "per-channel scales: W8 only");
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -154,10 +224,23 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
             dma4(q32 + rec * 4 + 2 * (cl & 1) + h, lds32 + wtile + u * 256);
         }
     };
+    // W8 tile of step kt as BN / 2 pair lines (line 8 (local tile) + g: rows g and g + 8), 256 B each: the records
+    // (32-k block kk, lane 4 g + t) of the step, logical chunk 4 kk + t stored at chunk position (4 kk + t) ^ g (the
+    // eight lines g of one read hit distinct banks); four 1-KB wave instructions (four lines each) per wave
+    auto dma_w8 = [&](int kt, unsigned wtile) {
+#pragma unroll
+        for (int i = 0; i < BN / 64; i++) {
+            const int u = wave * (BN / 64) + i, line = 4 * u + (lane >> 4), g = line & 7;
+            const int cl = (lane & 15) ^ g;
+            const int tl = min((n0 >> 4) + (line >> 3), ntile_last);
+            dma16(q + ((size_t)tl * (K >> 5) + kt * 4 + (cl >> 2)) * 32 + 4 * g + (cl & 3), lds32 + wtile + u * 1024);
+        }
+    };
     auto dma_sc = [&](int grp, unsigned sc) {
         if (wave < BN / 128) {
             const int tl = min((n0 >> 4) + 8 * wave + (lane >> 3), ntile_last);
-            dma4(s + ((size_t)tl * G128 + grp) * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
+            if constexpr (PC) dma4(s + (size_t)tl * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
+            else dma4(s + ((size_t)tl * G128 + grp) * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
         }
     };
     // activation scales of the step: [BM tokens][NGS] floats, 4 bytes per lane
@@ -174,6 +257,10 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
 
     constexpr unsigned kRawOff = 2 * kStage, kScOff = kRawOff + 2 * kRaw, kSxOff = kScOff + 2 * kSc;
     const int wm = wave >> 2, wn = wave & 3;
+    // first of the 4 consecutive weight rows (block-local) of register quad rq of MFMA tile bb, lanes l < 32 (+4 for
+    // l >= 32): kW8 tiles bb hold the rows g + 8 bb of the wave's four 16-row tiles, the others 32 consecutive rows
+    static_assert(WNT == 2, "kW8: the two row halves of four 16-row tiles");
+    auto wrow = [&](int bb, int rq) { return WF == kW8 ? (4 * wn + rq) * 16 + 8 * bb : wn * 32 * WNT + bb * 32 + 8 * rq; };
     f32x16_v acc[WMT][WNT];
     i32x16_v dsum[WMT][WNT];
 #pragma unroll
@@ -208,8 +295,10 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
     };
 
     dma_x(0, 0);
-    if constexpr (Q8) {
+    if constexpr (WF == kQ8) {
         dma_wq8(0, BM * BK);
+    } else if constexpr (WF == kW8) {
+        dma_w8(0, BM * BK);
     } else {
         dma_w4(0, kRawOff);
         if (KT > 1) dma_w4(1, kRawOff + kRaw);
@@ -217,7 +306,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
     dma_sc(0, kScOff);
     dma_sx(0, kSxOff);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
-    if constexpr (!Q8) {
+    if constexpr (WF == kW4) {
         read_words(lds + kRawOff);
 #pragma unroll
         for (int ch = 0; ch < 2; ch++)
@@ -236,26 +325,49 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         char* wnext = lds + ((kt + 1) & 1) * kStage + BM * BK;
         if (MORE) {
             dma_x(kt + 1, ((kt + 1) & 1) * kStage);
-            if constexpr (Q8) dma_wq8(kt + 1, ((kt + 1) & 1) * kStage + BM * BK);
+            if constexpr (WF == kQ8) dma_wq8(kt + 1, ((kt + 1) & 1) * kStage + BM * BK);
+            if constexpr (WF == kW8) dma_w8(kt + 1, ((kt + 1) & 1) * kStage + BM * BK);
             dma_sc(kt + 1, kScOff + ((kt + 1) & 1) * kSc);
             dma_sx(kt + 1, kSxOff + ((kt + 1) & 1) * kSx);
         }
-        if constexpr (!Q8) {
+        if constexpr (WF == kW4) {
             if (kt + 2 < KT) dma_w4(kt + 2, kRawOff + (kt & 1) * kRaw);
         }
         const char* xt = lds + (kt & 1) * kStage;
         const char* wt = xt + BM * BK;
         i32x4_v af[2][WMT], bfr[2][WNT];  // af: X (B operand), bfr: W (A operand)
+        i32x4_v wraw[2][2];                // kW8: the two records (t = 2 h, 2 h + 1) of the lane's pair line
         auto read_frags = [&](int ks, int buf) {
 #pragma unroll
             for (int a = 0; a < WMT; a++)
                 af[buf][a] = *reinterpret_cast<const i32x4_v*>(xt + lane_off[ks] + (wm * 32 * WMT + a * 32) * 128);
+            if constexpr (WF == kW8) {
+                // pair line wn * 32 + l % 32 (tile l % 32 / 8 of the wave's four, g = l % 8), records 2 h, 2 h + 1
+                const char* ln = wt + (wn * 32 + (lane & 31)) * 256;
 #pragma unroll
-            for (int bb = 0; bb < WNT; bb++)
-                bfr[buf][bb] = *reinterpret_cast<const i32x4_v*>(wt + lane_off[ks] + (wn * 32 * WNT + bb * 32) * 128);
+                for (int e = 0; e < 2; e++)
+                    wraw[buf][e] = *reinterpret_cast<const i32x4_v*>(ln + (((4 * ks + 2 * (lane >> 5) + e) ^ (lane & 7)) << 4));
+            } else {
+#pragma unroll
+                for (int bb = 0; bb < WNT; bb++)
+                    bfr[buf][bb] = *reinterpret_cast<const i32x4_v*>(wt + lane_off[ks] + (wn * 32 * WNT + bb * 32) * 128);
+            }
+        };
+        // kW8: record dwords 2 kb + half hold (row g: k, k + 1; row g + 8: k, k + 1); operand dword 2 e + kb of the
+        // rows g (bb = 0) / g + 8 (bb = 1) = the low / high byte pairs of dwords 2 kb and 2 kb + 1 of record e
+        auto split_rows = [&](int buf) {
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+#pragma unroll
+                for (int kb = 0; kb < 2; kb++) {
+                    const uint32_t d0 = (uint32_t)wraw[buf][e][2 * kb], d1 = (uint32_t)wraw[buf][e][2 * kb + 1];
+                    bfr[buf][0][2 * e + kb] = (int)__builtin_amdgcn_perm(d1, d0, 0x05040100u);
+                    bfr[buf][1][2 * e + kb] = (int)__builtin_amdgcn_perm(d1, d0, 0x07060302u);
+                }
         };
         read_frags(0, 0);
-        if constexpr (MORE && !Q8) read_words(lds + kRawOff + ((kt + 1) & 1) * kRaw);
+        if constexpr (WF == kW8) split_rows(0);
+        if constexpr (MORE && WF == kW4) read_words(lds + kRawOff + ((kt + 1) & 1) * kRaw);
         // weight scales of this lane's rows (4 consecutive rows per register quad, one 8-byte read) for the step
         const uint16_t* scb = reinterpret_cast<const uint16_t*>(lds + kScOff + (kt & 1) * kSc);
         const float* sxb = reinterpret_cast<const float*>(lds + kSxOff + (kt & 1) * kSx);
@@ -264,7 +376,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         for (int bb = 0; bb < WNT; bb++)
 #pragma unroll
             for (int rq = 0; rq < 4; rq++) {
-                const uint2 sp = *reinterpret_cast<const uint2*>(scb + wn * 32 * WNT + bb * 32 + 8 * rq + 4 * (lane >> 5));
+                const uint2 sp = *reinterpret_cast<const uint2*>(scb + wrow(bb, rq) + 4 * (lane >> 5));
                 swf[bb][4 * rq] = scale_to_f32<SDT>((uint16_t)(sp.x & 0xFFFFu));
                 swf[bb][4 * rq + 1] = scale_to_f32<SDT>((uint16_t)(sp.x >> 16));
                 swf[bb][4 * rq + 2] = scale_to_f32<SDT>((uint16_t)(sp.y & 0xFFFFu));
@@ -282,12 +394,15 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
                     const i32x16_v cin = ks % KPG == 0 ? i32x16_v{} : dsum[a][bb];
                     dsum[a][bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfr[ks & 1][bb], af[ks & 1][a], cin, 0, 0, 0);
                 }
-                if constexpr (MORE && !Q8) {
+                if constexpr (MORE && WF == kW4) {
 #pragma unroll
                     for (int e = 0; e < 2; e++) {
                         const int un = 2 * slot + e;  // 16 units over 8 rows
                         unit(wnext, un >> 3, (un >> 2) & 1, un & 3);
                     }
+                }
+                if constexpr (WF == kW8) {
+                    if (a == 0 && ks + 1 < BK / 32) split_rows((ks + 1) & 1);
                 }
                 slot++;
                 __builtin_amdgcn_sched_barrier(0);
@@ -323,7 +438,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
             if (tok >= T) continue;
 #pragma unroll
             for (int rb = 0; rb < 4; rb++) {
-                const int n = n0 + wn * 32 * WNT + bb * 32 + 8 * rb + ci;  // first of 4 consecutive rows
+                const int n = n0 + wrow(bb, rb) + ci;  // first of 4 consecutive rows
                 if (n >= N) continue;
                 const f32x16_v& v = acc[a][bb];
                 if constexpr (OUT == kOutGLU) {
@@ -393,7 +508,7 @@ void* i8_ws(size_t bytes, hipStream_t st) {
 size_t xq_bytes(int k, int t) { return ((size_t)t * k + 255) / 256 * 256; }
 size_t i8_ws_bytes(int k, int t) { return xq_bytes(k, t) + (size_t)t * (k / 32) * 4; }  // sx sized for G = 32
 
-template <int G, bool Q8>
+template <int G, int WF>
 void run_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int out, hipStream_t st) {
     char* ws = static_cast<char*>(i8_ws(i8_ws_bytes(w.k, t), st));
     int8_t* xq = reinterpret_cast<int8_t*>(ws);
@@ -405,7 +520,7 @@ void run_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, in
     const int nbn = (w.n + BN - 1) / BN, nbt = (t + BM - 1) / BM, ntiles = nbn * nbt;
     const unsigned blocks = (unsigned)(8 * ((ntiles + 7) / 8));
 #define QE_GI(SDT_, OUT_)                                                                                            \
-    gemm_i8_kernel<G, SDT_, OUT_, Q8><<<dim3(blocks), dim3(NTH), kLds, st>>>(w.q, w.s, w.n, w.k, xq, sx, t, c, ldc, nbn, \
+    gemm_i8_kernel<G, SDT_, OUT_, WF, false><<<dim3(blocks), dim3(NTH), kLds, st>>>(w.q, w.s, w.n, w.k, xq, sx, t, c, ldc, nbn, \
                                                                           ntiles)
     if (w.sdt == kScaleF16) {
         if (out == kOutGLU) QE_GI(kScaleF16, kOutGLU);
@@ -420,7 +535,42 @@ void run_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, in
     HIP_CHECK(hipGetLastError());
 }
 
+template <int SDT, bool PC>
+void run_w8a8(const W8& w, const int8_t* xq, const float* sx, void* c, int ldc, int t, bool out_bf16, hipStream_t st) {
+    const int nbn = (w.n + BN - 1) / BN, nbt = (t + BM - 1) / BM, ntiles = nbn * nbt;
+    const unsigned blocks = (unsigned)(8 * ((ntiles + 7) / 8));
+    if (out_bf16)
+        gemm_i8_kernel<128, SDT, kOutBF16, kW8, PC><<<dim3(blocks), dim3(NTH), kLds, st>>>(w.q, w.s, w.n, w.k, xq, sx, t,
+                                                                                        c, ldc, nbn, ntiles);
+    else
+        gemm_i8_kernel<128, SDT, kOutF32, kW8, PC><<<dim3(blocks), dim3(NTH), kLds, st>>>(w.q, w.s, w.n, w.k, xq, sx, t,
+                                                                                       c, ldc, nbn, ntiles);
+}
+
 }  // namespace
+
+void gemm_w8a8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st) {
+    CHECK(!w.q8 && !w.glu, "gemm_w8a8: W8 layout matrices only");
+    CHECK(w.n > 0 && w.n % 16 == 0 && w.k >= 128 && w.k % 128 == 0, "gemm_w8a8: n = %d, k = %d", w.n, w.k);
+    CHECK(t > 0, "gemm_w8a8: t = %d", t);
+    CHECK(ldx >= w.k && ((uintptr_t)x & 1) == 0, "gemm_w8a8: ldx = %d < k", ldx);
+    CHECK(ldc >= w.n, "gemm_w8a8: ldc = %d < n", ldc);
+    char* ws = static_cast<char*>(i8_ws(i8_ws_bytes(w.k, t), st));
+    int8_t* xq = reinterpret_cast<int8_t*>(ws);
+    float* sx = reinterpret_cast<float*>(ws + xq_bytes(w.k, t));
+    const unsigned pb = (unsigned)(((long)t * (w.k / 32) + 255) / 256);
+    if (((uintptr_t)x & 15) == 0 && ldx % 8 == 0) x_to_r8_kernel<true><<<dim3(pb), dim3(256), 0, st>>>(x, ldx, w.k, t, xq, sx);
+    else x_to_r8_kernel<false><<<dim3(pb), dim3(256), 0, st>>>(x, ldx, w.k, t, xq, sx);
+    HIP_CHECK(hipGetLastError());
+    if (w.sdt == kScaleF16) {
+        if (w.per_channel) run_w8a8<kScaleF16, true>(w, xq, sx, c, ldc, t, out_bf16, st);
+        else run_w8a8<kScaleF16, false>(w, xq, sx, c, ldc, t, out_bf16, st);
+    } else {
+        if (w.per_channel) run_w8a8<kScaleBF16, true>(w, xq, sx, c, ldc, t, out_bf16, st);
+        else run_w8a8<kScaleBF16, false>(w, xq, sx, c, ldc, t, out_bf16, st);
+    }
+    HIP_CHECK(hipGetLastError());
+}
 
 void gemm_i8_reserve(int k, int t) {
     if (k > 0 && t > 0) i8_ws(i8_ws_bytes(k, t), 0);
@@ -435,12 +585,12 @@ void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t
     CHECK(ldc >= (w.glu ? w.n / 2 : w.n), "gemm_w4_i8: ldc = %d", ldc);
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
     if (q8) {
-        if (G == 32) run_i8<32, true>(w, x, ldx, c, ldc, t, out, st);
-        else if (G == 64) run_i8<64, true>(w, x, ldx, c, ldc, t, out, st);
-        else run_i8<128, true>(w, x, ldx, c, ldc, t, out, st);
+        if (G == 32) run_i8<32, kQ8>(w, x, ldx, c, ldc, t, out, st);
+        else if (G == 64) run_i8<64, kQ8>(w, x, ldx, c, ldc, t, out, st);
+        else run_i8<128, kQ8>(w, x, ldx, c, ldc, t, out, st);
     } else {
-        if (G == 32) run_i8<32, false>(w, x, ldx, c, ldc, t, out, st);
-        else if (G == 64) run_i8<64, false>(w, x, ldx, c, ldc, t, out, st);
-        else run_i8<128, false>(w, x, ldx, c, ldc, t, out, st);
+        if (G == 32) run_i8<32, kW4>(w, x, ldx, c, ldc, t, out, st);
+        else if (G == 64) run_i8<64, kW4>(w, x, ldx, c, ldc, t, out, st);
+        else run_i8<128, kW4>(w, x, ldx, c, ldc, t, out, st);
     }
 }

@@ -108,6 +108,8 @@ void gemm_h_reserve(int k, int t);
 void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int G, bool out_bf16, hipStream_t st,
                 bool q8 = false);
 void gemm_i8_reserve(int k, int t);
+// the reference's W8A8 row GEMM of a W8 matrix (k_x_to_r8 + k_rows_qt), on the same pre-pass buffer
+void gemm_w8a8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
 void gemm_set_out_bf16(bool on);
 // reserve the split-K workspace of the current device (grown on demand otherwise, never during graph capture)
 void gemm_reserve(size_t bytes);

@@ -253,6 +253,27 @@ def gemm_w8(w: W8, x, out_bf16=False, y=None):
     return y
 
 
+def gemm_w8a8(w: W8, x, out_bf16=False, y=None):
+    """W8A8 row GEMM, the reference's prefill numerics for INT8 matrices (k_x_to_r8 + k_rows_qt;
+    qe_gemm_w8a8_ex): bit-identical to its arithmetic"""
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, False, x.device) if y is None else y
+    call("qe_gemm_w8a8_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
+         w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y
+
+
+def rows8(w: W8, x, y=None):
+    """the reference's Worker::rows8 dispatch (qe_rows8): W8A8 for m >= 64, k <= 4096 and an 8-element row
+    stride, else the W8A16 GEMM; fp32 out"""
+    m = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = torch.empty(m, w.n, dtype=torch.float32, device=x.device) if y is None else y
+    call("qe_rows8", w.q, w.s, w.n, w.k, w.flags, x, x.stride(0), y, y.stride(0), m, _stream())
+    return y
+
+
 @dataclass
 class Q8:
     """INT8 layer weights in the reference's Q8 byte order (src/kernels/q8_layout.h), bf16 group-128 scales"""

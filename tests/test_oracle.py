@@ -489,3 +489,58 @@ def test_gemm_i8_brute_force():
         for j in range(n):
             want[i, j] = sum(float(q[i, kk]) * float(sx[i, kk // G]) * float(w[j, kk]) * s[j, kk // 128] for kk in range(k))
     assert np.allclose(got, want, rtol=1e-12, atol=1e-12)
+
+
+def _rn_f32(v):
+    """an exact rational -> the nearest float32, ties to even (normal and subnormal range, no overflow)"""
+    from fractions import Fraction
+    if v == 0:
+        return np.float32(0)
+    a = abs(v)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    ulp = Fraction(2) ** max(e - 23, -149)
+    q, r = divmod(a, ulp)
+    if r * 2 > ulp or (r * 2 == ulp and q % 2 == 1):
+        q += 1
+    return np.float32(float(q * ulp) * (1 if v > 0 else -1))
+
+
+@pytest.mark.parametrize("per_channel", [False, True])
+def test_rows_w8a8_exact_rational(per_channel):
+    """rows_w8a8 = the per-group steps in exact rational arithmetic on a tiny shape: integer sum, one float32
+    rounding of sum * sx, one of the fused multiply-add p * sw + y (k_rows_qt, src/flash/flash_pfq.cuh:637-641)"""
+    from fractions import Fraction
+    rng = np.random.default_rng(7 + per_channel)
+    t, n, k = 3, 4, 384
+    ng = k // 128
+    xq = rng.integers(-127, 128, (t, k)).astype(np.int8)
+    sx = ((rng.random((t, ng)) * 0.05 + 1e-3).astype(np.float32).view(np.uint32) & np.uint32(0xFFFFFFFC)).view(np.float32)
+    w = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    sw = oracle.bf16_to_f32(synth.np_bf16((rng.standard_normal((n,) if per_channel else (n, ng)) * 0.01).astype(np.float32)))
+    got = oracle.rows_w8a8(xq, sx, w, sw, per_channel)
+    for i in range(t):
+        for j in range(n):
+            y = np.float32(0)
+            for g in range(ng):
+                s = int(np.dot(xq[i, 128 * g:128 * g + 128].astype(np.int64), w[j, 128 * g:128 * g + 128].astype(np.int64)))
+                p = _rn_f32(Fraction(s) * Fraction(float(sx[i, g])))
+                swg = sw[j] if per_channel else sw[j, g]
+                y = _rn_f32(Fraction(float(p)) * Fraction(float(swg)) + Fraction(float(y)))
+            assert got[i, j] == y, (i, j, got[i, j], y)
+
+
+def test_rows_w8a8_integer_inputs_exact():
+    """power-of-two scales and small integers: every partial result is a multiple of 2^-13 below 2^7 (20 bits), so
+    every rounding is exact and rows_w8a8 equals the float64 product"""
+    rng = np.random.default_rng(3)
+    t, n, k = 6, 10, 512
+    xq = rng.integers(-20, 21, (t, k)).astype(np.int8)
+    w = rng.integers(-20, 21, (n, k)).astype(np.int8)
+    sx = (2.0 ** rng.integers(-6, -4, (t, k // 128))).astype(np.float32)
+    sw = (2.0 ** rng.integers(-7, -5, (n, k // 128))).astype(np.float32)
+    got = oracle.rows_w8a8(xq, sx, w, sw, False)
+    xd = (xq.astype(np.float64).reshape(t, k // 128, 128) * sx[:, :, None]).reshape(t, k)
+    wd = (w.astype(np.float64).reshape(n, k // 128, 128) * sw[:, :, None]).reshape(n, k)
+    assert np.array_equal(got.astype(np.float64), xd @ wd.T)
