@@ -5,7 +5,9 @@
 //     gemm.cu:540-594);
 //   * the weights enter as the exact signed int8 u - 8;
 //   * each G-group's integer dot product (exact, int32) is converted to fp32, multiplied by sx and added at sw
-//     (the 128-k weight group scale) into fp32 accumulators.
+//     (the 128-k weight group scale) into fp32 accumulators: acc = fma(rn(sum * sx), sw, acc), with the int32 sums
+//     started at the bit pattern of 1.5 * 2^23 so that the first two steps are one fma.
+// The same kernel runs the W8A8 products of INT8 matrices (Q8 and W8 layouts, below).
 // The reference flushes per G-group into a per-128-k partial and scales that by sw; both are within fp32 rounding
 // of the float64 product of the dequantized int8 operands (the reference's gate, tests/test_gemm_i8.py:125-135:
 // relative rms below 1e-5 against that emulation).
@@ -171,6 +173,14 @@ __device__ __forceinline__ uint32_t nib_s8(uint32_t u) { return ((u | 0x80808080
 //   the same rn(sum sx)), so the result is fixed to the bit.
 enum Wf : int { kW4 = 0, kQ8 = 1, kW8 = 2 };
 
+// Every group's int32 sums start at the bit pattern of M = 1.5 * 2^23: |sum| < 2^22 (at most 128 * 127 * 127), so the
+// accumulator read as fp32 is M + sum exactly, and fma(M + sum, sx, -M sx) = rn(sum * sx) (M sx is exact, sx having 22
+// significant bits): the flush costs 2 VALU per output instead of convert, multiply and fma
+constexpr float kMagicF = 12582912.f;
+constexpr int kMagicI = 0x4B400000;
+constexpr i32x16_v kMagic16 = {kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI,
+                               kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI, kMagicI};
+
 template <int G, int SDT, int OUT, int WF, bool PC>
 __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                       int N, int K, const int8_t* __restrict__ xq,
@@ -197,7 +207,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
             const int r0 = (wave * (BM / 64) + i) * 8, row = r0 + (lane >> 3);
             const int ch = (lane & 7) ^ swz_f(row);
             const int tok = t0 + row < T ? t0 + row : T - 1;
-            dma16(xq + (size_t)tok * K + kt * BK + ch * 16, lds32 + xt + r0 * 128);
+            dma16(xq + (size_t)tok * K + kt * BK + ch * 16, __builtin_amdgcn_readfirstlane(lds32 + xt + r0 * 128));
         }
     };
     // the step's two raw 64-k W4 chunks: lane i of wave w < 8 loads record (tile 2 w + (i / 8) % 2, g = i % 8,
@@ -206,8 +216,8 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         if (wave < BN / 32) {
             const int tl = min((n0 >> 4) + 2 * wave + ((lane >> 3) & 1), ntile_last);
             const uint4* src = q + ((size_t)tl * (K >> 6) + 2 * kt) * 32 + 4 * (lane & 7) + (lane >> 4);
-            dma16(src, lds32 + raw + wave * 1024);
-            dma16(src + 32, lds32 + raw + BN * 32 + wave * 1024);
+            dma16(src, __builtin_amdgcn_readfirstlane(lds32 + raw + wave * 1024));
+            dma16(src + 32, __builtin_amdgcn_readfirstlane(lds32 + raw + BN * 32 + wave * 1024));
         }
     };
     // Q8 W tile of step kt: 128 wave instructions of 256 B (two 128-B rows), 16 per wave; lane l fills dword l % 4 of
@@ -221,7 +231,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
             const int cl = ((lane >> 2) & 7) ^ swz_f(row);
             const int tl = min((n0 + row) >> 4, ntile_last), g = row & 7, h = (row >> 3) & 1;
             const size_t rec = ((size_t)tl * (K >> 5) + kt * 4 + (cl >> 1)) * 32 + g * 4 + (lane & 3);
-            dma4(q32 + rec * 4 + 2 * (cl & 1) + h, lds32 + wtile + u * 256);
+            dma4(q32 + rec * 4 + 2 * (cl & 1) + h, __builtin_amdgcn_readfirstlane(lds32 + wtile + u * 256));
         }
     };
     // W8 tile of step kt as BN / 2 pair lines (line 8 (local tile) + g: rows g and g + 8), 256 B each: the records
@@ -233,14 +243,16 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
             const int u = wave * (BN / 64) + i, line = 4 * u + (lane >> 4), g = line & 7;
             const int cl = (lane & 15) ^ g;
             const int tl = min((n0 >> 4) + (line >> 3), ntile_last);
-            dma16(q + ((size_t)tl * (K >> 5) + kt * 4 + (cl >> 2)) * 32 + 4 * g + (cl & 3), lds32 + wtile + u * 1024);
+            dma16(q + ((size_t)tl * (K >> 5) + kt * 4 + (cl >> 2)) * 32 + 4 * g + (cl & 3),
+                  __builtin_amdgcn_readfirstlane(lds32 + wtile + u * 1024));
         }
     };
     auto dma_sc = [&](int grp, unsigned sc) {
         if (wave < BN / 128) {
             const int tl = min((n0 >> 4) + 8 * wave + (lane >> 3), ntile_last);
-            if constexpr (PC) dma4(s + (size_t)tl * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
-            else dma4(s + ((size_t)tl * G128 + grp) * 16 + 2 * (lane & 7), lds32 + sc + wave * 256);
+            const unsigned dst = __builtin_amdgcn_readfirstlane(lds32 + sc + wave * 256);
+            if constexpr (PC) dma4(s + (size_t)tl * 16 + 2 * (lane & 7), dst);
+            else dma4(s + ((size_t)tl * G128 + grp) * 16 + 2 * (lane & 7), dst);
         }
     };
     // activation scales of the step: [BM tokens][NGS] floats, 4 bytes per lane
@@ -249,13 +261,21 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         if (wave < NW) {
             const int i = wave * 64 + lane, row = i / NGS, gi = i % NGS;
             const int tok = t0 + row < T ? t0 + row : T - 1;
-            dma4(sxg + (size_t)tok * (K / G) + kt * NGS + gi, lds32 + sxo + wave * 256);
+            dma4(sxg + (size_t)tok * (K / G) + kt * NGS + gi, __builtin_amdgcn_readfirstlane(lds32 + sxo + wave * 256));
         }
     };
     const int jj = tid & 3, jg = (tid >> 2) & 7, jtr = tid >> 5;
     static_assert(BN * 2 == NTH, "one unpack job per thread");
 
+    // two stages of X, W and the scales in LDS (a third, the DMA two steps ahead, measured slower for kW8)
     constexpr unsigned kRawOff = 2 * kStage, kScOff = kRawOff + 2 * kRaw, kSxOff = kScOff + 2 * kSc;
+    auto dma_step = [&](int kk, int slot) {  // X, the Q8 / W8 tile and the scales of step kk into stage slot
+        dma_x(kk, slot * kStage);
+        if constexpr (WF == kQ8) dma_wq8(kk, slot * kStage + BM * BK);
+        if constexpr (WF == kW8) dma_w8(kk, slot * kStage + BM * BK);
+        dma_sc(kk, kScOff + slot * kSc);
+        dma_sx(kk, kSxOff + slot * kSx);
+    };
     const int wm = wave >> 2, wn = wave & 3;
     // first of the 4 consecutive weight rows (block-local) of register quad rq of MFMA tile bb, lanes l < 32 (+4 for
     // l >= 32): kW8 tiles bb hold the rows g + 8 bb of the wave's four 16-row tiles, the others 32 consecutive rows
@@ -294,17 +314,11 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         }
     };
 
-    dma_x(0, 0);
-    if constexpr (WF == kQ8) {
-        dma_wq8(0, BM * BK);
-    } else if constexpr (WF == kW8) {
-        dma_w8(0, BM * BK);
-    } else {
+    dma_step(0, 0);
+    if constexpr (WF == kW4) {
         dma_w4(0, kRawOff);
         if (KT > 1) dma_w4(1, kRawOff + kRaw);
     }
-    dma_sc(0, kScOff);
-    dma_sx(0, kSxOff);
     asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
     if constexpr (WF == kW4) {
         read_words(lds + kRawOff);
@@ -323,17 +337,12 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
     auto kstep = [&](int kt, auto more) {
         constexpr bool MORE = decltype(more)::value;
         char* wnext = lds + ((kt + 1) & 1) * kStage + BM * BK;
-        if (MORE) {
-            dma_x(kt + 1, ((kt + 1) & 1) * kStage);
-            if constexpr (WF == kQ8) dma_wq8(kt + 1, ((kt + 1) & 1) * kStage + BM * BK);
-            if constexpr (WF == kW8) dma_w8(kt + 1, ((kt + 1) & 1) * kStage + BM * BK);
-            dma_sc(kt + 1, kScOff + ((kt + 1) & 1) * kSc);
-            dma_sx(kt + 1, kSxOff + ((kt + 1) & 1) * kSx);
-        }
+        const int cur = kt & 1;
+        if (MORE) dma_step(kt + 1, (kt + 1) & 1);
         if constexpr (WF == kW4) {
             if (kt + 2 < KT) dma_w4(kt + 2, kRawOff + (kt & 1) * kRaw);
         }
-        const char* xt = lds + (kt & 1) * kStage;
+        const char* xt = lds + cur * kStage;
         const char* wt = xt + BM * BK;
         i32x4_v af[2][WMT], bfr[2][WNT];  // af: X (B operand), bfr: W (A operand)
         i32x4_v wraw[2][2];                // kW8: the two records (t = 2 h, 2 h + 1) of the lane's pair line
@@ -369,8 +378,8 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         if constexpr (WF == kW8) split_rows(0);
         if constexpr (MORE && WF == kW4) read_words(lds + kRawOff + ((kt + 1) & 1) * kRaw);
         // weight scales of this lane's rows (4 consecutive rows per register quad, one 8-byte read) for the step
-        const uint16_t* scb = reinterpret_cast<const uint16_t*>(lds + kScOff + (kt & 1) * kSc);
-        const float* sxb = reinterpret_cast<const float*>(lds + kSxOff + (kt & 1) * kSx);
+        const uint16_t* scb = reinterpret_cast<const uint16_t*>(lds + kScOff + cur * kSc);
+        const float* sxb = reinterpret_cast<const float*>(lds + kSxOff + cur * kSx);
         float swf[WNT][16];
 #pragma unroll
         for (int bb = 0; bb < WNT; bb++)
@@ -391,7 +400,7 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
             for (int a = 0; a < WMT; a++) {
 #pragma unroll
                 for (int bb = 0; bb < WNT; bb++) {
-                    const i32x16_v cin = ks % KPG == 0 ? i32x16_v{} : dsum[a][bb];
+                    const i32x16_v cin = ks % KPG == 0 ? kMagic16 : dsum[a][bb];
                     dsum[a][bb] = __builtin_amdgcn_mfma_i32_32x32x32_i8(bfr[ks & 1][bb], af[ks & 1][a], cin, 0, 0, 0);
                 }
                 if constexpr (MORE && WF == kW4) {
@@ -412,11 +421,15 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
 #pragma unroll
                 for (int a = 0; a < WMT; a++) {
                     const float sxa = sxb[(wm * 32 * WMT + a * 32 + (lane & 31)) * NGS + gi];
+                    const float msx = -kMagicF * sxa;  // exact: sx has 22 significant bits
 #pragma unroll
                     for (int bb = 0; bb < WNT; bb++)
 #pragma unroll
-                        for (int r = 0; r < 16; r++)
-                            acc[a][bb][r] = fmaf((float)dsum[a][bb][r] * sxa, swf[bb][r], acc[a][bb][r]);
+                        for (int r = 0; r < 16; r++) {
+                            // copied to a scalar first: hipcc lowers a bit_cast of an ext_vector element as element 0
+                            const int d = dsum[a][bb][r];
+                            acc[a][bb][r] = fmaf(fmaf(__builtin_bit_cast(float, d), sxa, msx), swf[bb][r], acc[a][bb][r]);
+                        }
                 }
                 __builtin_amdgcn_sched_barrier(0);
             }
