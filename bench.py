@@ -23,6 +23,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+INT8_PEAK_TOPS = 5033.2  # dense int8 MFMA, TOP/s
 
 
 def parse():
@@ -198,8 +199,10 @@ def bench_gemm(m, n, k, steps=10, warmup=3, copies=2, h16=False, i8=0):
             "ms_kernel": round(ev_ms, 4), "working_set": copies * (n * k // 2 + n * k // 64) + m * k * 2 + m * n * 2}
 
 
-def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=32):
-    """INT8 W8A16 per-channel: GEMV (m = 1) in GB/s, GEMM (m = 4096) in TFLOP/s"""
+def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=32, w8a8=False):
+    """INT8 W8A16 per-channel: GEMV (m = 1) in GB/s, GEMM (m = 4096) in TFLOP/s. w8a8: the
+    reference's W8A8 row GEMM of the same matrix (activation pre-pass + int8 GEMM, both timed), against the int8
+    peak"""
     import torch
     from qengine_amd import ops
     g = torch.Generator(device="cuda")
@@ -216,6 +219,8 @@ def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=32):
     y = torch.empty(m, n, dtype=torch.bfloat16, device="cuda")
     if m <= 16:
         fn = lambda i: ops.gemv_w8(ws[i], x, out_bf16=True, y=y)  # noqa: E731
+    elif w8a8:
+        fn = lambda i: ops.gemm_w8a8(ws[i], x, out_bf16=True, y=y)  # noqa: E731
     else:
         fn = lambda i: ops.gemm_w8(ws[i], x, out_bf16=True, y=y)  # noqa: E731
     _, ev_ms = time_launches(fn, steps if m <= 16 else 10, warmup, len(ws), graph=m <= 16)
@@ -226,9 +231,12 @@ def bench_w8(m, n=8192, k=2048, steps=100, warmup=10, copies=32):
         return {"m": m, "gbs": round(b / (ev_ms * 1e-3) / 1e9, 1), "pct_hbm": round(100 * b / (ev_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 1),
                 "us_kernel": round(ev_ms * 1e3, 2), "bytes": b, "working_set": b * ncopy}
     flop = 2.0 * m * n * k
-    return {"m": m, "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 1),
-            "pct_bf16_peak": round(100 * flop / (ev_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 1), "ms_kernel": round(ev_ms, 4),
-            "working_set": ncopy * (n * k + 2 * n) + 2 * m * k + 2 * m * n}
+    r = {"m": m, "tflops": round(flop / (ev_ms * 1e-3) / 1e12, 1),
+         "pct_bf16_peak": round(100 * flop / (ev_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 1), "ms_kernel": round(ev_ms, 4),
+         "working_set": ncopy * (n * k + 2 * n) + 2 * m * k + 2 * m * n}
+    if w8a8:
+        r["pct_int8_peak"] = round(100 * flop / (ev_ms * 1e-3) / 1e12 / INT8_PEAK_TOPS, 1)
+    return r
 
 
 def bench_moe(Ts=(1, 16, 4096), E=512, topk=10, H=2048, I=512):
@@ -354,7 +362,7 @@ def main():
                                    "h16_k5120_n17408": bench_gemm(8192, 17408, 5120, h16=True),
                                    "w4a8_g64_k5120_n17408": bench_gemm(8192, 17408, 5120, i8=64),
                                    "w4a8_g128_k5120_n17408": bench_gemm(8192, 17408, 5120, i8=128)},
-               "w8": lambda: {"m1": bench_w8(1), "m4096": bench_w8(4096)},
+               "w8": lambda: {"m1": bench_w8(1), "m4096": bench_w8(4096), "w8a8_m4096": bench_w8(4096, w8a8=True)},
                "moe": lambda: bench_moe(),
                "skinny": lambda: {f"m{m}_n{n}": (lambda r: {"us": round(r["kernel_ms_mean"] * 1e3, 2),
                                                              "gbs": round(r["gbs_kernel"], 1)})(
@@ -392,6 +400,7 @@ def main():
         secondary["prefill_w4a8_g64_k5120_n17408"] = bench_gemm(8192, 17408, 5120, i8=64)
         secondary["w8_gemv_m1_k2048_n8192"] = bench_w8(1)
         secondary["w8_gemm_m4096_k2048_n8192"] = bench_w8(4096)
+        secondary["w8a8_rows_m4096_k2048_n8192"] = bench_w8(4096, w8a8=True)
         secondary["moe_e512_top10_h2048_i512"] = bench_moe()
     cpu = None if args.no_cpu else cpu_baseline(args)
     if not args.no_cpu and not args.no_secondary:
