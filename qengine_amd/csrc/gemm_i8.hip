@@ -42,6 +42,7 @@ constexpr int kSc = BN * 2;                  // [BN / 16][16] weight scales of o
 constexpr int kSx = BM * 4 * 4;              // [BM][128 / G] activation scales, G >= 32
 constexpr int kLds = 2 * kStage + 2 * kRaw + 2 * kSc + 2 * kSx;
 enum Out : int { kOutF32 = 0, kOutBF16 = 1, kOutGLU = 2 };
+constexpr int kColGroup = 4;  // weight-column tiles per group of the tile order
 
 // byte p of a 16-k block holds k offset kPerm(p) = 2 (p / 4) + {0, 8, 1, 9}[p % 4]
 __device__ __forceinline__ int k_perm(int p) { return 2 * (p >> 2) + ((p & 1) ? 8 : 0) + ((p >> 1) & 1); }
@@ -197,7 +198,18 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
     const int per = (ntiles + 7) >> 3, b = blockIdx.x;
     const int tile = (b & 7) * per + (b >> 3);
     if (tile >= ntiles) return;
-    const int n0 = (tile % nbn) * BN, t0 = (tile / nbn) * BM;
+    // tile order: groups of kColGroup weight-column tiles, token blocks outer and columns inner within a group; each
+    // XCD takes a contiguous run of it (blocks b, b + 8, .. run on XCD b % 8), so its 32 resident tiles are 8 token
+    // blocks x 4 columns: per step 8 X slices (16 KB) and 4 W slices (32 KB) through its L2 instead of 1 X slice and
+    // 32 W slices (4x the HBM fetch: each W tile re-read per token block)
+    int tb, cb;
+    {
+        const int nbt = ntiles / nbn, full = nbn / kColGroup, cg = tile / (nbt * kColGroup);
+        const int w = cg < full ? kColGroup : nbn - full * kColGroup, r = tile - cg * nbt * kColGroup;
+        tb = r / w;
+        cb = cg * kColGroup + r % w;
+    }
+    const int n0 = cb * BN, t0 = tb * BM;
     const int G128 = K >> 7, KT = K / BK;
     const int ntile_last = (N >> 4) - 1;
 
