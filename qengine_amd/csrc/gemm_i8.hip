@@ -301,6 +301,20 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         for (int bb = 0; bb < WNT; bb++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[a][bb][r] = 0.f;
+    // kW8: byte offset of record e of k32 step ks in the lane's pair line = w8b[e][ks & 1] + 64 ks: chunk
+    // (4 ks + 2 h + e) ^ g = 4 (ks ^ (g >> 2)) + ((2 h + e) ^ (g & 3)), and ks ^ (g >> 2) = ks + (g >> 2) for even ks,
+    // ks - (g >> 2) for odd ks (so the four reads of a record take immediate offsets from two bases)
+    float swf_pc[PC ? WNT : 1][16];  // per-channel weight scales: the same every step, read once
+    int w8b[2][2];
+    {
+        const int g = lane & 7, hb = 2 * (lane >> 5), line = (wave & 3) * 32 + (lane & 31);
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int base = line * 256 + (((hb + e) ^ (g & 3)) << 4);
+            w8b[e][0] = base + ((g >> 2) << 6);
+            w8b[e][1] = base - ((g >> 2) << 6);
+        }
+    }
     int lane_off[BK / 32];  // k32 step ks: 16 bytes at chunk 2 ks + l / 32 of row l % 32
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ks++) lane_off[ks] = swz(lane & 31, 2 * ks + (lane >> 5));
@@ -364,10 +378,9 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
                 af[buf][a] = *reinterpret_cast<const i32x4_v*>(xt + lane_off[ks] + (wm * 32 * WMT + a * 32) * 128);
             if constexpr (WF == kW8) {
                 // pair line wn * 32 + l % 32 (tile l % 32 / 8 of the wave's four, g = l % 8), records 2 h, 2 h + 1
-                const char* ln = wt + (wn * 32 + (lane & 31)) * 256;
 #pragma unroll
                 for (int e = 0; e < 2; e++)
-                    wraw[buf][e] = *reinterpret_cast<const i32x4_v*>(ln + (((4 * ks + 2 * (lane >> 5) + e) ^ (lane & 7)) << 4));
+                    wraw[buf][e] = *reinterpret_cast<const i32x4_v*>(wt + w8b[e][ks & 1] + 64 * ks);
             } else {
 #pragma unroll
                 for (int bb = 0; bb < WNT; bb++)
@@ -393,16 +406,27 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         const uint16_t* scb = reinterpret_cast<const uint16_t*>(lds + kScOff + cur * kSc);
         const float* sxb = reinterpret_cast<const float*>(lds + kSxOff + cur * kSx);
         float swf[WNT][16];
+        auto load_sw = [&](float (&dst)[WNT][16]) {
 #pragma unroll
-        for (int bb = 0; bb < WNT; bb++)
+            for (int bb = 0; bb < WNT; bb++)
 #pragma unroll
-            for (int rq = 0; rq < 4; rq++) {
-                const uint2 sp = *reinterpret_cast<const uint2*>(scb + wrow(bb, rq) + 4 * (lane >> 5));
-                swf[bb][4 * rq] = scale_to_f32<SDT>((uint16_t)(sp.x & 0xFFFFu));
-                swf[bb][4 * rq + 1] = scale_to_f32<SDT>((uint16_t)(sp.x >> 16));
-                swf[bb][4 * rq + 2] = scale_to_f32<SDT>((uint16_t)(sp.y & 0xFFFFu));
-                swf[bb][4 * rq + 3] = scale_to_f32<SDT>((uint16_t)(sp.y >> 16));
-            }
+                for (int rq = 0; rq < 4; rq++) {
+                    const uint2 sp = *reinterpret_cast<const uint2*>(scb + wrow(bb, rq) + 4 * (lane >> 5));
+                    dst[bb][4 * rq] = scale_to_f32<SDT>((uint16_t)(sp.x & 0xFFFFu));
+                    dst[bb][4 * rq + 1] = scale_to_f32<SDT>((uint16_t)(sp.x >> 16));
+                    dst[bb][4 * rq + 2] = scale_to_f32<SDT>((uint16_t)(sp.y & 0xFFFFu));
+                    dst[bb][4 * rq + 3] = scale_to_f32<SDT>((uint16_t)(sp.y >> 16));
+                }
+        };
+        if constexpr (PC) {
+            if (kt == 0) load_sw(swf_pc);
+#pragma unroll
+            for (int bb = 0; bb < WNT; bb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) swf[bb][r] = swf_pc[bb][r];
+        } else {
+            load_sw(swf);
+        }
         __builtin_amdgcn_sched_barrier(0);
         int slot = 0;
 #pragma unroll
