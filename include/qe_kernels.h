@@ -62,21 +62,31 @@ void qe_set_config(const qe_config_t* cfg);
 void qe_gemm_tune_file(const char* path);
 void qe_gemm_tune_clear(void);
 int qe_gemm_tune_entries(void);
-/* The prefill GEMM's split-K workspace is the library's (per device, grown on demand outside graph capture; a call
- * captured into a graph without enough of it runs unsplit). Reserve `bytes` on the current device before capturing
- * (the reference's gemm_reserve_ws). */
+/* Library-owned workspaces of the prefill GEMMs (the split-K partial sums, the fp16-accumulate and W4A8 / W8A8
+ * pre-pass buffers) are kept per (device, stream): calls on one stream share a buffer (they run in order), calls on
+ * two streams of a device use two, so concurrent streams (or graphs replayed on two streams) never overwrite each
+ * other's workspace (the reference keeps them thread_local, src/kernels/gemm.cu:3258-3368). A buffer grows on a call
+ * outside graph capture; during capture it is not grown (the GEMM then runs unsplit; a pre-pass aborts with a message).
+ * qe_gemm_reserve sizes the split-K workspace of the current device's default stream before capturing (the
+ * reference's gemm_reserve_ws); qe_gemm_reserve_s that of `stream`. */
 void qe_gemm_reserve(size_t bytes);
+void qe_gemm_reserve_s(size_t bytes, void* stream);
+/* test hook: how many workspace buffers of a kind (0 split-K, 1 W4A8 / W8A8 pre-pass, 2 fp16-accumulate pre-pass)
+ * the library holds, over all devices and streams. No counterpart in the reference. */
+int qe_workspace_count(int kind);
 /* Prefill GEMM with the reference's fp16-accumulate numerics (gemm_h_kernel + x_to_h_kernel,
  * src/kernels/gemm.cu:236-461): activations scaled per token to |x| <= 16 (xs = amax / 16) and rounded to fp16,
  * weights as the exact integers u - 8 in fp16, each 64-k chunk's partial rounded to fp16 and scaled by its group
  * scale into fp32, the token scale in the epilogue. flags: QE_SCALE_F16, QE_OUT_BF16, QE_GLU (y = the bf16
- * activation [t][n / 2]). The pre-pass buffer (t * (2 k + 4) bytes) is the library's, grown on first use per
- * device; qe_gemm_h_reserve(k, t) sizes it before graph capture (a capture that needs more aborts with a message).
+ * activation [t][n / 2]). The pre-pass buffer (t * (2 k + 4) bytes) is the library's, one per (device, stream),
+ * grown on first use; qe_gemm_h_reserve(k, t) sizes the default stream's, qe_gemm_h_reserve_s that of `stream`,
+ * before graph capture (a capture that needs more aborts with a message).
  * No single counterpart function in the reference (its gemm_w4 picks this path by QE_GEMM_H16); also reached
  * through qe_gemm_w4* with qe_config_t.gemm_h16 = 1. */
 void qe_gemm_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                     int flags, void* stream);
 void qe_gemm_h_reserve(int k, int t);
+void qe_gemm_h_reserve_s(int k, int t, void* stream);
 /* W4A8 prefill GEMM, the reference's default prefill numerics (gemm_w4_i8 = x_to_i8_kernel + gemm_i8*_kernel,
  * src/kernels/gemm.cu:463-594,4513-4518): activations quantized per (token, G-group), G = 32, 64 or 128, to int8
  * with sx = amax / 127 (two lowest mantissa bits cleared) and q = rn(x / sx); weights as the exact int8 u - 8;
@@ -84,8 +94,8 @@ void qe_gemm_h_reserve(int k, int t);
  * reference src/capi.cpp:104 (y fp32 [t][n], or bf16 after qe_gemm_set_out_bf16(1); bf16 scales), qe_gemm_w4_i8_glu
  * src/capi.cpp:109 (act bf16 [t][n/2] of a GLU matrix); ci / ks (the reference's tile candidate and kernel variant)
  * are accepted and ignored. qe_gemm_w4_i8_ex: strides, stream, flags QE_SCALE_F16 / QE_OUT_BF16 / QE_GLU. The
- * pre-pass buffer (t * (k + k / 8) bytes) is the library's, grown on first use per device; qe_gemm_i8_reserve(k, t)
- * sizes it before graph capture. */
+ * pre-pass buffer (t * (k + k / 8) bytes) is the library's, one per (device, stream), grown on first use;
+ * qe_gemm_i8_reserve(k, t) sizes the default stream's, qe_gemm_i8_reserve_s that of `stream`, before graph capture. */
 void qe_gemm_w4_i8(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int t, int G, int ci,
                    int ks);
 void qe_gemm_w4_i8_glu(const void* q, const void* s, int n, int k, const uint16_t* x, void* act, int t, int G, int ci,
@@ -93,6 +103,7 @@ void qe_gemm_w4_i8_glu(const void* q, const void* s, int n, int k, const uint16_
 void qe_gemm_w4_i8_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                       int G, int flags, void* stream);
 void qe_gemm_i8_reserve(int k, int t);
+void qe_gemm_i8_reserve_s(int k, int t, void* stream);
 /* test hook: qe_gemm_w4_ex with a given choice instead of the tuner's (cfg 0: 256 x 256 tiles, 1: 256 x 128; ks: K
  * ranges of the last partial round's tiles, 1 / 2 / 4); returns 1 if that split applies to the shape (else it runs
  * unsplit and returns 0). The reference's QE_GEMM_FORCE (src/kernels/gemm.cu:4376-4394). */
@@ -123,8 +134,10 @@ void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, f
  * Replaces reference src/capi.cpp:52. */
 void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);
 
-/* skinny GEMM, bit-identical to qe_gemv_w4g for every row count; returns 0 when the shape is unsupported
- * (m outside 1..16), 1 when it ran. Replaces reference src/capi.cpp:79 (skinny_w4, skinny.cu). */
+/* skinny GEMM, bit-identical to qe_gemv_w4g for every row count; m = 1..32 (the reference's skinny_w4 range,
+ * skinny.cu:572): 17..32 rows run as one launch of the wide kernel, which needs 16-byte aligned rows (k % 8 == 0)
+ * and an even K slicing. Returns 0 (nothing written) when the shape is unsupported, 1 when it ran. Replaces
+ * reference src/capi.cpp:79-83 (skinny_w4, skinny.cu:572-604). */
 int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);
 
 /* qe_gemv_w4 on an explicit stream. Replaces reference src/capi.cpp:101. */

@@ -9,6 +9,7 @@ Parity pins (each function is checked against something other than itself in tes
   repack_w4         round trip through an independent decoder written from the PTX ISA m16n8k16 A-fragment
                     layout + the reference's nibble pairing (gemv.cu:25-36), bijection, known answers
   dequant_w4        closed form bf16_rn((u - 8) * s) in numpy/torch (tests/test_gemv.py:36)
+  dequant_w4_f16    closed form fp16_rn((u - 8) * s) through torch's float -> half conversion
   matmul_bf16       numpy float64 matmul (|err| bound), brute force on tiny shapes
   glu_rows / glu    the reference's interleave closed form (tests/test_q8.py:75-79 interleave_ref) + torch silu
   quantize_w8       the reference's torch closed form (tests/test_w8.py:6-9)
@@ -20,7 +21,9 @@ Parity pins (each function is checked against something other than itself in tes
                     bijection, known answers written from the layout comment (q8_layout.h:5-12)
   dequant_q8        closed form bf16_rn((u - 128) * s) in numpy
   moe_pack          records decoded back to the source rows with the independent fragment decoder
-  moe_ref           float64 composite of the pinned pieces above (the layer's checker)
+  moe_ref           an independent float64 torch composition of the layer (routing by lexsort, the reference test's
+                    unpack, torch's silu), with planted mistakes (gate / up swapped, the routing weight inside the
+                    silu, no renormalisation, ties to the higher index, a dropped expert) that it must reject
   xh_pos / xh_pack  the lane / k-step statement of the XH layout (gemv_h16.cuh:8-10) for every position, bijection
                     per 64-k chunk, torch's clamp + fp16 conversion for the values
   gemv_h16          exact on integer-valued inputs (equal to the float64 product), and elsewhere within the
@@ -131,6 +134,13 @@ def dequant_w4(q, s, n, k, sdt):
     out = np.empty((n, k), np.uint16)
     lib().or_dequant_w4(_p(q), _p(s), n, k, int(sdt), _p(out))
     return out
+
+
+def dequant_w4_f16(q, s, n, k):
+    """-> float32 [n][k] of fp16_rn((u - 8) * s) (fp16 scales): the exact product in float32, rounded to fp16 (numpy's
+    float32 -> float16 conversion rounds to nearest even)"""
+    e = unpack_w4(q, n, k).astype(np.float32) * np.repeat(f16_to_f32(s), 128, axis=1)
+    return e.astype(np.float16).astype(np.float32)
 
 
 def glu_rows(q, s, n, k, bits=4):
@@ -286,7 +296,8 @@ def moe_pack(gu_q, gu_s, dn_q, dn_s, E, H, I):
 
 def moe_ref(logits, x, gu_q, gu_s, dn_q, dn_s, topk, H, I, tokens=None, exact=False):
     """one MoE layer in float64: out[t] = sum_k w_k * down_e(silu(gate_e x) * up_e x) with (sel, w) from moe_route,
-    on the bf16-dequantized experts (exact: the unrounded (u - 8) * s); tokens: subset of rows (default all).
+    on the weight operands the layer's kernels multiply: gate_up bf16_rn((u - 8) * s), down fp16_rn((u - 8) * s)
+    (exact: the unrounded (u - 8) * s for both); no intermediate rounding; tokens: subset of rows (default all).
     Returns (out [len(tokens)][H], sel, w)."""
     sel, w = moe_route(logits, topk)
     T = logits.shape[0]
@@ -294,14 +305,16 @@ def moe_ref(logits, x, gu_q, gu_s, dn_q, dn_s, topk, H, I, tokens=None, exact=Fa
     xf = bf16_to_f32(x).astype(np.float64)
     cache = {}
 
-    def deq(q, s, n, k):
+    def deq(q, s, n, k, f16):
         if exact:
             return unpack_w4(q, n, k).astype(np.float64) * np.repeat(f16_to_f32(s), 128, axis=1)
+        if f16:
+            return dequant_w4_f16(q, s, n, k).astype(np.float64)
         return bf16_to_f32(dequant_w4(q, s, n, k, 1)).astype(np.float64)
 
     def expert(e):
         if e not in cache:
-            cache[e] = (deq(gu_q[e], gu_s[e], 2 * I, H), deq(dn_q[e], dn_s[e], H, I))
+            cache[e] = (deq(gu_q[e], gu_s[e], 2 * I, H, False), deq(dn_q[e], dn_s[e], H, I, True))
         return cache[e]
 
     out = np.zeros((len(tokens), H))

@@ -78,9 +78,13 @@ void qe_set_config(const qe_config_t* cfg) {
 void qe_gemm_tune_file(const char* path) { gemm_tune_file(path); }
 void qe_gemm_tune_clear(void) { gemm_table_clear(); }
 int qe_gemm_tune_entries(void) { return (int)gemm_table_size(); }
-void qe_gemm_reserve(size_t bytes) { gemm_reserve(bytes); }
-void qe_gemm_h_reserve(int k, int t) { gemm_h_reserve(k, t); }
-void qe_gemm_i8_reserve(int k, int t) { gemm_i8_reserve(k, t); }
+void qe_gemm_reserve(size_t bytes) { gemm_reserve(bytes, 0); }
+void qe_gemm_h_reserve(int k, int t) { gemm_h_reserve(k, t, 0); }
+void qe_gemm_i8_reserve(int k, int t) { gemm_i8_reserve(k, t, 0); }
+void qe_gemm_reserve_s(size_t bytes, void* stream) { gemm_reserve(bytes, as_stream(stream)); }
+void qe_gemm_h_reserve_s(int k, int t, void* stream) { gemm_h_reserve(k, t, as_stream(stream)); }
+void qe_gemm_i8_reserve_s(int k, int t, void* stream) { gemm_i8_reserve(k, t, as_stream(stream)); }
+int qe_workspace_count(int kind) { return stream_ws_count(kind); }
 
 // W4A8 (reference src/capi.cpp:104-113): ci (tile candidate) and ks (kernel variant) select among the reference's
 // CUDA kernels; this build has one kernel per activation group and ignores them
@@ -135,10 +139,16 @@ void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, 
     matmul_w4(mk_w4(q, s, n, k, glu != 0, kScaleBF16), x, k, y, glu ? n / 2 : n, m, false, 0);
 }
 
+// the reference's skinny_w4 takes 1..32 rows (src/kernels/skinny.cu:572); here 1..16 rows run the decode GEMV and
+// 17..32 rows one launch of the wide skinny kernel, which needs 16-byte aligned rows and an even K slicing (else 0:
+// unsupported, the caller falls back to qe_gemv_w4 as the reference's callers do)
 int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu) {
-    if (m < 1 || m > kMaxGemvRows || n % 16 != 0 || k % 128 != 0) return 0;
+    if (m < 1 || m > kWideRows || n <= 0 || k <= 0 || n % 16 != 0 || k % 128 != 0 || k % 8 != 0) return 0;
+    const W4 w = mk_w4(q, s, n, k, glu != 0, kScaleBF16);
+    if (m > kMaxGemvRows && !skinny_w4_wide_fits(w, x, k)) return 0;
     gemv_workspace_init();
-    gemv_w4(mk_w4(q, s, n, k, glu != 0, kScaleBF16), x, k, y, glu ? n / 2 : n, m, false, 0);
+    if (m > kMaxGemvRows) skinny_w4_wide(w, x, k, y, glu ? n / 2 : n, m, false, 0);
+    else gemv_w4(w, x, k, y, glu ? n / 2 : n, m, false, 0);
     return 1;
 }
 

@@ -486,34 +486,6 @@ __global__ void __launch_bounds__(256) splitk_reduce_kernel(const float* __restr
     }
 }
 
-// ---- library-owned split-K workspace, one per device: grown outside graph capture, outgrown buffers retired (kept
-//      allocated: a graph captured earlier may still use them); nullptr while capturing when it is too small
-constexpr int kMaxDev = 64;
-std::mutex g_ws_mu;
-struct SplitWs {
-    void* p = nullptr;
-    size_t bytes = 0;
-    std::vector<void*> retired;
-} g_ws[kMaxDev];
-
-float* split_ws(size_t bytes, hipStream_t st) {
-    int dev = 0;
-    HIP_CHECK(hipGetDevice(&dev));
-    CHECK(dev >= 0 && dev < kMaxDev, "device %d", dev);
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    SplitWs& w = g_ws[dev];
-    if (w.bytes >= bytes) return reinterpret_cast<float*>(w.p);
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    HIP_CHECK(hipStreamIsCapturing(st, &cs));
-    if (cs != hipStreamCaptureStatusNone) return nullptr;
-    void* np = nullptr;
-    HIP_CHECK(hipMalloc(&np, bytes));
-    if (w.p) w.retired.push_back(w.p);
-    w.p = np;
-    w.bytes = bytes;
-    return reinterpret_cast<float*>(np);
-}
-
 // tile configurations: 0 = 256 tokens x 256 rows (WMT 4, WNT 2), 1 = 256 x 128 (4, 1)
 constexpr int kNumCfg = 2;
 template <int CFG>
@@ -556,8 +528,8 @@ bool gemm_geom(int cfg, int n, int k, int t, int ks, GemmGeom& g) {
 
 }  // namespace
 
-void gemm_reserve(size_t bytes) {
-    if (bytes > 0) CHECK(split_ws(bytes, 0) != nullptr, "gemm_reserve: called during graph capture");
+void gemm_reserve(size_t bytes, hipStream_t st) {
+    stream_ws_reserve(kWsSplit, bytes, st);
 }
 
 namespace {
@@ -590,7 +562,7 @@ void run_choice(int cfg, int ks, const uint4* q, const uint16_t* s, int n, int k
     GemmGeom g;
     float* part = nullptr;
     if (ks > 1) {
-        if (!gemm_geom(cfg, n, k, t, ks, g) || (part = split_ws(g.ws_bytes, st)) == nullptr) ks = 1;
+        if (!gemm_geom(cfg, n, k, t, ks, g) || (part = static_cast<float*>(stream_ws(kWsSplit, g.ws_bytes, st))) == nullptr) ks = 1;
     }
     if (ks == 1) gemm_geom(cfg, n, k, t, 1, g);
     if (cfg == 0) launch_cfg<FMT, SDT, 0>(q, s, n, k, x, ldx, t, c, ldc, out, sdt, g, part, st);

@@ -280,42 +280,23 @@ __global__ void __launch_bounds__(NTH) gemm_h_kernel(const uint4* __restrict__ q
     }
 }
 
-// ---- library-owned pre-pass buffers (xh [t][k] fp16, xs [t] fp32), one per device: grown outside graph capture,
-//      outgrown buffers kept (a graph captured earlier may still read them)
-constexpr int kMaxDev = 64;
-std::mutex g_mu;
-struct HWs {
-    void* p = nullptr;
-    size_t bytes = 0;
-    std::vector<void*> retired;
-} g_ws[kMaxDev];
-
+// the pre-pass buffer (xh [t][k] fp16, xs [t] fp32) of (device, stream): a capture that needs more than an eager call
+// or gemm_h_reserve on its stream sized aborts with a message
 void* h_ws(size_t bytes, hipStream_t st) {
-    int dev = 0;
-    HIP_CHECK(hipGetDevice(&dev));
-    CHECK(dev >= 0 && dev < kMaxDev, "device %d", dev);
-    std::lock_guard<std::mutex> lk(g_mu);
-    HWs& w = g_ws[dev];
-    if (w.bytes >= bytes) return w.p;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    HIP_CHECK(hipStreamIsCapturing(st, &cs));
-    CHECK(cs == hipStreamCaptureStatusNone,
-          "gemm_w4h: the pre-pass buffer (%zu bytes) must be sized by an eager call or qe_gemm_h_reserve before capture",
+    void* p = stream_ws(kWsH, bytes, st);
+    CHECK(p != nullptr,
+          "gemm_w4h: the pre-pass buffer (%zu bytes) must be sized by an eager call or qe_gemm_h_reserve(_s) on this "
+          "stream before capture",
           bytes);
-    void* np = nullptr;
-    HIP_CHECK(hipMalloc(&np, bytes));
-    if (w.p) w.retired.push_back(w.p);
-    w.p = np;
-    w.bytes = bytes;
-    return np;
+    return p;
 }
 
 size_t h_ws_bytes(int k, int t) { return ((size_t)t * k * 2 + 255) / 256 * 256 + (size_t)t * 4; }
 
 }  // namespace
 
-void gemm_h_reserve(int k, int t) {
-    if (k > 0 && t > 0) h_ws(h_ws_bytes(k, t), 0);
+void gemm_h_reserve(int k, int t, hipStream_t st) {
+    if (k > 0 && t > 0) stream_ws_reserve(kWsH, h_ws_bytes(k, t), st);
 }
 
 // out: 0 fp32, 1 bf16, 2 GLU (bf16 activation [t][n / 2])

@@ -524,34 +524,15 @@ __global__ void __launch_bounds__(NTH) gemm_i8_kernel(const uint4* __restrict__ 
         }
 }
 
-// ---- library-owned pre-pass buffers (xq [t][k] int8, sx [t][k / G] fp32), one per device, grown outside graph
-//      capture, outgrown buffers kept (a graph captured earlier may still read them)
-constexpr int kMaxDev = 64;
-std::mutex g_mu;
-struct I8Ws {
-    void* p = nullptr;
-    size_t bytes = 0;
-    std::vector<void*> retired;
-} g_ws[kMaxDev];
-
+// the pre-pass buffer (xq [t][k] int8, sx [t][k / G] fp32) of (device, stream): a capture that needs more than an
+// eager call or gemm_i8_reserve on its stream sized aborts with a message
 void* i8_ws(size_t bytes, hipStream_t st) {
-    int dev = 0;
-    HIP_CHECK(hipGetDevice(&dev));
-    CHECK(dev >= 0 && dev < kMaxDev, "device %d", dev);
-    std::lock_guard<std::mutex> lk(g_mu);
-    I8Ws& w = g_ws[dev];
-    if (w.bytes >= bytes) return w.p;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    HIP_CHECK(hipStreamIsCapturing(st, &cs));
-    CHECK(cs == hipStreamCaptureStatusNone,
-          "gemm_w4_i8: the pre-pass buffer (%zu bytes) must be sized by an eager call or qe_gemm_i8_reserve before capture",
+    void* p = stream_ws(kWsI8, bytes, st);
+    CHECK(p != nullptr,
+          "gemm_w4_i8: the pre-pass buffer (%zu bytes) must be sized by an eager call or qe_gemm_i8_reserve(_s) on "
+          "this stream before capture",
           bytes);
-    void* np = nullptr;
-    HIP_CHECK(hipMalloc(&np, bytes));
-    if (w.p) w.retired.push_back(w.p);
-    w.p = np;
-    w.bytes = bytes;
-    return np;
+    return p;
 }
 
 size_t xq_bytes(int k, int t) { return ((size_t)t * k + 255) / 256 * 256; }
@@ -621,8 +602,8 @@ void gemm_w8a8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t,
     HIP_CHECK(hipGetLastError());
 }
 
-void gemm_i8_reserve(int k, int t) {
-    if (k > 0 && t > 0) i8_ws(i8_ws_bytes(k, t), 0);
+void gemm_i8_reserve(int k, int t, hipStream_t st) {
+    if (k > 0 && t > 0) stream_ws_reserve(kWsI8, i8_ws_bytes(k, t), st);
 }
 
 void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int G, bool out_bf16,

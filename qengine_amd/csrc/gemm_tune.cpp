@@ -18,9 +18,12 @@ std::mutex g_mu;
 std::map<std::string, std::map<GemmKey, GemmChoice>> g_tab;  // device line -> choices
 std::string g_path;
 
-std::string dev_line() {
-    int dev = 0;
-    HIP_CHECK(hipGetDevice(&dev));
+// the device's line, built once per device index (the PCI bus id and CU count do not change while the process runs):
+// every prefill GEMM call looks its choice up, and the HIP queries and string formatting are host cost on each call
+constexpr int kMaxDevLines = 64;
+std::string g_dev_lines[kMaxDevLines];  // guarded by g_mu
+
+std::string dev_line_uncached(int dev) {
     char bus[64] = "?";
     if (hipDeviceGetPCIBusId(bus, sizeof(bus), dev) != hipSuccess) snprintf(bus, sizeof(bus), "dev%d", dev);
     int cus = 0;
@@ -28,6 +31,20 @@ std::string dev_line() {
     std::ostringstream o;
     o << "device " << bus << " " << cus;
     return o.str();
+}
+
+std::string dev_line() {
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevLines) return dev_line_uncached(dev);
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (!g_dev_lines[dev].empty()) return g_dev_lines[dev];
+    }
+    const std::string l = dev_line_uncached(dev);
+    std::lock_guard<std::mutex> lk(g_mu);
+    g_dev_lines[dev] = l;
+    return l;
 }
 
 void load_locked() {
@@ -90,6 +107,10 @@ int gemm_bucket(int t) {
 }
 
 bool gemm_table_find(const GemmKey& key, GemmChoice& ch) {
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        if (g_tab.empty()) return false;  // nothing tuned or loaded: no device lookup at all
+    }
     const std::string d = dev_line();
     std::lock_guard<std::mutex> lk(g_mu);
     auto it = g_tab.find(d);

@@ -3,9 +3,12 @@
 #include "gemv_impl.hpp"
 
 #include <algorithm>
+#include <atomic>
 
 namespace {
-int g_cus = 0;
+// CU count per device index (devices may differ, e.g. under compute partitioning); 0 = not queried yet
+constexpr int kMaxCuDev = 64;
+std::atomic<int> g_cus[kMaxCuDev];
 QeConfig g_cfg;
 }
 
@@ -19,14 +22,18 @@ void qe_config_set(const QeConfig& c) {
     g_cfg = c;
 }
 
+// the current device's CU count (every grid-sizing decision uses it)
 int qe_num_cus() {
-    if (g_cus == 0) {
-        int dev, cus = 0;
-        HIP_CHECK(hipGetDevice(&dev));
-        HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-        g_cus = cus > 0 ? cus : 256;
+    int dev = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    CHECK(dev >= 0 && dev < kMaxCuDev, "device %d", dev);
+    int c = g_cus[dev].load(std::memory_order_relaxed);
+    if (c == 0) {
+        HIP_CHECK(hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev));
+        c = c > 0 ? c : 256;
+        g_cus[dev].store(c, std::memory_order_relaxed);
     }
-    return g_cus;
+    return c;
 }
 
 // The decode GEMV keeps no device workspace (its K slices are reduced in LDS); the entry point stays for the

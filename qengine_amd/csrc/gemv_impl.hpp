@@ -45,8 +45,6 @@ __device__ __forceinline__ uint32_t bf16x2_b13(uint32_t t) { return __builtin_am
 constexpr uint32_t kNib = 0x0F0F0F0Fu;
 // the same with the fp16 magic 0x64 (1024 + u) and packed fp16 arithmetic (v_pk_add_f16 / v_pk_fma_f16; packed fp16
 // is not the packed fp32 these kernels avoid): the exact integer u - 8, and for bytes u = w + 128, w / 16
-typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
-typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ uint32_t f16x2_b02(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04020400u); }
 __device__ __forceinline__ uint32_t f16x2_b13(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04030401u); }
 __device__ __forceinline__ uint32_t f16x2_sub1032(uint32_t p) {

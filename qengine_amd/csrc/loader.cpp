@@ -227,16 +227,22 @@ struct StFile {
             st.dtype = dt->str;
             const size_t es = dtype_size(st.dtype);
             CHECK(es > 0, "safetensors: %s: %s has the unknown dtype %s", p.c_str(), kv.first.c_str(), st.dtype.c_str());
-            size_t count = 1;
+            // element count and byte size without wrap-around: a header whose dims multiply past 64 bits (e.g.
+            // [2^36, 2^32]) must not pass as a small tensor
+            size_t count = 1, nbytes = 0;
             for (const Json& d : sh->arr) {
                 CHECK(d.kind == Json::kNum && d.num >= 0 && d.num < (1ll << 40), "safetensors: %s: %s: bad shape",
                       p.c_str(), kv.first.c_str());
                 st.shape.push_back(d.num);
-                count *= (size_t)d.num;
+                CHECK(!__builtin_mul_overflow(count, (size_t)d.num, &count), "safetensors: %s: %s: the shape overflows",
+                      p.c_str(), kv.first.c_str());
             }
+            CHECK(!__builtin_mul_overflow(count, es, &nbytes), "safetensors: %s: %s: the byte size overflows", p.c_str(),
+                  kv.first.c_str());
+            // (e - b) == nbytes and e <= dsize: the tensor's bytes lie inside the file's data
             const long long b = off->arr[0].num, e = off->arr[1].num;
             CHECK(off->arr[0].kind == Json::kNum && off->arr[1].kind == Json::kNum && b >= 0 && e >= b &&
-                      (size_t)e <= dsize && (size_t)(e - b) == count * es,
+                      (size_t)e <= dsize && (size_t)(e - b) == nbytes,
                   "safetensors: %s: %s: data_offsets [%lld, %lld] for %zu elements of %zu bytes (data %zu bytes)",
                   p.c_str(), kv.first.c_str(), b, e, count, es, dsize);
             st.data = data0 + b;
@@ -276,7 +282,8 @@ W4LoadDims w4_load_dims(const StFile& f, const char* const* names, const int* r0
           "load_w4: %s: packed I32 [n][words] and 16-bit scales [n][k/128] expected (%s, %s)", names[0],
           q0.dtype.c_str(), s0.dtype.c_str());
     const long long K = s0.shape[1] * 128;
-    CHECK(K > 0 && (q0.shape[1] * 32) % K == 0, "load_w4: %s: packed width %lld for K %lld", names[0], q0.shape[1], K);
+    CHECK(K > 0 && K < (1ll << 31) && (q0.shape[1] * 32) % K == 0, "load_w4: %s: packed width %lld for K %lld",
+          names[0], q0.shape[1], K);
     d.bits = (int)(q0.shape[1] * 32 / K);
     CHECK((d.bits == 4 || d.bits == 8) && q0.shape[1] * 32 == K * d.bits, "load_w4: %s: packed width %lld for K %lld",
           names[0], q0.shape[1], K);

@@ -11,8 +11,11 @@
 // index, weights exp(l_i - l_max) / sum_sel exp(l_j - l_max). Segmentation (reference k_jobs_pf, :6007-6100) is a
 // counting sort whose order inside an expert is ascending (token, k) (the reference's atomics leave it open):
 // tokens are processed in chunks of 64 with per-expert 64-bit token masks, so every slot is a pure function of
-// the routing. The per-(token, k) down outputs go to bf16 slots summed in k order (reference k_moe_sum,
-// :6436-6482), so the layer is deterministic.
+// the routing. The GLU activations and the per-(token, k) down outputs are stored as fp16 of the value / 16 (the
+// reference's fp16 intermediates: its XH activations and kSlotScale slots, :6185,6308,6421-6427); the slots are summed
+// in k order (reference k_moe_sum, :6436-6482), so the layer is deterministic. The down projection multiplies the
+// fp16 activation by the weights fp16_rn((u - 8) s) on the f16 matrix cores, gate_up the bf16 input by
+// bf16_rn((u - 8) s) on the bf16 ones.
 //
 // Decode (T <= 32): the grouped GEMVs reuse the decode GEMV tile (gemv_impl.hpp) with gathered activation rows,
 // jobs = (expert, chunk of <= 2 rows). Prefill: grouped MFMA GEMMs over (expert, 128-row tile) jobs, one block per
@@ -495,11 +498,12 @@ constexpr int kDecRows = 2;  // rows per decode job
 // Matrix-core decode tile (W4, fp16 scales, slices of NG <= 8 groups, MT <= 4 gathered activation rows) behind
 // gemv_tile's interface. Lane 16 q + i holds A row i of the 16-row tile (its half of the records (g = i % 8, t = q):
 // t = (w >> 4 (i / 8)) & 0x0F0F0F0F) and B column i = activation row i (class-major staged activations, one
-// ds_read_b128 per MFMA). The A values are the reference's weight operand bf16_rn((u - 8) s), s the row's group scale
-// (the prefill GEMMs' operand too, so a token gets the same weights at every T), accumulated across the groups by the
-// MFMAs in fp32. Activations, scales and every group's records are loaded before any wait. Returns red in gemv_tile's
-// layout [S][2][MT][16] (half 1 zero) for rsum().
-template <int MT, int NG>
+// ds_read_b128 per MFMA). The A values are the weight operand bf16_rn((u - 8) s) (gate_up, bf16 activations) or, with
+// F16, fp16_rn((u - 8) s) (down, on the fp16 activation), s the row's group scale (the prefill GEMMs' operands too, so
+// a token gets the same weights at every T), accumulated across the groups by the MFMAs in fp32. Activations, scales
+// and every group's records are loaded before any wait. Returns red in gemv_tile's layout [S][2][MT][16] (half 1
+// zero) for rsum().
+template <int MT, int NG, bool F16 = false>
 __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __restrict__ qp,
                                                const uint16_t* __restrict__ sp, const uint32_t* const* xw, int m,
                                                size_t qgs, size_t sgs) {
@@ -562,15 +566,20 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
             u32x4_v b = *reinterpret_cast<const u32x4_v*>(
                 &xl[(ii * MT + (i < MT ? i : 0)) * XS + (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
             b = i < MT ? b : u32x4_v{0u, 0u, 0u, 0u};
-            const bf16x8_v bb = __builtin_bit_cast(bf16x8_v, b);
             const u32x4_v rec = wv[ii][mm >> 1];
             const int j0 = 2 * (mm & 1);
             const uint32_t t0 = rec[j0] & lmask, t1 = rec[j0 + 1] & lmask;
-            const u32x4_v a = {pack_bf16x2(fmaf(qe_tile::cvt_ubyte<0>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t0), sc, bias)),
-                               pack_bf16x2(fmaf(qe_tile::cvt_ubyte<1>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t0), sc, bias)),
-                               pack_bf16x2(fmaf(qe_tile::cvt_ubyte<0>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t1), sc, bias)),
-                               pack_bf16x2(fmaf(qe_tile::cvt_ubyte<1>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t1), sc, bias))};
-            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb, acc, 0, 0, 0);
+            auto pk = [](float lo, float hi) { return F16 ? pack_f16x2(lo, hi) : pack_bf16x2(lo, hi); };
+            const u32x4_v a = {pk(fmaf(qe_tile::cvt_ubyte<0>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t0), sc, bias)),
+                               pk(fmaf(qe_tile::cvt_ubyte<1>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t0), sc, bias)),
+                               pk(fmaf(qe_tile::cvt_ubyte<0>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t1), sc, bias)),
+                               pk(fmaf(qe_tile::cvt_ubyte<1>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t1), sc, bias))};
+            if constexpr (F16)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a), __builtin_bit_cast(f16x8_v, b),
+                                                             acc, 0, 0, 0);
+            else
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), __builtin_bit_cast(bf16x8_v, b),
+                                                              acc, 0, 0, 0);
         }
     }
     // 4. lane (q, i < MT) holds rows 4 q .. 4 q + 3 of activation row i
@@ -610,7 +619,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
     for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
         const int r = idx >> 3, gg = idx & 7;
         const float v = silu_f32(rsum<MT>(red, S, r, gg)) * rsum<MT>(red, S, r, gg + 8) * slot_w[slot0 + r];
-        act[(size_t)(slot0 + r) * sh.I + g * 128 + tile * 8 + gg] = f32_to_bf16(v);
+        act[(size_t)(slot0 + r) * sh.I + g * 128 + tile * 8 + gg] = f32_to_f16(v * kMoeF16Scale);
     }
 }
 
@@ -649,7 +658,7 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_route_gate_up_kernel(
     if (threadIdx.x < 8) {
         const int gg = threadIdx.x;
         const float v = silu_f32(rsum<1>(red, S, 0, gg)) * rsum<1>(red, S, 0, gg + 8) * sw[p];
-        act[(size_t)p * sh.I + g * 128 + tile * 8 + gg] = f32_to_bf16(v);
+        act[(size_t)p * sh.I + g * 128 + tile * 8 + gg] = f32_to_f16(v * kMoeF16Scale);
     }
 }
 
@@ -677,23 +686,25 @@ __global__ void __launch_bounds__(64) moe_dec_down_kernel(
     constexpr int NH = NGRP <= 8 ? NGRP : 8;
     static_assert(NGRP <= 8 || NGRP == 16, "moe decode down: I / 128 in 1..8 or 16");
     const int idx = threadIdx.x, r = idx >> 4, rr = idx & 15;
-    const float* red = mfma_dec_tile<MT, NH>(lds, qp, sp, xw, m, sh.rec / 16, sh.rec / 4);
+    const float* red = mfma_dec_tile<MT, NH, true>(lds, qp, sp, xw, m, sh.rec / 16, sh.rec / 4);
     float v = idx < m * 16 ? rsum<MT>(red, 1, r, rr) : 0.f;
     if constexpr (NGRP == 16) {
         __syncthreads();
         const uint32_t* xw2[MT];
 #pragma unroll
         for (int q = 0; q < MT; q++) xw2[q] = xw[q] + 8 * 64;  // activations of groups 8..15
-        red = mfma_dec_tile<MT, 8>(lds, qp + 8 * (sh.rec / 16), sp + 8 * (sh.rec / 2), xw2, m, sh.rec / 16, sh.rec / 4);
+        red = mfma_dec_tile<MT, 8, true>(lds, qp + 8 * (sh.rec / 16), sp + 8 * (sh.rec / 2), xw2, m, sh.rec / 16,
+                                         sh.rec / 4);
         v += idx < m * 16 ? rsum<MT>(red, 1, r, rr) : 0.f;
     }
-    if (idx < m * 16) slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_bf16(v);
+    // the activation is act / 16, so v is the slot / 16: stored as is (fp16)
+    if (idx < m * 16) slot_out[(size_t)(slot0 + r) * sh.H + tile * 16 + rr] = f32_to_f16(v);
 }
 
 // T * topk <= 64 (decode, few pairs), I / 128 <= 8: the down GEMV and the combine in one launch. Block (16-row tile
 // of H, token t) of topk waves; wave k multiplies expert sel[t, k]'s tile by act slot inv[t, k] over the whole K = I
-// (the tile of moe_dec_down_kernel with one activation row), and 16 lanes sum the waves' bf16-rounded slots in k
-// order in fp32: the values moe_dec_down_kernel + moe_combine_kernel produce, without the slot_out round trip.
+// (the tile of moe_dec_down_kernel with one activation row), and 16 lanes sum the waves' fp16-rounded slots (x 16) in
+// k order in fp32: the values moe_dec_down_kernel + moe_combine_kernel produce, without the slot_out round trip.
 template <int NGRP>
 __global__ void __launch_bounds__(64 * 16) moe_dec_down_combine_kernel(
     const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ act, const int32_t* __restrict__ sel,
@@ -705,11 +716,11 @@ __global__ void __launch_bounds__(64 * 16) moe_dec_down_combine_kernel(
     const uint4* qp = reinterpret_cast<const uint4*>(rp + sh.gg_q + sh.gg_s) + (size_t)tile * 2 * 32;
     const uint16_t* sp = reinterpret_cast<const uint16_t*>(rp + sh.gg_q + sh.gg_s + sh.gd_q) + (size_t)tile * 16;
     const uint32_t* xw[1] = {reinterpret_cast<const uint32_t*>(act + (size_t)slot * sh.I)};
-    const float* red = mfma_dec_tile<1, NGRP>(lds, qp, sp, xw, 1, sh.rec / 16, sh.rec / 4);
+    const float* red = mfma_dec_tile<1, NGRP, true>(lds, qp, sp, xw, 1, sh.rec / 16, sh.rec / 4);
     if (threadIdx.x < 16) {
         const int rr = threadIdx.x;
         float a = 0.f;
-        for (int kk = 0; kk < topk; kk++) a += bf16_to_f32(f32_to_bf16(rsum<1>(red + kk * 2 * 16, 1, 0, rr)));
+        for (int kk = 0; kk < topk; kk++) a += 16.f * f16_round(rsum<1>(red + kk * 2 * 16, 1, 0, rr));
         const size_t o = (size_t)t * sh.H + tile * 16 + rr;
         if (out_bf16) reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16(a);
         else reinterpret_cast<float*>(out)[o] = a;
@@ -740,8 +751,8 @@ __global__ void moe_combine_kernel(const uint16_t* __restrict__ slot_out, const 
         if (k < topk) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                a[2 * j] += bf16_to_f32((uint16_t)v[k][j]);
-                a[2 * j + 1] += bf16_to_f32((uint16_t)(v[k][j] >> 16));
+                a[2 * j] += 16.f * f16_to_f32((uint16_t)v[k][j]);
+                a[2 * j + 1] += 16.f * f16_to_f32((uint16_t)(v[k][j] >> 16));
             }
         }
     }

@@ -16,9 +16,12 @@
 // MFMAs take the chunks of a step in the order c(ks, kh) = 2 (2 (ks % 2) + kh) + ks / 2 (k16 step ks, k half kh): a
 // lane needs only words kh and 2 + kh of its row pair's four records, every lane of a k16 step the same byte pair
 // (h = ks / 2), and the B operand is chunk c of the token's row, one ds_read_b128 of the swizzled activation tile.
-// Low nibbles = A of row g (operand 0), high nibbles = A of row g + 8 (operand 1). Weights are bf16_rn((u - 8) s)
-// (the high nibbles are converted as 16 u and multiplied by s / 16: the same fma), activations bf16, products
-// accumulated in fp32 by the MFMAs: the dense kernel's arithmetic; only the order of the k inside the step differs.
+// Low nibbles = A of row g (operand 0), high nibbles = A of row g + 8 (operand 1). gate_up (MODE 1): weights
+// bf16_rn((u - 8) s) (the high nibbles are converted as 16 u and multiplied by s / 16: the same fma) on bf16
+// activations, the dense kernel's arithmetic (only the order of the k inside the step differs); down (MODE 2): weights
+// fp16_rn((u - 8) s) on the fp16 activation (act / 16) on the f16 matrix cores (v_mfma_f32_32x32x16_f16, the same
+// operand layout). Products accumulated in fp32 by the MFMAs. The activation and the slot rows are fp16 of the
+// value / 16 (the reference's fp16 intermediates).
 //
 // Output: D row i = 8 (r / 4) + 4 (l / 32) + r % 4 of lane l register r is A row m = i: tile r / 4 of the wave, row
 // pair g = 4 (l / 32) + r % 4; operand 0 holds row g (gate), operand 1 row g + 8 (up) of the same register, so the
@@ -157,8 +160,9 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
         const int bb = u >> 2, t = u & 3;
         const uint32_t v = mw[S][bb][t][j & 1];
         const float s = bb ? sh16[S] : sl[S], bias = bb ? bh[S] : bl[S];
-        an[j & 1][bb][t] = (j >> 1) ? pack_bf16x2(fmaf(cvt_ubyte<1>(v), s, bias), fmaf(cvt_ubyte<3>(v), s, bias))
-                                    : pack_bf16x2(fmaf(cvt_ubyte<0>(v), s, bias), fmaf(cvt_ubyte<2>(v), s, bias));
+        auto pk = [](float lo, float hi) { return MODE == 2 ? pack_f16x2(lo, hi) : pack_bf16x2(lo, hi); };
+        an[j & 1][bb][t] = (j >> 1) ? pk(fmaf(cvt_ubyte<1>(v), s, bias), fmaf(cvt_ubyte<3>(v), s, bias))
+                                    : pk(fmaf(cvt_ubyte<0>(v), s, bias), fmaf(cvt_ubyte<2>(v), s, bias));
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
@@ -212,8 +216,15 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
 #pragma unroll
                 for (int i = 0; i < NS; i++) {
                     const int a = i >> 1;
-                    if (i & 1) acc[a][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A1, xf[ks & 1][a], acc[a][1], 0, 0, 0);
-                    else acc[a][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A0, xf[ks & 1][a], acc[a][0], 0, 0, 0);
+                    if constexpr (MODE == 2) {
+                        const bf16x8_v xb = xf[ks & 1][a];  // bit casts take a scalar temporary
+                        const f16x8_v B = __builtin_bit_cast(f16x8_v, xb);
+                        if (i & 1) acc[a][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_v, a1), B, acc[a][1], 0, 0, 0);
+                        else acc[a][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_v, a0), B, acc[a][0], 0, 0, 0);
+                    } else {
+                        if (i & 1) acc[a][1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A1, xf[ks & 1][a], acc[a][1], 0, 0, 0);
+                        else acc[a][0] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(A0, xf[ks & 1][a], acc[a][0], 0, 0, 0);
+                    }
                     if (ks + 1 < BK / 16) {
 #pragma unroll
                         for (int u = 0; u < 8; u++)
@@ -261,10 +272,11 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
             for (int q = 0; q < 4; q++) {
                 float v[4];
 #pragma unroll
-                for (int j = 0; j < 4; j++) v[j] = silu_f32(acc[a][0][4 * q + j]) * acc[a][1][4 * q + j] * sw;
+                for (int j = 0; j < 4; j++)
+                    v[j] = silu_f32(acc[a][0][4 * q + j]) * acc[a][1][4 * q + j] * sw * kMoeF16Scale;
                 const int col = ((wrow >> 4) + q) * 8 + 4 * kh;
                 *reinterpret_cast<uint2*>(ma.out + (size_t)slot * ma.I + col) =
-                    uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    uint2{pack_f16x2(v[0], v[1]), pack_f16x2(v[2], v[3])};
             }
         } else {
 #pragma unroll
@@ -273,10 +285,11 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
                 uint16_t* o = ma.out + (size_t)slot * ma.H + n;
                 const f32x16_v& lo = acc[a][0];
                 const f32x16_v& hi = acc[a][1];
+                // the activation is act / 16, so the sums are the slot / 16: stored as is (fp16)
                 *reinterpret_cast<uint2*>(o) =
-                    uint2{pack_bf16x2(lo[4 * q], lo[4 * q + 1]), pack_bf16x2(lo[4 * q + 2], lo[4 * q + 3])};
+                    uint2{pack_f16x2(lo[4 * q], lo[4 * q + 1]), pack_f16x2(lo[4 * q + 2], lo[4 * q + 3])};
                 *reinterpret_cast<uint2*>(o + 8) =
-                    uint2{pack_bf16x2(hi[4 * q], hi[4 * q + 1]), pack_bf16x2(hi[4 * q + 2], hi[4 * q + 3])};
+                    uint2{pack_f16x2(hi[4 * q], hi[4 * q + 1]), pack_f16x2(hi[4 * q + 2], hi[4 * q + 3])};
             }
         }
     }

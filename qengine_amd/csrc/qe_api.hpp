@@ -53,6 +53,7 @@ void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
 void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st);
 // 17..32 rows in one pass (INT4, x 16-byte aligned, ldx % 8 == 0); the rows' bits equal the 16-row launches'
 void skinny_w4_wide(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
+bool skinny_w4_wide_fits(const W4& w, const uint16_t* x, int ldx);
 // the same kernel on W8 / Q8 records (GLU for Q8): m = 1..16, x 16-byte aligned, ldx % 8 == 0
 void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st);
 // m = 1 decode GEMV on the matrix cores (gemv1.hip); false when the shape takes the VALU GEMV (uneven K slices,
@@ -88,6 +89,14 @@ const QeConfig& qe_config();
 void qe_config_set(const QeConfig& c);
 void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 
+// ---- library-owned workspaces, one per (kind, device, stream) (workspace.cpp) ----
+enum WsKind : int { kWsSplit = 0, kWsI8 = 1, kWsH = 2, kNumWs = 3 };
+// the buffer of (kind, current device, st), at least `bytes`: grown outside graph capture (the outgrown one kept
+// allocated); nullptr during capture when it is too small
+void* stream_ws(int kind, size_t bytes, hipStream_t st);
+void stream_ws_reserve(int kind, size_t bytes, hipStream_t st);
+int stream_ws_count(int kind);  // buffers of that kind allocated so far (all devices and streams)
+
 // ---- prefill GEMM (bf16 MFMA on dequantized tiles staged in LDS) ----
 // tuned: time the candidates on the first call of a (shape, token bucket) outside graph capture (also when the
 // config's gemm_tune is set); otherwise the stored choice, else the cost model
@@ -102,17 +111,17 @@ void gemm_w4_choice(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, i
 bool gemm_split_applies(int cfg, int n, int k, int t, int ks);
 // the reference's fp16-accumulate prefill numerics (gemm_h.hip); gemm_h_reserve sizes its pre-pass buffer
 void gemm_w4h(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
-void gemm_h_reserve(int k, int t);
+void gemm_h_reserve(int k, int t, hipStream_t st);
 // the reference's W4A8 prefill numerics (gemm_i8.hip): activation group G in {32, 64, 128}
 // q8: the matrix is in the Q8 layout (signed int8 weights, W8A8)
 void gemm_w4_i8(const W4& w, const uint16_t* x, int ldx, void* c, int ldc, int t, int G, bool out_bf16, hipStream_t st,
                 bool q8 = false);
-void gemm_i8_reserve(int k, int t);
+void gemm_i8_reserve(int k, int t, hipStream_t st);
 // the reference's W8A8 row GEMM of a W8 matrix (k_x_to_r8 + k_rows_qt), on the same pre-pass buffer
 void gemm_w8a8(const W8& w, const uint16_t* x, int ldx, void* c, int ldc, int t, bool out_bf16, hipStream_t st);
 void gemm_set_out_bf16(bool on);
-// reserve the split-K workspace of the current device (grown on demand otherwise, never during graph capture)
-void gemm_reserve(size_t bytes);
+// reserve the split-K workspace of (the current device, st) (grown on demand otherwise, never during graph capture)
+void gemm_reserve(size_t bytes, hipStream_t st);
 bool gemm_out_bf16();
 
 // GEMV for m <= 32 (split into row blocks of 16), GEMM above (reference gemv.cuh:187-190)

@@ -55,6 +55,8 @@ constexpr int kMatmulGemvRows = 64;
 #ifdef __HIPCC__
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_v;
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_v;
+typedef _Float16 f16x2_v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8_v __attribute__((ext_vector_type(8)));
 typedef __attribute__((ext_vector_type(4))) float f32x4_v;
 typedef __attribute__((ext_vector_type(16))) float f32x16_v;
 
@@ -77,5 +79,17 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     const f32x2_v v = {lo, hi};
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
+// two floats -> an fp16 pair, round to nearest even (gfx950 v_cvt_pk_f16_f32); fp16 bits -> float (exact)
+__device__ __forceinline__ uint32_t pack_f16x2(float lo, float hi) {
+    typedef __attribute__((ext_vector_type(2))) float f32x2_v;
+    const f32x2_v v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2_v));
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t v) { return (float)__builtin_bit_cast(_Float16, v); }
+__device__ __forceinline__ float f16_round(float f) { return (float)(_Float16)f; }
+__device__ __forceinline__ uint16_t f32_to_f16(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }
+// MoE intermediates (the GLU activation and the per-(token, k) down outputs) are fp16 of the value / 16, the
+// reference's formats (its XH activation scale and kSlotScale, flash_kernels.cuh:6185,6308,6421-6427)
+constexpr float kMoeF16Scale = 0.0625f;
 __device__ __forceinline__ float silu_f32(float x) { return x / (1.f + __expf(-x)); }
 #endif

@@ -479,6 +479,12 @@ void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, i
     else qe_skinny::launch<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }
 
+// whether skinny_w4_wide runs its rows as one launch: 16-byte aligned rows and an even K slicing (the uneven-slice
+// variant's 16 waves x 32 staged rows exceed the LDS, so those shapes take two 16-row launches)
+bool skinny_w4_wide_fits(const W4& w, const uint16_t* x, int ldx) {
+    return ((uintptr_t)x & 15) == 0 && ldx % 8 == 0 && qe_gemv::decode_groups(w.n, w.k) > 0;
+}
+
 // 17..32 activation rows in one pass over the weights (two 16-row B blocks per MFMA A operand)
 void skinny_w4_wide(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
     CHECK(w.n > 0 && w.k > 0 && w.n % 16 == 0 && w.k % 128 == 0 && m > kMaxGemvRows && m <= kWideRows,

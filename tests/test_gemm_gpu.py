@@ -12,8 +12,8 @@ import torch
 
 import oracle
 from qengine_amd import call, ops, synth
-from test_gemv_gpu import (TOL, assert_bf16_close, assert_glu_close, err_ratio, exact_w4, glu_act, matmul_f64,
-                           oracle_ref, oracle_ref_w8, out_f32)
+from test_gemv_gpu import (TOL, assert_bf16_close, assert_gate, assert_glu_close, assert_rn_of, err_ratio, exact_w4,
+                           glu_act, matmul_f64, oracle_ref, oracle_ref_w8, out_f32)
 
 pytestmark = pytest.mark.gpu
 
@@ -123,13 +123,19 @@ def test_gemm_w4_baseline_shapes_sampled(dev, n, k):
     w, q, s = setup(n, k, 1, seed=n)
     x = synth.x_dev(t, k, seed=3)
     y = ops.gemm_w4(w, x, out_bf16=True)
-    torch.cuda.synchronize()
     rows = np.random.default_rng(4).choice(t, 48, replace=False)
     rows.sort()
-    xh = synth.bits(x[torch.from_numpy(rows).to(dev)].contiguous())
+    sel = torch.from_numpy(rows).to(dev)
+    y = y[sel].contiguous()
+    y32 = ops.gemm_w4(w, x)[sel].contiguous()
+    torch.cuda.synchronize()
+    xh = synth.bits(x[sel].contiguous())
+    # the GEMM multiplies the reference's operand bf16_rn((u - 8) s): ref = that dequantization, product in float64
     ref = oracle_ref(xh, q, s, n, k, 1)
-    yr = out_f32(y[torch.from_numpy(rows).to(dev)].contiguous())
-    assert_bf16_close(yr, ref)
+    assert_gate(y32.cpu().numpy(), ref, f"C2 n={n} k={k} fp32 out")
+    assert_gate(out_f32(y), ref, f"C2 n={n} k={k} bf16 out")
+    assert_rn_of(y, y32.cpu().numpy(), "C2")
+    assert err_ratio(y32.cpu().numpy(), ref) <= 1e-4
 
 
 @pytest.mark.parametrize("per_channel", [True, False])
@@ -154,11 +160,16 @@ def test_gemm_w8_baseline_shape_sampled(dev):
     w = ops.tile_w8(synth.to_dev(q), synth.to_dev(s, torch.float16), True)
     x = synth.x_dev(t, k, seed=78)
     y = ops.gemm_w8(w, x, out_bf16=True)
-    torch.cuda.synchronize()
     rows = np.sort(np.random.default_rng(5).choice(t, 48, replace=False))
     sel = torch.from_numpy(rows).to(dev)
+    y = y[sel].contiguous()
+    y32 = ops.gemm_w8(w, x)[sel].contiguous()
+    torch.cuda.synchronize()
     ref = oracle_ref_w8(synth.bits(x[sel].contiguous()), q, s, n, k, True)
-    assert_bf16_close(out_f32(y[sel].contiguous()), ref)
+    # per-channel scales: max|y| ~ 20 rms, so the unrelaxed gate is on the fp32 output and the bf16 output is its RN
+    assert_gate(y32.cpu().numpy(), ref, "C3 M=4096 W8A16 fp32 out")
+    assert_rn_of(y, y32.cpu().numpy(), "C3 M=4096")
+    assert_bf16_close(out_f32(y), ref)
 
 
 # n = 40960, t = 512: 2 x 160 tiles of 256 x 256 on 256 CUs leave a last round of 64 tiles, which the split runs as

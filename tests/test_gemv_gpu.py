@@ -37,6 +37,23 @@ def assert_bf16_close(y, ref, tol=TOL):
     assert np.all(np.abs(y - ref) <= bound), float((np.abs(y - ref) / bound).max())
 
 
+def assert_gate(y, ref, what, tol=TOL):
+    """the BASELINE gate as stated, with no allowance: max|y - ref| <= tol * rms(ref), ref = the fp32 dequantize-then-
+    matmul reference on the weight operand the kernel multiplies; prints the ratio"""
+    r = err_ratio(y, ref)
+    print(f"gate {what}: max|y - ref| / rms(ref) = {r:.3e}", flush=True)
+    assert r <= tol, (what, r)
+    return r
+
+
+def assert_rn_of(y_bf16, y_f32, what):
+    """a bf16 output equals the round-to-nearest-even of the same call's fp32 output, bit for bit (so the gate on the
+    fp32 output covers the bf16 output up to its own rounding, <= 2^-9 |y|)"""
+    want = synth.np_bf16(np.asarray(y_f32, np.float32))
+    got = synth.bits(y_bf16) if isinstance(y_bf16, torch.Tensor) else np.asarray(y_bf16)
+    assert np.array_equal(got, want), (what, int(np.sum(got != want)))
+
+
 def ref_gate(y, ref):
     """reference tests/test_gemv.py:84 gate"""
     return float(np.abs(np.asarray(y, np.float64) - ref).max() / np.abs(ref).max())
@@ -185,6 +202,49 @@ def test_reference_named_hooks(dev):
     assert err_ratio(y.cpu().numpy(), matmul_f64(xh32, exact_w4(q, s, n, k, 0))) <= 1e-4
 
 
+# the reference's row counts for its skinny == GEMV test (reference tests/test_skinny.py:13)
+MS_SKINNY = [1, 2, 5, 8, 9, 12, 15, 16, 17, 20, 24, 25, 31, 32]
+
+
+@pytest.mark.parametrize("n,k", [(5120, 5120), (2048, 1280)])
+def test_skinny_hook_bit_identical_to_gemv_w4g(dev, n, k):
+    """the reference's skinny test (tests/test_skinny.py:16-41) bound to this library: qe_skinny_w4 returns 1 for
+    every m in its MS list (1..32, the reference's skinny_w4 range, skinny.cu:572) and its outputs equal qe_gemv_w4g's
+    bit for bit, plain (fp32) and GLU (bf16 act); plain outputs within 1e-4 rms of the exact product"""
+    for glu in (0, 1):
+        w, q, s = setup_w4(n, k, 0, seed=71 + glu, glu=bool(glu))
+        xh = synth.x_host(32, k, seed=72 + glu)
+        ref_ex = matmul_f64(xh, exact_w4(q, s, n, k, 0))
+        for m in MS_SKINNY:
+            x = synth.to_dev(xh[:m])
+            cols, dt = (n // 2, torch.bfloat16) if glu else (n, torch.float32)
+            y0 = torch.full((m, cols), float("nan"), dtype=dt, device=dev)
+            y1 = y0.clone()
+            call("qe_gemv_w4g", w.q, w.s, n, k, x, y0, m, glu)
+            r = call("qe_skinny_w4", w.q, w.s, n, k, x, y1, m, glu)
+            torch.cuda.synchronize()
+            assert r == 1, (glu, m)
+            iv = torch.int16 if glu else torch.int32
+            assert torch.equal(y0.view(iv), y1.view(iv)), (glu, m)
+            if not glu:
+                assert err_ratio(y1.cpu().numpy(), ref_ex[:m]) <= 1e-4, m
+
+
+def test_skinny_hook_unsupported_returns_0(dev):
+    """17..32 rows need an even K slicing for the one-launch wide kernel: K / 128 = 63 has none, so qe_skinny_w4
+    returns 0 there (the reference's "unsupported", its callers fall back to gemv_w4) and writes nothing; 1..16 rows
+    run"""
+    n, k = 1024, 8064
+    w, q, s = setup_w4(n, k, 0, seed=73)
+    x = synth.to_dev(synth.x_host(20, k, seed=74))
+    for m, want in ((16, 1), (17, 0), (20, 0)):
+        y = torch.full((m, n), float("nan"), device=dev)
+        r = call("qe_skinny_w4", w.q, w.s, n, k, x[:m], y, m, 0)
+        torch.cuda.synchronize()
+        assert r == want, m
+        assert bool(torch.isnan(y).all()) == (want == 0), m
+
+
 @pytest.mark.parametrize("n,k", [(5120, 5120), (17408, 5120)])
 @pytest.mark.parametrize("m", [1, 2, 4, 8, 16])
 def test_gemv_w4_baseline_shapes(dev, n, k, m):
@@ -193,8 +253,20 @@ def test_gemv_w4_baseline_shapes(dev, n, k, m):
         pytest.skip("not a BASELINE shape")
     w, q, s = setup_w4(n, k, 1, seed=1000 + n)
     xh = synth.x_host(m, k, seed=2000 + m)
-    y = out_f32(ops.gemv_w4(w, synth.to_dev(xh), out_bf16=True))
-    assert_bf16_close(y, oracle.matmul_bf16(xh, oracle.dequant_w4(q, s, n, k, 1)))
+    x = synth.to_dev(xh)
+    y16 = ops.gemv_w4(w, x, out_bf16=True)
+    y32 = ops.gemv_w4(w, x)
+    torch.cuda.synchronize()
+    # the decode kernels multiply the unrounded weights (u - 8) * s: ref = that exact fp32 dequantization, product in
+    # float64; the gate holds on the fp32 and on the bf16 output, and the bf16 output is the RN of the fp32 one
+    ref_ex = matmul_f64(xh, exact_w4(q, s, n, k, 1))
+    assert_gate(y32.cpu().numpy(), ref_ex, f"C0/C1 m={m} n={n} fp32 out")
+    assert_gate(out_f32(y16), ref_ex, f"C0/C1 m={m} n={n} bf16 out")
+    assert_rn_of(y16, y32.cpu().numpy(), "C0/C1")
+    assert err_ratio(y32.cpu().numpy(), ref_ex) <= 1e-4
+    # against the reference's bf16-rounded weight operand: the weight rounding (~2^-9 relative per weight) plus the
+    # output's own rounding
+    assert_bf16_close(out_f32(y16), oracle.matmul_bf16(xh, oracle.dequant_w4(q, s, n, k, 1)))
 
 
 @pytest.mark.parametrize("n,k", [(16, 128), (48, 384), (80, 640)])
@@ -266,6 +338,10 @@ def test_gemv_w8_parity(dev, per_channel, n, k):
         assert_bf16_close(out_f32(y), ref[:m])
         y32 = ops.gemv_w8(w, x[:m])
         torch.cuda.synchronize()
+        # the unrelaxed gate on the fp32 output (per-channel scales make the outputs heavy-tailed: max|y| ~ 20 rms,
+        # so a bf16 output's own rounding, up to 2^-9 |y|, alone can exceed 2e-2 rms); the bf16 output is its RN
+        assert_gate(y32.cpu().numpy(), ref_ex[:m], f"W8 m={m} n={n} k={k} pc={per_channel} fp32 out")
+        assert_rn_of(y, y32.cpu().numpy(), "W8 GEMV")
         if m == 1:  # the VALU GEMV at short slices (m >= 2: the matrix-core kernel, the same rows for every m)
             assert err_ratio(y32.cpu().numpy(), full.cpu().numpy()[:1]) <= 1e-5
         else:

@@ -85,6 +85,12 @@ def test_header_parser_on_handmade_json(tmp_path):
     ('{"a": {"dtype": "F32", "shape": [1], "data_offsets": [0, 4]}', bytes(4), "JSON header"),
     ('{"a": {"dtype": "F32", "shape": [1.5], "data_offsets": [0, 4]}}', bytes(4), "non-integer"),
     ('{"a": {"dtype": "F32", "shape": [1]}}', bytes(4), "malformed entry"),
+    # dims whose product wraps past 64 bits (2^36 * 2^32) to 0 elements, with empty data_offsets
+    ('{"q": {"dtype": "I32", "shape": [68719476736, 4294967296], "data_offsets": [0, 0]}}', bytes(8), "overflows"),
+    # no wrap of the count, but of the byte size (2^39 * 2^24 elements of 4 bytes = 2^65)
+    ('{"q": {"dtype": "F32", "shape": [549755813888, 16777216], "data_offsets": [0, 8]}}', bytes(8), "byte size"),
+    # no wrap, more bytes than the file holds (2^39 * 2^20 fp32)
+    ('{"q": {"dtype": "F32", "shape": [549755813888, 1048576], "data_offsets": [0, 8]}}', bytes(8), "data_offsets"),
 ])
 def test_malformed_files_abort_with_message(tmp_path, header, data, msg):
     p = handmade(tmp_path, header, data)

@@ -1,17 +1,20 @@
 """MoE grouped INT4 expert layer through the C-ABI vs the CPU oracle: routing and segmentation bit-exact, packed
-records bit-exact, the layer within 2e-2 * rms(ref) plus the output's own rounding.
+records bit-exact, the layer within 2e-2 * rms(ref) (BASELINE shapes and multi-job experts: on the fp32 output, no
+allowance; smaller cases on bf16 outputs plus the output's own rounding).
 
-The layer keeps two bf16 intermediates, as the reference keeps fp16 ones (the GLU activation, flash_kernels.cuh:6185,
-and the per-(token, k) down slots, :6421-6427). Every path (decode T <= 32, prefill T > 32) multiplies the reference's
-weight operand bf16_rn((u - 8) * s), so every path is compared with the oracle on the bf16-dequantized weights, and
-the two paths agree on the same tokens up to fp32 summation order (test_moe_decode_prefill_boundary)."""
+The layer keeps the reference's two fp16 intermediates (the GLU activation, flash_kernels.cuh:6185, and the
+per-(token, k) down slots, :6421-6427), both as fp16 of the value / 16. Every path (decode T <= 32, prefill T > 32)
+multiplies the same weight operands, gate_up bf16_rn((u - 8) * s) on the bf16 input and down fp16_rn((u - 8) * s) on
+the fp16 activation, so every path is compared with the oracle on those operands (oracle.moe_ref, float64, no
+intermediate rounding), and the two paths agree on the same tokens up to fp32 summation order
+(test_moe_decode_prefill_boundary)."""
 import numpy as np
 import pytest
 import torch
 
 import oracle
 from qengine_amd import ops, synth
-from test_gemv_gpu import assert_bf16_close, out_f32
+from test_gemv_gpu import assert_bf16_close, assert_gate, assert_rn_of, out_f32
 
 pytestmark = pytest.mark.gpu
 
@@ -107,29 +110,6 @@ def test_moe_decode_fused_down_combine_bit_exact(dev):
     assert_bf16_close(y1, ref)
 
 
-def pipeline_ref(lg, xh, gq, gs, dq, ds, topk, H, I):
-    """this build's layer numerics on the oracle's bf16-dequantized experts (float64 products): act =
-    bf16(silu(gate) up w_k) (gate_up epilogue), slot = bf16(down . act) (down epilogue), out = bf16 of the fp32 sum
-    over k in order (combine). The float64 oracle (moe_ref) has no intermediate rounding; with every token on every
-    expert the two bf16 stores alone can exceed the BASELINE gate on a few outputs, so the multi-job test checks the
-    kernels against this model instead."""
-    def bf(a):
-        return oracle.bf16_to_f32(synth.np_bf16(np.asarray(a, np.float64))).astype(np.float64)
-    sel, w = oracle.moe_route(lg, topk)
-    xf = oracle.bf16_to_f32(xh).astype(np.float64)
-    E = gq.shape[0]
-    W = [(oracle.bf16_to_f32(oracle.dequant_w4(gq[e], gs[e], 2 * I, H, 1)).astype(np.float64),
-          oracle.bf16_to_f32(oracle.dequant_w4(dq[e], ds[e], H, I, 1)).astype(np.float64)) for e in range(E)]
-    out = np.zeros((lg.shape[0], H), np.float32)
-    for t in range(lg.shape[0]):
-        for k in range(topk):
-            wgu, wdn = W[int(sel[t, k])]
-            gu = wgu @ xf[t]
-            act = bf(gu[:I] / (1 + np.exp(-gu[:I])) * gu[I:] * float(w[t, k]))
-            out[t] += bf(wdn @ act).astype(np.float32)
-    return bf(out)
-
-
 def test_moe_decode_fused_route_gate_up_bit_exact(dev):
     """T <= 4 routes inside the gate_up blocks (no segmentation: slot = pair), T = 5 routes, segments and runs the
     grouped gate_up; with T * topk <= 64 both take the same gate_up K slicing and the fused down + combine, and every
@@ -149,9 +129,10 @@ def test_moe_decode_fused_route_gate_up_bit_exact(dev):
 
 
 def test_moe_decode_prefill_boundary(dev):
-    """T <= 32 runs the decode kernels, T >= 33 the prefill GEMMs; both multiply the reference's weight operand
-    bf16_rn((u - 8) s) and keep bf16 act / slot intermediates, so the same 32 tokens through both paths differ only by
-    fp32 summation order (an intermediate's bf16 rounding can flip)"""
+    """T <= 32 runs the decode kernels, T >= 33 the prefill GEMMs; both multiply the same weight operands and keep the
+    same fp16 act / slot intermediates, so the same 32 tokens through both paths differ only by fp32 summation order
+    (an intermediate's fp16 rounding can flip: fp16 steps are 8x finer than bf16 ones, so flips are more frequent and
+    each moves the result 8x less)"""
     E, topk, H, I = 64, 10, 2048, 512
     gq, gs, dq, ds = synth.moe_host(E, H, I, seed=51)
     moe = ops.MoE.pack(synth.to_dev(gq), synth.to_dev(gs, torch.float16), synth.to_dev(dq),
@@ -166,28 +147,20 @@ def test_moe_decode_prefill_boundary(dev):
     ref, _, _ = oracle.moe_ref(lgh[:32], xh[:32], gq, gs, dq, ds, topk, H, I)
     rms = np.sqrt(np.mean(ref.astype(np.float64) ** 2))
     d = y33[:32].astype(np.float64) - y32
-    # measured: max 6.7e-3 rms, rms 8.3e-5 rms, 98.5 % bit-equal (exact against bf16-rounded weights: max 3.0e-2)
-    assert np.abs(d).max() <= 1.5e-2 * rms, float(np.abs(d).max() / rms)
-    assert np.sqrt(np.mean(d ** 2)) <= 5e-4 * rms, float(np.sqrt(np.mean(d ** 2)) / rms)
-    assert np.mean(y33[:32] == y32) >= 0.95, float(np.mean(y33[:32] == y32))
+    dmax, drms, eq = np.abs(d).max() / rms, np.sqrt(np.mean(d ** 2)) / rms, np.mean(y33[:32] == y32)
+    print(f"decode vs prefill: max {dmax:.2e} rms, rms {drms:.2e} rms, {eq:.3f} bit-equal", flush=True)
+    # with bf16 intermediates this was max 6.7e-3 rms, rms 8.3e-5 rms, 98.5 % bit-equal
+    assert dmax <= 5e-3 and drms <= 1e-4, (dmax, drms)
+    assert eq >= 0.75, eq
 
 
 @pytest.mark.parametrize("T,E", [(300, 8), (700, 4)])
 def test_moe_layer_multi_job(dev, T, E):
-    """prefill experts with more rows than one job (128 rows): ~150 and 700 rows per expert. Against the layer's own
-    rounding model: bit-equal up to a flipped bf16 rounding of an intermediate (fp32 summation order)."""
+    """prefill experts with more rows than one job (128 rows): ~150 and 700 rows per expert, the unrelaxed gate on the
+    fp32 output against the oracle"""
     seed = T + E
-    y, ref, *_ = _layer(dev, T, E=E, topk=4, H=512, I=256, seed=seed)
-    gq, gs, dq, ds = synth.moe_host(E, 512, 256, seed=seed)
-    sim = pipeline_ref(synth.logits_host(T, E, seed=seed + 1), synth.x_host(T, 512, seed=seed + 2), gq, gs, dq, ds,
-                       4, 512, 256)
-    rms = np.sqrt(np.mean(ref ** 2))
-    # a flipped rounding moves one slot by an ulp of its own size, which a cancelling sum need not dwarf: bit-equal
-    # almost everywhere, the rest within the gate
-    assert np.mean(y == sim) >= 0.99, float(np.mean(y == sim))
-    assert np.abs(y - sim).max() <= 2e-2 * rms, float(np.abs(y - sim).max() / rms)
-    if E == 8:
-        assert_bf16_close(y, ref)
+    y, ref, *_ = _layer(dev, T, E=E, topk=4, H=512, I=256, seed=seed, out_bf16=False)
+    assert_gate(y, ref, f"MoE multi-job T={T} E={E} fp32 out")
 
 
 def test_moe_layer_fp32_out_deterministic(dev):
@@ -200,10 +173,17 @@ def test_moe_layer_fp32_out_deterministic(dev):
 
 @pytest.mark.parametrize("T", [1, 16, 4096])
 def test_moe_layer_baseline(dev, T):
-    """512 experts, top-10, H = 2048, I = 512 (T = 4096: 24 sampled tokens)"""
+    """512 experts, top-10, H = 2048, I = 512 (T = 4096: 24 sampled tokens). The unrelaxed gate
+    on the fp32 output against the float64 layer on the reference's weight operand (oracle.moe_ref, pinned by an
+    independent torch composition on the CPU); the bf16 output is the RN of the fp32 one"""
     tokens = None if T <= 16 else np.sort(np.random.default_rng(7).choice(T, 24, replace=False))
-    y, ref, *_ = _layer(dev, T, E=512, topk=10, H=2048, I=512, seed=100 + T, tokens=tokens)
-    assert_bf16_close(y, ref)
+    y32, ref, moe, lg, xh = _layer(dev, T, E=512, topk=10, H=2048, I=512, seed=100 + T, tokens=tokens,
+                                   out_bf16=False)
+    assert_gate(y32, ref, f"C4 T={T} fp32 out")
+    y16 = moe(torch.from_numpy(lg).to(dev), synth.to_dev(xh), out_bf16=True)
+    torch.cuda.synchronize()
+    y16 = synth.bits(y16)
+    assert_rn_of(y16 if tokens is None else y16[tokens], y32, f"C4 T={T}")
 
 
 @pytest.mark.parametrize("T", [1, 16, 40])

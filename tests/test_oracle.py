@@ -124,6 +124,20 @@ def test_dequant_w4_closed_form(sdt):
     assert np.array_equal(oracle.dequant_w4(q, s, n, k, sdt), ref)
 
 
+def test_dequant_w4_f16_closed_form():
+    """fp16_rn((u - 8) * s) (the MoE down operand) through torch: (unpack * s.repeat_interleave(128)).half(), with
+    tiny scales (fp16 subnormal products) and large ones"""
+    n, k = 48, 384
+    q, s = synth.w4_host(n, k, seed=6, sdt=1)
+    s[0, :] = np.array([1e-6], np.float16).view(np.uint16)[0]
+    s[1, :] = np.array([4000.0], np.float16).view(np.uint16)[0]
+    w = torch.from_numpy(oracle.unpack_w4(q, n, k).astype(np.float32))
+    sf = torch.from_numpy(oracle.f16_to_f32(s)).repeat_interleave(128, dim=1)
+    ref = (w * sf).half().float().numpy()
+    got = oracle.dequant_w4_f16(q, s, n, k)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
 def test_glu_rows_matches_interleave_closed_form():
     """reference tests/test_q8.py:75-79: stack([gate.reshape(-1, 8, k), up.reshape(-1, 8, k)], 1)"""
     n, k = 64, 256
@@ -280,6 +294,78 @@ def test_moe_pack_decodes_to_source_rows():
             ud = _decode_w4_fragments(parts[2].view(np.uint32), H, 128)
             assert np.array_equal(ud, oracle.unpack_w4(dq[e], H, I)[:, 128 * g:128 * g + 128] + 8)
             assert np.array_equal(parts[3].view(np.uint16), ds[e][:, g])
+
+
+def _moe_layer_torch(lg, xh, gq, gs, dq, ds, topk, H, I, plant=None):
+    """one MoE layer composed independently of the oracle, in float64 torch:
+      * routing: numpy lexsort on (-logit, expert index) (value desc, index asc: flash_kernels.cuh:4006-4089), weights
+        softmax(logits) renormalised over the selection;
+      * experts: the reference test's unpack ((q >> 4 j) & 15) - 8 (tests/test_gemv.py:13-15) times the fp16 group
+        scale, rounded by torch to bf16 for gate_up (tests/test_gemv.py:36) and to fp16 for down (the operands the
+        layer's kernels multiply); rows [0, I) of gate_up are the gate, [I, 2I) the up (the loader's "gate rows, then
+        up rows", flash.cu:1564-1565);
+      * out[t] = sum_k w_k * W_down (silu(W_gate x) * (W_up x)) (the routing weight scales the activation,
+        flash_kernels.cuh:6185; down is linear, so that equals scaling the expert output).
+    plant: a deliberate mistake, to show that the comparison can fail: "swap" (silu on the up half), "w_in_silu"
+    (silu(w gate) up), "no_renorm" (softmax over all experts, not renormalised), "ties_high" (ties broken by the
+    higher index), "drop_k" (the last selected expert left out)."""
+    import torch.nn.functional as F
+    T, E = lg.shape
+    x = torch.from_numpy(oracle.bf16_to_f32(xh).astype(np.float64))
+
+    def deq(q, s, n, k, half=False):
+        wp = torch.from_numpy(q)
+        u = ((wp.unsqueeze(-1) >> torch.arange(0, 32, 4, dtype=torch.int32)) & 15).reshape(n, k) - 8
+        sf = torch.from_numpy(s.view(np.float16).astype(np.float32)).repeat_interleave(128, dim=1)
+        w = u.float() * sf
+        return (w.half() if half else w.bfloat16()).double()
+
+    out = torch.zeros(T, H, dtype=torch.float64)
+    for t in range(T):
+        idx = np.arange(E)
+        order = np.lexsort((E - idx if plant == "ties_high" else idx, -lg[t].astype(np.float64)))[:topk]
+        p = np.exp(lg[t].astype(np.float64) - lg[t].max())
+        p /= p.sum()
+        wk = p[order] if plant == "no_renorm" else p[order] / p[order].sum()
+        for j, e in enumerate(order[:topk - 1] if plant == "drop_k" else order):
+            wgu = deq(gq[e], gs[e], 2 * I, H)
+            gate, up = wgu[:I] @ x[t], wgu[I:] @ x[t]
+            if plant == "swap":
+                gate, up = up, gate
+            if plant == "w_in_silu":
+                act = F.silu(wk[j] * gate) * up
+            else:
+                act = F.silu(gate) * up * wk[j]
+            out[t] += deq(dq[e], ds[e], H, I, half=True) @ act
+    return out.numpy()
+
+
+@pytest.mark.parametrize("topk,ties", [(1, False), (2, True), (3, False)])
+def test_moe_ref_matches_independent_torch_layer(topk, ties):
+    """oracle.moe_ref (the only checker of the MoE layer) against the independent float64 torch composition above.
+    topk = 1: every routing weight is exactly 1; topk = 2 with three tied top logits: the two lowest-index ones are
+    selected with weights exactly 0.5 (the k-sum and the tie rule); topk = 3: general weights (the oracle's fp32
+    routing weights, 1e-7 relative). Each planted mistake moves the result far past the agreement bound."""
+    E, H, I, T = 8, 256, 128, 4
+    gq, gs, dq, ds = synth.moe_host(E, H, I, seed=17 + topk)
+    lg = synth.logits_host(T, E, seed=23 + topk)
+    if ties:
+        for t in range(T):
+            lg[t, [1, 4, 6]] = lg[t].max() + 0.5
+    xh = synth.x_host(T, H, seed=29 + topk)
+    got, sel, w = oracle.moe_ref(lg, xh, gq, gs, dq, ds, topk, H, I)
+    want = _moe_layer_torch(lg, xh, gq, gs, dq, ds, topk, H, I)
+    rms = np.sqrt(np.mean(want ** 2))
+    bound = 1e-12 if topk <= 2 else 1e-6
+    assert np.abs(got - want).max() <= bound * rms, float(np.abs(got - want).max() / rms)
+    if topk == 1:
+        assert np.all(w == 1.0)
+    if ties:
+        assert np.all(sel == [1, 4]) and np.all(w == 0.5)
+    plants = ["swap", "no_renorm", "drop_k"] + (["w_in_silu", "ties_high"] if ties else [])
+    for plant in plants:
+        bad = _moe_layer_torch(lg, xh, gq, gs, dq, ds, topk, H, I, plant=plant)
+        assert np.abs(got - bad).max() > 0.05 * rms, (plant, float(np.abs(got - bad).max() / rms))
 
 
 # ---------------------------------------------------------------- Q8 layout (reference src/kernels/q8_layout.h)
