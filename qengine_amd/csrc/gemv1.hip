@@ -21,6 +21,7 @@
 //     DPP, and the K slices (waves) through LDS in a fixed order: deterministic.
 // Per lane and group that is 28 VALU for the unpack and 8 for the scales, against about 60 for the VALU GEMV.
 #include "gemv_impl.hpp"
+#include "mfma_tile.hpp"
 
 namespace qe_gemv1 {
 using namespace qe_gemv;
@@ -205,14 +206,182 @@ gemv1_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N,
     }
 }
 
+
+// ---- the streaming variant (long K slices): per wave a K slice of NG groups streamed through a window of D records,
+// the slice's activations and scales staged into LDS by DMA in their natural order (no VALU), each B operand gathered
+// by two ds_read2_b32 (dwords 32 h + t + {0, 4, 8, 12} of a group: the class (h, t) of words 0 / 1, and + 16 for words
+// 2 / 3), the bias -136 x (class sum) by two MFMAs on the same B operands (A = -136). Measured on the C0 shape
+// (N = 17408, K = 5120) against the kernel above in the same processes: 8-14 % faster on the boxes whose GEMV runs
+// slowest (10.1-11.8 us -> 9.4-10.4 us), within 1 % (slower) on the fastest ones (9.1-9.3 us); longer slices with a
+// small window do best (a deeper window leaves each wave a backlog of arrived groups to compute after the stream
+// ends), and fewer waves carry less per-wave set-up.
+template <int NG>
+constexpr int st_xbytes() { return (NG * 256 + 1023) / 1024 * 1024; }
+template <int NG>
+constexpr int st_wbytes() { return st_xbytes<NG>() + 1024 + 256; }  // x, scales (NG x 32 B <= 1 KB), zeros
+
+template <int NG, int D, int SDT>
+__global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
+gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K,
+              const uint16_t* __restrict__ x, void* __restrict__ y, int out) {
+    static_assert(NG * 32 <= 1024 && D >= 1 && D <= 4 && D < NG, "gemv1s slice");
+    constexpr int XB = st_xbytes<NG>(), WB = st_wbytes<NG>();
+    extern __shared__ __attribute__((aligned(16))) char lds8[];
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const int tile = blockIdx.x, G = K >> 7, gb = w * NG;
+    char* wl = lds8 + (size_t)w * WB;
+    const unsigned wl32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)wl);
+    float* red = reinterpret_cast<float*>(lds8 + (size_t)S * WB);  // [S][16]
+
+    // 1. DMAs of the slice's activations (1 KB per instruction; lanes past the slice re-read its last 16 bytes into
+    //    the padding) and scales (NG x 32 B), then the first D weight records; the zero area for the lanes off the
+    //    diagonal. The DMAs are the oldest loads, so once at most D are outstanding they have landed.
+    const char* xs0 = reinterpret_cast<const char*>(x) + (size_t)gb * 256;
+#pragma unroll
+    for (int r = 0; r < XB / 1024; r++) {
+        const int p = 64 * r + L < NG * 16 ? 64 * r + L : NG * 16 - 1;
+        qe_tile::dma16(xs0 + 16 * p, wl32 + 1024 * r);
+    }
+    {
+        const int p = L < NG * 2 ? L : NG * 2 - 1;
+        qe_tile::dma16(reinterpret_cast<const char*>(s + ((size_t)tile * G + gb) * 16) + 16 * p, wl32 + XB);
+    }
+    const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + L;
+    u32x4_v wv[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) wv[i] = ld_stream(qp + (size_t)i * 64);
+    reinterpret_cast<uint32_t*>(wl + XB + 1024)[L] = 0u;
+    if constexpr (D == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+    else if constexpr (D == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if constexpr (D == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 2. per group: B operands (diagonal lanes: class (h = qb / 2, t = c % 4); others: zeros), the bias MFMAs, the 4
+    //    weight MFMAs, acc += s * D (the lane's register c % 4 is the useful one, as in gemv1_kernel)
+    const int qb = L >> 4, c = L & 15;
+    const bool diag = (c >> 2) == qb;
+    const uint32_t* bb = diag ? reinterpret_cast<const uint32_t*>(wl) + 32 * (qb >> 1) + (c & 3)
+                              : reinterpret_cast<const uint32_t*>(wl + XB + 1024);
+    const int bstep = diag ? 64 : 0;
+    const int grow = 4 * ((c >> 2) & 1) + qb;
+    const uint16_t* sl = reinterpret_cast<const uint16_t*>(wl + XB);
+    constexpr uint32_t kBias = 0xC308C308u;  // bf16 (-136, -136)
+    const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{kBias, kBias, kBias, kBias});
+    f32x4_v acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NG; i++) {
+        const uint32_t* b = bb + i * bstep;
+        const u32x4_v b01 = {b[0], b[4], b[8], b[12]}, b23 = {b[16], b[20], b[24], b[28]};
+        const bf16x8_v B01 = __builtin_bit_cast(bf16x8_v, b01), B23 = __builtin_bit_cast(bf16x8_v, b23);
+        const float s_lo = scale_to_f32<SDT>(sl[i * 16 + grow]);
+        const float s_hi = scale_to_f32<SDT>(sl[i * 16 + grow + 8]);
+        const u32x4_v r = wv[i % D];
+        u32x4_v t0, t1;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            t0[j] = r[j] & kNib;
+            t1[j] = (r[j] >> 4) & kNib;
+        }
+        auto opnd = [&](const u32x4_v& t, int j) {
+            const u32x4_v a = {bf16x2_b02(t[j]), bf16x2_b13(t[j]), bf16x2_b02(t[j + 1]), bf16x2_b13(t[j + 1])};
+            return __builtin_bit_cast(bf16x8_v, a);
+        };
+        const bf16x8_v A0 = opnd(t0, 0), A1 = opnd(t1, 0), A2 = opnd(t0, 2), A3 = opnd(t1, 2);
+        if (i + D < NG) wv[i % D] = ld_stream(qp + (size_t)(i + D) * 64);
+        f32x4_v cb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, B01, f32x4_v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        cb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, B23, cb, 0, 0, 0);
+        f32x4_v dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B01, cb, 0, 0, 0);
+        f32x4_v dh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A1, B01, cb, 0, 0, 0);
+        dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A2, B23, dl, 0, 0, 0);
+        dh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A3, B23, dh, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            acc_lo[e] = fmaf(s_lo, dl[e], acc_lo[e]);
+            acc_hi[e] = fmaf(s_hi, dh[e], acc_hi[e]);
+        }
+    }
+
+    // 3. the lane's register, the quad and chunk halves by DPP, the slices through LDS in order (as gemv1_kernel)
+    constexpr int kDppRowRor8 = 0x128;
+    float vlo = pick4(acc_lo, (c & 1) != 0, (c & 2) != 0), vhi = pick4(acc_hi, (c & 1) != 0, (c & 2) != 0);
+    vlo = dpp_add<kDppXor1>(vlo);
+    vhi = dpp_add<kDppXor1>(vhi);
+    vlo = dpp_add<kDppXor2>(vlo);
+    vhi = dpp_add<kDppXor2>(vhi);
+    vlo = dpp_add<kDppRowRor8>(vlo);
+    vhi = dpp_add<kDppRowRor8>(vhi);
+    if ((c & 11) == 0) {
+        red[w * 16 + grow] = vlo;
+        red[w * 16 + grow + 8] = vhi;
+    }
+    __syncthreads();
+    const int row0 = 16 * tile;
+    if (out == kOutGLU) {
+        if (threadIdx.x < 8) {
+            const int gg = threadIdx.x;
+            float a = 0.f, b = 0.f;
+            for (int ws = 0; ws < S; ws++) {
+                a += red[ws * 16 + gg];
+                b += red[ws * 16 + gg + 8];
+            }
+            reinterpret_cast<uint16_t*>(y)[row0 / 2 + gg] = f32_to_bf16(silu_f32(a) * b);
+        }
+    } else if (threadIdx.x < 16) {
+        const int rw = threadIdx.x;
+        float v = 0.f;
+        for (int ws = 0; ws < S; ws++) v += red[ws * 16 + rw];
+        if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[row0 + rw] = f32_to_bf16(v);
+        else reinterpret_cast<float*>(y)[row0 + rw] = v;
+    }
+}
+
+// slices of the streaming variant: the fewest waves per tile (S in {2, 4, 8}, S dividing K / 128, NG = K / 128 / S
+// in {5, 8, 10, 16, 20}) whose grid still has >= 8 waves per CU; 0 when none fits (the caller takes gemv1_kernel)
+int stream_groups(int n, int k) {
+    const int tiles = n / 16, G = k / 128;
+    for (int S : {2, 4, 8}) {
+        if (G % S) continue;
+        const int ng = G / S;
+        if (ng != 5 && ng != 8 && ng != 10 && ng != 16 && ng != 20) continue;
+        if ((long)tiles * S >= 8L * qe_num_cus()) return ng;
+    }
+    return 0;
+}
 }  // namespace qe_gemv1
 
-// m = 1 on the matrix cores when K / 128 splits evenly into slices of 10, 8, 5, 4 or 2 groups and x is 16-byte
-// aligned; returns false otherwise (the caller takes the VALU GEMV)
+// m = 1 on the matrix cores (x 16-byte aligned): the streaming kernel where stream_groups finds a slicing, else
+// gemv1_kernel when K / 128 splits evenly into slices of 10, 8, 5, 4 or 2 groups; returns false otherwise (the caller
+// takes the VALU GEMV)
 bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) {
     using namespace qe_gemv1;
+    if (((uintptr_t)x & 15) != 0) return false;
+    const int sng = stream_groups(w.n, w.k);
+    if (sng > 0) {
+        const int S = w.k / 128 / sng;
+        const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
+#define QE_GEMV1S(NG_, SDT_)                                                                                  \
+    gemv1s_kernel<NG_, 3, SDT_><<<grid, block, (size_t)S * st_wbytes<NG_>() + (size_t)S * 64, st>>>(        \
+        w.q, w.s, w.n, w.k, x, y, out)
+#define QE_GEMV1S_NG(SDT_)                          \
+    do {                                            \
+        if (sng == 20) QE_GEMV1S(20, SDT_);         \
+        else if (sng == 16) QE_GEMV1S(16, SDT_);    \
+        else if (sng == 10) QE_GEMV1S(10, SDT_);    \
+        else if (sng == 8) QE_GEMV1S(8, SDT_);      \
+        else QE_GEMV1S(5, SDT_);                    \
+    } while (0)
+        if (w.sdt == kScaleF16) QE_GEMV1S_NG(kScaleF16);
+        else QE_GEMV1S_NG(kScaleBF16);
+#undef QE_GEMV1S_NG
+#undef QE_GEMV1S
+        HIP_CHECK(hipGetLastError());
+        return true;
+    }
     const int ng = decode_groups(w.n, w.k);
-    if (ng == 0 || ((uintptr_t)x & 15) != 0) return false;
+    if (ng == 0) return false;
     const int S = w.k / 128 / ng;
     const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
     // all of a slice's records in flight for slices of up to 5 groups, else a window of 3
