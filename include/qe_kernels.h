@@ -279,7 +279,10 @@ size_t qe_moe_workspace_bytes(int T, int E, int topk, int H, int I);
 size_t qe_moe_record_bytes(int H, int I);
 
 /* one MoE layer: out [T][H] (fp32, or bf16 with QE_OUT_BF16) = sum_k w_k * down_e(silu(gate_e x) * up_e x) for the
- * top-k experts e of each token; logits fp32 [T][E], x bf16 [T][H]. H % 512 == 0, I % 128 == 0. */
+ * top-k experts e of each token; logits fp32 [T][E], x bf16 [T][H]. H % 512 == 0, I % 128 == 0. Numerics: gate_up
+ * multiplies x by bf16_rn((u - 8) s), the activation silu(gate) up w_k is kept as fp16 of act / 16, down multiplies it
+ * by fp16_rn((u - 8) s) and each (token, k) result is kept as an fp16 slot (value / 16), summed in k order in fp32
+ * (the reference's fp16 intermediates, flash_kernels.cuh:6185,6308,6421-6482); deterministic. */
 void qe_moe_w4(const float* logits, const uint16_t* x, const void* records, int T, int E, int topk, int H, int I,
                void* out, int flags, void* workspace, size_t ws_bytes, void* stream);
 
