@@ -155,6 +155,10 @@ void qe_gemv_w4h(const void* q, const void* s, int n, int k, const uint16_t* x, 
                  void* yh);
 /* x already XH, stride ldx */
 void qe_gemv_w4hx(const void* q, const void* s, int n, int k, const uint16_t* xh, float* y, int m, int glu, int ldx);
+/* the wide H16 GEMV (reference src/capi.cpp:72-77, gemv_w4hx): returns 1 when the m rows ran as one launch, 0 (nothing
+ * written) when unsupported: m 1..32 (17..32 rows need an even K slicing; the reference's 33..64 return 0 here, its
+ * callers then take qe_gemv_w4hx), ldx % 64 == 0, xh 16-byte aligned. Bit-identical to qe_gemv_w4hx. */
+int qe_gemv_w4hxx(const void* q, const void* s, int n, int k, const uint16_t* xh, float* y, int m, int glu, int ldx);
 /* build-defined: scales dtype / output bf16 / GLU by flags, explicit strides and stream, optional yh [m][ldyh] */
 void qe_gemv_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* xh, int ldx, void* y, int ldy, int m,
                     int flags, void* yh, int ldyh, void* stream);

@@ -191,6 +191,16 @@ void qe_gemv_w4hx(const void* q, const void* s, int n, int k, const uint16_t* xh
              xh, ldx, y, glu ? n / 2 : n, m, false, nullptr, 0, 0);
 }
 
+// the reference's wide H16 GEMV hook (src/capi.cpp:72-77, gemv_w4hx: 9..64 rows, false when unsupported): here 1 when
+// the rows run as one launch (m <= 32 with the conditions of gemv_h16_one_launch), else 0 and nothing is written
+int qe_gemv_w4hxx(const void* q, const void* s, int n, int k, const uint16_t* xh, float* y, int m, int glu, int ldx) {
+    if (!gemv_h16_one_launch(n, k, false, xh, ldx, m)) return 0;
+    gemv_workspace_init();
+    gemv_h16(reinterpret_cast<const uint4*>(q), reinterpret_cast<const uint16_t*>(s), n, k, kScaleBF16, false, glu != 0,
+             xh, ldx, y, glu ? n / 2 : n, m, false, nullptr, 0, 0);
+    return 1;
+}
+
 void qe_gemv_w4h_ex(const void* q, const void* s, int n, int k, const uint16_t* xh, int ldx, void* y, int ldy, int m,
                     int flags, void* yh, int ldyh, void* stream) {
     gemv_workspace_init();

@@ -24,6 +24,11 @@ void gemv_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     else launch_gemv<kFmtW4, kScaleBF16>(w.q, w.s, w.n, w.k, x, ldx, y, ldy, m, out, w.sdt, st);
 }
 
+bool gemv_h16_one_launch(int n, int k, bool q8, const uint16_t* xh, int ldx, int m) {
+    return !q8 && m >= 1 && m <= kWideRows && n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && ldx >= k &&
+           ldx % 64 == 0 && ((uintptr_t)xh & 15) == 0 && (m <= kMaxGemvRows || decode_groups(n, k) > 0);
+}
+
 void gemv_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8, bool glu, const uint16_t* xh, int ldx,
               void* y, int ldy, int m, bool out_bf16, uint16_t* yh, int ldyh, hipStream_t st) {
     CHECK(n > 0 && k > 0 && n % 16 == 0 && k % 128 == 0 && m >= 1, "gemv_h16 %d %d %d", n, k, m);
@@ -33,8 +38,11 @@ void gemv_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8,
           "multiple of 64 (ldyh %d)", glu ? n / 2 : n, ldyh);
     const int out = glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
     const size_t esz = (glu || out_bf16) ? 2 : 4;
-    for (int r0 = 0; r0 < m; r0 += kMaxGemvRows) {
-        const int mm = m - r0 < kMaxGemvRows ? m - r0 : kMaxGemvRows;
+    // INT4 with an even K slicing: row blocks of up to 32 in one pass over the weights (the wide skinny kernel, the
+    // rows' bits those of 16-row launches); else blocks of 16
+    const int rb = !q8 && decode_groups(n, k) > 0 ? kWideRows : kMaxGemvRows;
+    for (int r0 = 0; r0 < m; r0 += rb) {
+        const int mm = m - r0 < rb ? m - r0 : rb;
         skinny_h16(q, s, n, k, sdt, q8, xh + (size_t)r0 * ldx, ldx, reinterpret_cast<char*>(y) + (size_t)r0 * ldy * esz,
                    ldy, mm, out, yh ? yh + (size_t)r0 * ldyh : nullptr, ldyh, st);
     }

@@ -65,6 +65,9 @@ void xh_pack(const uint16_t* x, int ldx, int k, int m, uint16_t* xh, int ldxh, h
 void skinny_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8, const uint16_t* xh, int ldx, void* y,
                 int ldy, int m, int out, uint16_t* yh, int ldyh, hipStream_t st);
 // any m (16-row launches); checks the shapes
+// whether gemv_h16 runs m rows as one launch (INT4, m <= 32, XH rows 64-element strided and 16-byte aligned, and for
+// 17..32 rows an even K slicing): the reference's wide H16 GEMV contract (gemv_w4hx, false when unsupported)
+bool gemv_h16_one_launch(int n, int k, bool q8, const uint16_t* xh, int ldx, int m);
 void gemv_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8, bool glu, const uint16_t* xh, int ldx,
               void* y, int ldy, int m, bool out_bf16, uint16_t* yh, int ldyh, hipStream_t st);
 // the m = 1 GEMV's record stream with no arithmetic (its HBM read floor); falls back to 4-group slices where the

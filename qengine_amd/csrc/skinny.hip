@@ -409,7 +409,7 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     const int dg = decode_groups(n, k);
     const Slicing sc = dg > 0 ? Slicing{dg, (k >> 7) / dg} : gemv_slicing(n, k);
     const int mt = m == 1 ? 1 : m == 2 ? 2 : m <= 4 ? 4 : m <= 8 ? 8 : m <= 16 ? 16 : 32;
-    CHECK(mt <= 16 || (FMT == qe_gemv::kFmtW4 && !H16), "skinny: %d rows per launch (32-row launches: INT4 only)", m);
+    CHECK(mt <= 16 || FMT == qe_gemv::kFmtW4, "skinny: %d rows per launch (32-row launches: INT4 only)", m);
     const dim3 block(64 * sc.S);
     // two tiles per wave (where n / 16 is even) at m >= 5, and for m <= 4 on grids of fewer than 16 waves per CU at
     // one tile per wave. Measured (K = 5120): RT = 2 is 3 % slower at m = 2, 4 on N = 17408 (8704 waves), 3 % faster
@@ -443,7 +443,7 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     else if (mt == 4) QE_SK_NG(4);
     else if (mt == 8) QE_SK_NG(8);
     else if (mt == 16) QE_SK_NG(16);
-    else if constexpr (FMT == qe_gemv::kFmtW4 && !H16 && !UA) {
+    else if constexpr (FMT == qe_gemv::kFmtW4 && !UA) {
         // 32 rows: even slices only (the uneven-slice variant's 16 waves x 32 staged rows exceed the LDS); else two
         // launches of 16 and m - 16 rows (the same sums per row)
         if (sc.ng == 0) {

@@ -24,6 +24,7 @@ def lib():
                                "(there is no fallback path)")
         _LIB = ctypes.CDLL(LIB_PATH)
         _LIB.qe_skinny_w4.restype = ctypes.c_int
+        _LIB.qe_gemv_w4hxx.restype = ctypes.c_int
         _LIB.qe_abi_version.restype = ctypes.c_int
     return _LIB
 

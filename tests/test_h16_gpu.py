@@ -174,6 +174,31 @@ def test_gemv_w4h_batch_equals_alone(dev, glu):
     assert not bad, bad
 
 
+@pytest.mark.parametrize("glu", [0, 1])
+def test_gemv_w4hxx_one_launch_hook(dev, glu):
+    """the reference's wide H16 hook (src/capi.cpp:72-77): qe_gemv_w4hxx returns 1 when the rows run as one launch
+    (m <= 32; 17..32 rows on the wide kernel) with outputs bit-identical to qe_gemv_w4hx, and 0 with nothing written
+    for 33..64 rows and for 17..32 rows without an even K slicing (K / 128 = 63)"""
+    from qengine_amd import call
+    for n, k, ok_wide in ((2048, 2048, True), (1024, 8064, False)):
+        w, _, _ = w4_bf16(n, k, seed=31 + glu, glu=bool(glu))
+        xh = ops.xh_pack(synth.to_dev(x_outliers(64, k, seed=32)))
+        cols, dt = (n // 2, torch.bfloat16) if glu else (n, torch.float32)
+        iv = torch.int16 if glu else torch.int32
+        for m in (9, 16, 17, 24, 32, 33, 64):
+            y0 = torch.full((m, cols), float("nan"), dtype=dt, device=dev)
+            y1 = y0.clone()
+            call("qe_gemv_w4hx", w.q, w.s, n, k, xh, y0, m, glu, k)
+            r = call("qe_gemv_w4hxx", w.q, w.s, n, k, xh, y1, m, glu, k)
+            torch.cuda.synchronize()
+            want = 1 if (m <= 16 or (m <= 32 and ok_wide)) else 0
+            assert r == want, (n, k, m, r)
+            if r:
+                assert torch.equal(y0.view(iv), y1.view(iv)), (n, k, m)
+            else:
+                assert bool(torch.isnan(y1.float()).all()), (n, k, m)
+
+
 def test_gemv_w4h_ex_strides_scale_f16_out_bf16(dev):
     """the build-defined entry point: fp16 scales, bf16 output, padded XH rows (ldx > k) on a side stream"""
     n, k, m = 512, 1024, 6
