@@ -76,8 +76,9 @@ void qe_gemm_reserve_s(size_t bytes, void* stream);
 int qe_workspace_count(int kind);
 /* Prefill GEMM with the reference's fp16-accumulate numerics (gemm_h_kernel + x_to_h_kernel,
  * src/kernels/gemm.cu:236-461): activations scaled per token to |x| <= 16 (xs = amax / 16) and rounded to fp16,
- * weights as the exact integers u - 8 in fp16, each 64-k chunk's partial rounded to fp16 and scaled by its group
- * scale into fp32, the token scale in the epilogue. flags: QE_SCALE_F16, QE_OUT_BF16, QE_GLU (y = the bf16
+ * weights as the exact integers u - 8 in fp16, each 64-k chunk's partial rounded to fp16 (once; the reference rounds
+ * after every 16-k MMA step, so the bits are not the reference's) and scaled by its group scale into fp32, the token
+ * scale in the epilogue. flags: QE_SCALE_F16, QE_OUT_BF16, QE_GLU (y = the bf16
  * activation [t][n / 2]). The pre-pass buffer (t * (2 k + 4) bytes) is the library's, one per (device, stream),
  * grown on first use; qe_gemm_h_reserve(k, t) sizes the default stream's, qe_gemm_h_reserve_s that of `stream`,
  * before graph capture (a capture that needs more aborts with a message).
@@ -147,7 +148,8 @@ void qe_gemv_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x,
  * XH layout: fp16 x / 16 with |x| clamped to 2047, the columns of each 64-k chunk permuted (k bits b0..b5 ->
  * b0 | b3<<1 | b4<<2 | b5<<3 | b1<<4 | b2<<5). Weights as exact integers in fp16, f16 MFMA over each 64-k chunk, the
  * chunk partial rounded to fp16, then added to fp32 at group scale x 16. Every row count gives the same bits per row.
- * Replaces reference src/capi.cpp:55-66. */
+ * Not bit-identical to the reference, which rounds its fp16 accumulator after every 16-k MMA step (here once per 64-k
+ * chunk; the difference is bounded by the tests). Replaces reference src/capi.cpp:55-66. */
 /* bf16 x [m][k] -> XH [m][ldxh] (k % 64 == 0) */
 void qe_xh_pack(const uint16_t* x, int k, int m, void* xh, int ldxh);
 /* packs x into xh_ws [m][k] fp16, then the H16 GEMV; glu: y is the bf16 act [m][n/2]; yh (optional): XH copy of y */

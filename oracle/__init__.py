@@ -27,11 +27,13 @@ Parity pins (each function is checked against something other than itself in tes
   xh_pos / xh_pack  the lane / k-step statement of the XH layout (gemv_h16.cuh:8-10) for every position, bijection
                     per 64-k chunk, torch's clamp + fp16 conversion for the values
   gemv_h16          exact on integer-valued inputs (equal to the float64 product), and elsewhere within the
-                    closed-form bound of one fp16 rounding per 64-k chunk of the float64 product
+                    closed-form bound of one fp16 rounding per 64-k chunk (step = 64) or per 16-k step (step = 16,
+                    the reference's MMA accumulation) of the float64 product
   x_to_h            torch's float32 amax / division / product and fp16 conversion (an independent RNE
                     implementation), known answers (zero row, amax = 16)
   gemm_h            exact on integer-valued inputs (equal to the float64 product), and elsewhere within the
-                    closed-form bound of one fp16 rounding per 64-k chunk of the float64 product
+                    closed-form bound of one fp16 rounding per 64-k chunk (step = 64) of the float64 product;
+                    step = 16 (the reference's per-MMA-step rounding) is the same code path as gemv_h16's, pinned there
   x_to_i8           the reference test's own torch emulation (tests/test_gemm_i8.py:52-61 quant_emul) restated in
                     torch, known answers (zero group, amax = 127 * 2^e)
   gemm_i8           float64 product of the dequantized int8 operands: brute force on tiny shapes
@@ -354,19 +356,27 @@ def xh_values(xh, k):
     return np.ascontiguousarray(xh[:, xh_pos(np.arange(k))]).view(np.float16).astype(np.float64)
 
 
-def gemv_h16(xv, w, s, wdiv=1):
+def gemv_h16(xv, w, s, wdiv=1, step=64):
     """the H16 decode arithmetic (gemv_h16.cuh:12-15 and xh_flush :59-67; Q8: gemv.cu:786-792): xv [m][k] the XH
-    values (x / 16), w [n][k] the exact integer weights, s [n][k/128] the group scales (float). Every 64-k chunk's
-    partial sum of xv * (w / wdiv) (wdiv = 16 for Q8) is formed exactly and rounded once to fp16, then added at
-    scale * 16 * wdiv. Returns float64 [m][n]; the kernels add the flushed chunks in fp32."""
+    values (x / 16), w [n][k] the exact integer weights, s [n][k/128] the group scales (float). step = 64 (this
+    build's kernels): every 64-k chunk's partial sum of xv * (w / wdiv) (wdiv = 16 for Q8) is formed exactly and
+    rounded once to fp16; step = 16 (the reference's m16n8k16 fp16-accumulate MMA steps): the chunk's fp16 accumulator
+    takes the exact sum of each 16-k step (k = 64 c + 16 j .. + 15) and is rounded to fp16 after every step. Then the
+    chunk is added at scale * 16 * wdiv. Returns float64 [m][n]; the kernels add the flushed chunks in fp32."""
     xv = np.asarray(xv, np.float64)
     m, k = xv.shape
     wf = np.asarray(w, np.float64) / wdiv
     sf = np.asarray(s, np.float64) * (16.0 * wdiv)
     acc = np.zeros((m, wf.shape[0]))
     for c in range(k // 64):
-        part = xv[:, 64 * c:64 * c + 64] @ wf[:, 64 * c:64 * c + 64].T
-        acc += part.astype(np.float16).astype(np.float64) * sf[:, c // 2][None, :]
+        if step == 64:
+            part = (xv[:, 64 * c:64 * c + 64] @ wf[:, 64 * c:64 * c + 64].T).astype(np.float16)
+        else:
+            part = np.zeros((m, wf.shape[0]), np.float16)
+            for j in range(4):
+                k0 = 64 * c + 16 * j
+                part = (part.astype(np.float64) + xv[:, k0:k0 + 16] @ wf[:, k0:k0 + 16].T).astype(np.float16)
+        acc += part.astype(np.float64) * sf[:, c // 2][None, :]
     return acc
 
 
@@ -382,18 +392,26 @@ def x_to_h(x):
     return prod.astype(np.float16).astype(np.float64), xs
 
 
-def gemm_h(xh, xs, w, s):
+def gemm_h(xh, xs, w, s, step=64):
     """the fp16-accumulate prefill arithmetic (gemm.cu:236-461): xh [t][k] the fp16 activation values, xs [t] the
-    token scales, w [n][k] the exact integer weights u - 8, s [n][k/128] the group scales (float). Every 64-k
-    chunk's partial sum is formed exactly and rounded once to fp16 (the reference rounds inside the chunk too),
-    added at its group scale, and the token scale multiplies the sum. Returns float64 [t][n]."""
+    token scales, w [n][k] the exact integer weights u - 8, s [n][k/128] the group scales (float). step = 64 (this
+    build's kernel): every 64-k chunk's partial sum is formed exactly and rounded once to fp16; step = 16 (the
+    reference's fp16-accumulate MMA steps): the chunk's fp16 accumulator is rounded after every 16-k step. Then the
+    chunk is added at its group scale, and the token scale multiplies the sum. Returns float64 [t][n]."""
     xh = np.asarray(xh, np.float64)
     t, k = xh.shape
     sf = np.asarray(s, np.float64)
     acc = np.zeros((t, w.shape[0]))
     for c in range(k // 64):  # the weights are converted chunk by chunk (full-size matrices stay integer)
-        part = xh[:, 64 * c:64 * c + 64] @ np.asarray(w[:, 64 * c:64 * c + 64], np.float64).T
-        acc += part.astype(np.float16).astype(np.float64) * sf[:, c // 2][None, :]
+        if step == 64:
+            part = (xh[:, 64 * c:64 * c + 64] @ np.asarray(w[:, 64 * c:64 * c + 64], np.float64).T).astype(np.float16)
+        else:
+            part = np.zeros((t, w.shape[0]), np.float16)
+            for j in range(4):
+                k0 = 64 * c + 16 * j
+                part = (part.astype(np.float64) + xh[:, k0:k0 + 16] @ np.asarray(w[:, k0:k0 + 16], np.float64).T
+                        ).astype(np.float16)
+        acc += part.astype(np.float64) * sf[:, c // 2][None, :]
     return acc * np.asarray(xs, np.float64)[:, None]
 
 

@@ -76,6 +76,14 @@ def test_gemm_h_parity(dev, n, k, t, sdt):
     assert np.sqrt(np.mean((y - ref) ** 2) / np.mean(ref ** 2)) < 1e-5
     exact = oracle.bf16_to_f32(xb).astype(np.float64) @ exact_w4(q, s, n, k, sdt).astype(np.float64).T
     assert np.abs(y - exact).max() / np.abs(exact).max() < 1e-2  # the reference's gate
+    # the reference rounds every 16-k MMA step to fp16, this kernel each 64-k chunk once: bit parity is not claimed,
+    # the gap to the step-16 emulation is bounded and printed
+    ref16 = oracle.gemm_h(xh, xs, wi, s_f, step=16)
+    g_rms = np.sqrt(np.mean((y - ref16) ** 2) / np.mean(ref16 ** 2))
+    g_max = np.abs(y - ref16).max() / np.sqrt(np.mean(ref16 ** 2))
+    print(f"gemm_h n={n} k={k} t={t} vs the reference's 16-k rounding: rel rms {g_rms:.2e}, max {g_max:.2e} rms",
+          flush=True)
+    assert g_rms <= 1e-3 and g_max <= 5e-3, (g_rms, g_max)
     yb = out_f32(ops.gemm_w4h(w, synth.to_dev(xb), out_bf16=True))
     assert np.all(np.abs(yb - y) <= 2.0 ** -8 * np.abs(y))  # bf16 output = RNE of the fp32 output
 

@@ -121,6 +121,9 @@ def test_gemv_w4h_parity(dev, n, k):
     w, wi, s = w4_bf16(n, k, seed=n + k)
     x = x_outliers(33, k, seed=k)
     ref, ex = emul(x, wi, s), exact(x, wi, s)
+    # the reference's accumulation rounds every 16-k MMA step to fp16, this build each 64-k chunk once (oracle step 16
+    # vs 64): bit parity with the reference is not claimed; the gap to the step-16 emulation is bounded and printed
+    ref16 = oracle.gemv_h16(oracle.xh_values(oracle.xh_pack(x), k), wi, s, 1, step=16)
     rb = relrms(oracle.bf16_to_f32(oracle.f32_to_bf16(ex.astype(np.float32))), ex)
     for m in (1, 3, 16, 33):
         y, xh, _ = ops.gemv_w4h(w, synth.to_dev(x[:m]))
@@ -129,6 +132,11 @@ def test_gemv_w4h_parity(dev, n, k):
         yv = y.cpu().numpy()
         check_h16(yv, ref[:m])
         assert relrms(yv, ex[:m]) < 2 * rb + 1e-4
+        g_rms = relrms(yv, ref16[:m])
+        g_max = np.abs(yv - ref16[:m]).max() / np.sqrt(np.mean(ref16[:m] ** 2))
+        print(f"H16 n={n} k={k} m={m} vs the reference's 16-k rounding: rel rms {g_rms:.2e}, max {g_max:.2e} rms",
+              flush=True)
+        assert g_rms <= 1e-3 and g_max <= 5e-3, (g_rms, g_max)
 
 
 def test_gemv_w4h_glu_and_yh(dev):

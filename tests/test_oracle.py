@@ -483,6 +483,33 @@ def test_gemv_h16_within_one_fp16_rounding_per_chunk(wdiv):
     assert np.abs(got - exact).max() > 1e-3 * bound.max()
 
 
+@pytest.mark.parametrize("wdiv", [1, 16])
+def test_gemv_h16_step16_within_four_roundings_per_chunk(wdiv):
+    """the reference's accumulation (an fp16 rounding after every 16-k MMA step, step = 16): |h16 - exact| <= sum
+    over 64-k chunks of 4 half fp16 ulps of the chunk's magnitude bound at its scale; exact on integer inputs; it
+    differs from the once-per-chunk rounding (step = 64), so the two emulations are not the same function"""
+    rng = np.random.default_rng(20 + wdiv)
+    m, n, k = 4, 32, 1024
+    x = synth.np_bf16(rng.standard_normal((m, k)).astype(np.float32) * 3)
+    xv = oracle.xh_values(oracle.xh_pack(x), k)
+    w = rng.integers(-8, 8, (n, k)) if wdiv == 1 else rng.integers(-127, 128, (n, k))
+    s = np.abs(rng.standard_normal((n, k // 128))) * 0.01
+    got = oracle.gemv_h16(xv, w, s, wdiv, step=16)
+    exact = (xv * 16) @ (w * np.repeat(s, 128, axis=1)).T
+    mag = np.einsum("mci,nci->mcn", np.abs(xv).reshape(m, k // 64, 64), np.abs(w / wdiv).reshape(n, k // 64, 64))
+    half_ulp = 2.0 ** (np.floor(np.log2(np.maximum(mag, 2.0 ** -14))) - 11)
+    bound = (4 * half_ulp * (np.repeat(s, 2, axis=1).T * 16 * wdiv)[None]).sum(axis=1)
+    assert np.all(np.abs(got - exact) <= bound)
+    assert not np.array_equal(got, oracle.gemv_h16(xv, w, s, wdiv, step=64))
+    # small integers (x / 16 in -3..3, w in -8..7: every partial sum of a chunk is a multiple of 1 / wdiv below 1536 /
+    # wdiv, 11 bits) with power-of-two scales: every partial is exact in fp16, so is the result
+    xi = synth.np_bf16((rng.integers(-3, 4, (m, k)) * 16).astype(np.float32))
+    xvi = oracle.xh_values(oracle.xh_pack(xi), k)
+    wi = rng.integers(-8, 8, (n, k))
+    si = 2.0 ** rng.integers(-6, -3, (n, k // 128)).astype(np.float64)
+    assert np.array_equal(oracle.gemv_h16(xvi, wi, si, wdiv, step=16), (xvi * 16) @ (wi * np.repeat(si, 128, axis=1)).T)
+
+
 def test_x_to_h_matches_torch():
     """x_to_h against torch's float32 arithmetic and fp16 conversion; a zero row takes xs = 1, xh = 0; a row whose
     amax is 16 keeps its values (xs = 1)"""
