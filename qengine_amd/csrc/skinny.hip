@@ -16,9 +16,9 @@
 //     dwords of k = 64 h + 16 j + 2 t (+8)), which is exactly the B operand: one ds_read_b128 per MFMA. They are
 //     loaded as 16-byte pieces (every wave-level load instruction costs the address unit about the same, so 4-byte
 //     loads per row made the activations, not the weights, the bound at MT >= 8).
-//   * The bias 136 (u = w + 8 over the 128 of the magic) is removed by one more MFMA per k step with A = -136:
-//     C = sum (128 + u) x - 136 sum x = sum (u - 8) x, all products exact in fp32. The group scale is applied
-//     once per group: acc += s * C.
+//   * The bias 136 (u = w + 8 over the 128 of the magic) is removed by one more MFMA per k step with A = -136, in
+//     a chain of its own that serves all of the wave's tiles: C = sum (128 + u) x + (-136 sum x) = sum (u - 8) x,
+//     all products exact in fp32. The group scale is applied once per group: acc += s * C.
 //   * A wave computes RT = 2 tiles (16-row tiles 2 b, 2 b + 1 of block b) where that pays: one activation load,
 //     staging and B operand read serve both tiles' MFMAs.
 //   * K slices per block are those of the m = 1 matrix-core kernel (decode_groups; gemv_slicing's uneven slices
@@ -134,21 +134,32 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             }
     };
 
-    // 1. loads in consumption order: the slice's scales (8 dwords per group, dword p on lane p % 64); UPX: every
-    //    group's activations, then the first D groups of weight records; else (x_j, w_j) pairs for the first D groups
+    // 1. loads in consumption order, none waited for before the weight window is issued: the slice's scales (8
+    //    dwords per group, dword p on lane p % 64, written to LDS once the window is in flight: a write right after
+    //    the load waits one memory latency ahead of the weight stream); UPX every group's activations, then the first
+    //    D groups of weight records; else (x_j, w_j) pairs for the first D groups. Lanes past the scales (and UPX
+    //    pieces past the slice) load and store the last dword (piece) again: the stores are unconditional, so the
+    //    compiler keeps each load where it is issued here.
     constexpr int PR = (NGM * 8 + 63) / 64;  // rounds of 64 scale dwords / activation pieces (slices of > 8 groups)
+    uint32_t sraw[RT][PR];
+    auto sidx = [&](int pr) {
+        const int p = L + 64 * pr, lim = FMT == kFmtW8C ? 8 : ng * 8;
+        return p < lim ? p : lim - 1;
+    };
 #pragma unroll
     for (int r = 0; r < RT; r++) {
-        if constexpr (FMT == kFmtW8C) {  // one scale per row: the tile's 16 (8 dwords), for every group
-            const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + (size_t)(tile0 + r) * 16);
-            if (L < 8) reinterpret_cast<uint32_t*>(sl16)[r * NGM * 8 + L] = sp[L];
-        } else {
-            const uint32_t* sp = reinterpret_cast<const uint32_t*>(s + ((size_t)(tile0 + r) * G + gb) * 16);
+        const uint32_t* sp = reinterpret_cast<const uint32_t*>(
+            FMT == kFmtW8C ? s + (size_t)(tile0 + r) * 16 : s + ((size_t)(tile0 + r) * G + gb) * 16);
 #pragma unroll
-            for (int pr = 0; pr < PR; pr++)
-                if (L + 64 * pr < ng * 8) reinterpret_cast<uint32_t*>(sl16)[r * NGM * 8 + L + 64 * pr] = sp[L + 64 * pr];
-        }
+        for (int pr = 0; pr < PR; pr++) sraw[r][pr] = sp[sidx(pr)];
     }
+    auto stage_scales = [&]() {
+#pragma unroll
+        for (int r = 0; r < RT; r++)
+#pragma unroll
+            for (int pr = 0; pr < (FMT == kFmtW8C ? 1 : PR); pr++)
+                reinterpret_cast<uint32_t*>(sl16)[r * NGM * 8 + sidx(pr)] = sraw[r][pr];
+    };
     u32x4_v xr[UPX ? 1 : D][XP];  // activation register slots (per-group staging)
     // records of lane (g, t): W4 one per 64 k (two per group), W8 one per 32 k (four per group); 32 per record column
     constexpr int LPG = FMT == kFmtW4 ? 2 : 4;
@@ -177,20 +188,21 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                 xv[pr][tok][1] = ld16(src + 4);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int ii = 0; ii < D; ii++)
             if (ii < ng) ldw(ii, ii);
+        __builtin_amdgcn_sched_barrier(0);
+        stage_scales();
 #pragma unroll
         for (int pr = 0; pr < PR; pr++) {
-            const int pc = L + 64 * pr;
-            if (pc < XL) {
+            const int pc = L + 64 * pr < XL ? L + 64 * pr : XL - 1;
 #pragma unroll
-                for (int tok = 0; tok < MT; tok++)
+            for (int tok = 0; tok < MT; tok++)
 #pragma unroll
-                    for (int e = 0; e < 8; e++)
-                        xl[((pc >> 3) * MT + tok) * kXStride + (H16 ? 8 * (pc & 7) + e : x_slot<kFmtW4>(8 * (pc & 7) + e))] =
-                            xv[pr][tok][e >> 2][e & 3];
-            }
+                for (int e = 0; e < 8; e++)
+                    xl[((pc >> 3) * MT + tok) * kXStride + (H16 ? 8 * (pc & 7) + e : x_slot<kFmtW4>(8 * (pc & 7) + e))] =
+                        xv[pr][tok][e >> 2][e & 3];
         }
     } else {
 #pragma unroll
@@ -200,6 +212,8 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                 ldw(ii, ii);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+        stage_scales();
         stxg(xr[0], 0);  // group 0 -> buffer 0
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -235,27 +249,30 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
         for (int r = 0; r < RT; r++)
 #pragma unroll
             for (int e = 0; e < LPG; e++) rc[r][e] = wv[d][r][e];
-        // refill the window: group ii + D goes where group ii was
+        // refill the window: group ii + D goes where group ii was, issued here (left to itself the scheduler sinks
+        // these loads below the group's MFMAs, and the window drains before each refill)
         if (ii + D < ng) {
             if constexpr (!UPX) ldxg(xr[d], ii + D);
             ldw(d, ii + D);
         }
-        // per k step: one B operand read (the group's activations) serves the weight MFMA and the bias MFMA
-        // (A = -136) of each tile: c = sum (128 + u) x - 136 sum x = sum (u - 8) x
-        f32x4_v c[RT][NB];
+        __builtin_amdgcn_sched_barrier(0);
+        // per k step: one B operand read (the group's activations) serves each tile's weight MFMA and one bias MFMA
+        // (A = -136, the same for every row and tile): c_r + cb = sum (128 + u) x - 136 sum x = sum (u - 8) x
+        f32x4_v c[RT][NB], cb[NB];
 #pragma unroll
-        for (int r = 0; r < RT; r++)
+        for (int nb = 0; nb < NB; nb++) {
+            cb[nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int nb = 0; nb < NB; nb++) c[r][nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+            for (int r = 0; r < RT; r++) c[r][nb] = f32x4_v{0.f, 0.f, 0.f, 0.f};
+        }
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
             bf16x8_v bb[NB];  // the B operands (H16: the same bits as f16x8)
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
-                u32x4_v bv = {0u, 0u, 0u, 0u};
-                if (MT >= 16 || i < MT)
-                    bv = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + 16 * nb + (i < MT ? i : 0)) * kXStride +
-                                                               (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
+                // columns i >= MT read row 0 again: MFMA columns are independent and those are never stored
+                const u32x4_v bv = *reinterpret_cast<const u32x4_v*>(&xl[(xrow + 16 * nb + (i < MT ? i : 0)) * kXStride +
+                                                                        (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
                 bb[nb] = __builtin_bit_cast(bf16x8_v, bv);
             }
             const int j0 = 2 * (mm & 1);
@@ -317,9 +334,12 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
                                                                           __builtin_bit_cast(f16x8_v, bn), c[r][nb], 0, 0, 0);
                     } else {
                         c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), bb[nb], c[r][nb], 0, 0, 0);
-                        c[r][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb[nb], c[r][nb], 0, 0, 0);
                     }
                 }
+            }
+            if constexpr (!H16) {
+#pragma unroll
+                for (int nb = 0; nb < NB; nb++) cb[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, bb[nb], cb[nb], 0, 0, 0);
             }
             if constexpr (H16) {
                 if (mm & 1) {  // end of a 64-k chunk: its partial in fp16, then into fp32 at the group scale x 16 (x 256)
@@ -350,10 +370,10 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
             const float s2 = scale_rt<SDT>((uint16_t)(sv.y & 0xffffu), sdt), s3 = scale_rt<SDT>((uint16_t)(sv.y >> 16), sdt);
 #pragma unroll
             for (int nb = 0; nb < NB; nb++) {
-                acc[r][nb][0] = fmaf(s0, c[r][nb][0], acc[r][nb][0]);
-                acc[r][nb][1] = fmaf(s1, c[r][nb][1], acc[r][nb][1]);
-                acc[r][nb][2] = fmaf(s2, c[r][nb][2], acc[r][nb][2]);
-                acc[r][nb][3] = fmaf(s3, c[r][nb][3], acc[r][nb][3]);
+                acc[r][nb][0] = fmaf(s0, c[r][nb][0] + cb[nb][0], acc[r][nb][0]);
+                acc[r][nb][1] = fmaf(s1, c[r][nb][1] + cb[nb][1], acc[r][nb][1]);
+                acc[r][nb][2] = fmaf(s2, c[r][nb][2] + cb[nb][2], acc[r][nb][2]);
+                acc[r][nb][3] = fmaf(s3, c[r][nb][3] + cb[nb][3], acc[r][nb][3]);
             }
         }
         if constexpr (!UPX) {
@@ -375,22 +395,31 @@ __attribute__((amdgpu_waves_per_eu(WPE))) skinny_kernel(
         for (int nb = 0; nb < NB; nb++)
             *reinterpret_cast<f32x4_v*>(&red[(size_t)w * WSZ + (r * MTR + 16 * nb + i) * 16 + 4 * qg]) = acc[r][nb];
     __syncthreads();
+    // an output's S partials are read at once (slots past S read slot S - 1 and are not added) and summed in slice
+    // order; the outputs are indexed over MT rows (index math by shifts), rows >= m are not stored
+    constexpr int KW = NG > 0 ? kMaxWaves : kMaxWavesGeneric;
     auto rsum = [&](int r, int tok, int rr) {
+        float p[KW];
+#pragma unroll
+        for (int ws = 0; ws < KW; ws++) p[ws] = red[(size_t)(ws < S ? ws : S - 1) * WSZ + (r * MTR + tok) * 16 + rr];
         float v = 0.f;
-        for (int ws = 0; ws < S; ws++) v += red[(size_t)ws * WSZ + (r * MTR + tok) * 16 + rr];
+#pragma unroll
+        for (int ws = 0; ws < KW; ws++) v = ws < S ? v + p[ws] : v;
         return v;
     };
     if (out == kOutGLU) {
-        for (int idx = threadIdx.x; idx < RT * m * 8; idx += blockDim.x) {
-            const int r = idx / (m * 8), tok = (idx >> 3) - r * m, gg = idx & 7;
+        for (int idx = threadIdx.x; idx < RT * MT * 8; idx += blockDim.x) {
+            const int r = idx / (MT * 8), tok = (idx >> 3) % MT, gg = idx & 7;
+            if (tok >= m) continue;
             const int col = 8 * (tile0 + r) + gg;
             const float v = silu_f32(rsum(r, tok, gg)) * rsum(r, tok, gg + 8);
             reinterpret_cast<uint16_t*>(y)[(size_t)tok * ldy + col] = f32_to_bf16(v);
             if (yh) yh[(size_t)tok * ldyh + xh_pos(col)] = to_xh(v);
         }
     } else {
-        for (int idx = threadIdx.x; idx < RT * m * 16; idx += blockDim.x) {
-            const int r = idx / (m * 16), tok = (idx >> 4) - r * m, rr = idx & 15;
+        for (int idx = threadIdx.x; idx < RT * MT * 16; idx += blockDim.x) {
+            const int r = idx / (MT * 16), tok = (idx >> 4) % MT, rr = idx & 15;
+            if (tok >= m) continue;
             const float v = rsum(r, tok, rr);
             const int col = 16 * (tile0 + r) + rr;
             const size_t o = (size_t)tok * ldy + col;
