@@ -36,6 +36,25 @@ __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {
     else return sdt == kScaleF16 ? scale_to_f32<kScaleF16>(v) : scale_to_f32<kScaleBF16>(v);
 }
 
+// The reference operand of a nibble byte v (v = u, or v = 16 u where a high nibble is kept in place), with fewer VALU
+// instructions than a per-weight int -> float conversion:
+//   bf16: the 0x64 byte magic makes fp16 1024 + v (one v_perm per pair of weights), and one v_fma_mix_f32 per weight
+//         gives (1024 + v) sv + bv = (u - 8) s exactly in fp32 (sv = s, bv = -1032 s for v = u; sv = s / 16,
+//         bv = -72 s for v = 16 u: every product and the sum fit fp32's 24 bits), rounded once to bf16
+//   fp16 (v = u only): (1024 + u) - 1032 = u - 8 exactly in packed fp16, then one packed fp16 multiply by s rounds
+//         the exact product (u - 8) s once: fp16_rn((u - 8) s)
+// Pairs are bytes (0, 2) and (1, 3) of t.
+__device__ __forceinline__ uint32_t magic_f16_b02(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04020400u); }
+__device__ __forceinline__ uint32_t magic_f16_b13(uint32_t t) { return __builtin_amdgcn_perm(0x64646464u, t, 0x04030401u); }
+__device__ __forceinline__ uint32_t dq_bf16_pair(uint32_t magic_pair, float sv, float bv) {
+    const f16x2_v h = __builtin_bit_cast(f16x2_v, magic_pair);
+    return pack_bf16x2(fmaf((float)h[0], sv, bv), fmaf((float)h[1], sv, bv));
+}
+__device__ __forceinline__ uint32_t dq_f16_pair(uint32_t magic_pair, f16x2_v s2) {
+    const f16x2_v w = __builtin_bit_cast(f16x2_v, magic_pair) - f16x2_v{(_Float16)1032.f, (_Float16)1032.f};
+    return __builtin_bit_cast(uint32_t, w * s2);
+}
+
 // dequantize the 8 nibbles of one W4 word (rows g / g + 8, k0 + {0, 1, 8, 9}) to bf16_rn((u - 8) * s) and store them
 // as 4 bf16 pairs at (row, k0) (row, k0 + 8) (row + 8, k0) (row + 8, k0 + 8) of the tile
 __device__ __forceinline__ void dq_w4_word(uint32_t wd, float s_lo, float s_hi, char* wt, int row, int k0) {

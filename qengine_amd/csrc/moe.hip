@@ -552,34 +552,38 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // 3. per group: the row's scale, 4 k steps of one MFMA on the dequantized weights (pairs of bytes 0 / 2 and 1 / 3
-    //    of the nibble words: k, k + 1 and k + 8, k + 9 of the record's byte order)
-    // rows g + 8 (lanes i >= 8) keep their high nibbles in place (16 u) and take s / 16: the same fma, no shift
+    //    of the nibble words: k, k + 1 and k + 8, k + 9 of the record's byte order; qe_tile::dq_bf16_pair /
+    //    dq_f16_pair). bf16: rows g + 8 (lanes i >= 8) keep their high nibbles in place (v = 16 u) and take s / 16;
+    //    fp16: those lanes shift their nibbles down. B columns i >= MT read row 0 again (never stored).
     const uint32_t lmask = sh ? 0xF0F0F0F0u : qe_tile::nib_mask();
-    const float lscale = sh ? 0.0625f : 1.f;
     f32x4_v acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ii = 0; ii < NG; ii++) {
-        const float s_row = scale_to_f32<kScaleF16>(sl16[ii * 16 + i]);
-        const float sc = s_row * lscale, bias = -8.f * s_row;
+        const uint16_t s_bits = sl16[ii * 16 + i];
+        const float s_row = scale_to_f32<kScaleF16>(s_bits);
+        const float sv = sh ? s_row * 0.0625f : s_row, bv = sh ? -72.f * s_row : -1032.f * s_row;
+        const _Float16 s_h = __builtin_bit_cast(_Float16, s_bits);
+        const f16x2_v s2 = {s_h, s_h};
 #pragma unroll
         for (int mm = 0; mm < 4; mm++) {
-            u32x4_v b = *reinterpret_cast<const u32x4_v*>(
+            const u32x4_v b = *reinterpret_cast<const u32x4_v*>(
                 &xl[(ii * MT + (i < MT ? i : 0)) * XS + (4 * (mm >> 1) + qg) * 8 + 4 * (mm & 1)]);
-            b = i < MT ? b : u32x4_v{0u, 0u, 0u, 0u};
             const u32x4_v rec = wv[ii][mm >> 1];
             const int j0 = 2 * (mm & 1);
-            const uint32_t t0 = rec[j0] & lmask, t1 = rec[j0 + 1] & lmask;
-            auto pk = [](float lo, float hi) { return F16 ? pack_f16x2(lo, hi) : pack_bf16x2(lo, hi); };
-            const u32x4_v a = {pk(fmaf(qe_tile::cvt_ubyte<0>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t0), sc, bias)),
-                               pk(fmaf(qe_tile::cvt_ubyte<1>(t0), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t0), sc, bias)),
-                               pk(fmaf(qe_tile::cvt_ubyte<0>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<2>(t1), sc, bias)),
-                               pk(fmaf(qe_tile::cvt_ubyte<1>(t1), sc, bias), fmaf(qe_tile::cvt_ubyte<3>(t1), sc, bias))};
-            if constexpr (F16)
+            u32x4_v a;
+            if constexpr (F16) {
+                const uint32_t t0 = (rec[j0] >> sh) & qe_tile::nib_mask(), t1 = (rec[j0 + 1] >> sh) & qe_tile::nib_mask();
+                a = u32x4_v{qe_tile::dq_f16_pair(qe_tile::magic_f16_b02(t0), s2), qe_tile::dq_f16_pair(qe_tile::magic_f16_b13(t0), s2),
+                            qe_tile::dq_f16_pair(qe_tile::magic_f16_b02(t1), s2), qe_tile::dq_f16_pair(qe_tile::magic_f16_b13(t1), s2)};
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a), __builtin_bit_cast(f16x8_v, b),
                                                              acc, 0, 0, 0);
-            else
+            } else {
+                const uint32_t t0 = rec[j0] & lmask, t1 = rec[j0 + 1] & lmask;
+                a = u32x4_v{qe_tile::dq_bf16_pair(qe_tile::magic_f16_b02(t0), sv, bv), qe_tile::dq_bf16_pair(qe_tile::magic_f16_b13(t0), sv, bv),
+                            qe_tile::dq_bf16_pair(qe_tile::magic_f16_b02(t1), sv, bv), qe_tile::dq_bf16_pair(qe_tile::magic_f16_b13(t1), sv, bv)};
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), __builtin_bit_cast(bf16x8_v, b),
                                                               acc, 0, 0, 0);
+            }
         }
     }
     // 4. lane (q, i < MT) holds rows 4 q .. 4 q + 3 of activation row i
