@@ -129,14 +129,15 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         }
         const uint32_t* rw = reinterpret_cast<const uint32_t*>(raw + (jtr >> 1) * 1024) + (8 * (jtr & 1) + jg) * 4 + jj;
         const float scl = scale_rt<SDT>(reinterpret_cast<const uint16_t*>(sc)[jtr * 16 + jg + 8 * h], sdt);
-        const float bias = -8.f * scl;
+        // h = 1 keeps its nibbles high (v = 16 u): qe_tile::dq_pair's s / 16, -72 s
+        const float sv = h ? scl * 0.0625f : scl, bv = h ? -72.f * scl : -1032.f * scl;
+        const uint32_t msk = h ? 0xF0F0F0F0u : nib_mask();
         uint32_t lo[4], hi[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const uint32_t wd = rw[64 * t];
-            const uint32_t u = (h ? wd >> 4 : wd) & nib_mask();  // bytes: k0, k0+8, k0+1, k0+9
-            lo[t] = pack_bf16x2(fmaf(cvt_ubyte<0>(u), scl, bias), fmaf(cvt_ubyte<2>(u), scl, bias));
-            hi[t] = pack_bf16x2(fmaf(cvt_ubyte<1>(u), scl, bias), fmaf(cvt_ubyte<3>(u), scl, bias));
+            const uint32_t u = rw[64 * t] & msk;  // bytes: k0, k0+8, k0+1, k0+9
+            lo[t] = dq_pair(magic_f16<kSel02>(u), sv, bv);
+            hi[t] = dq_pair(magic_f16<kSel13>(u), sv, bv);
         }
         const int row = jtr * 16 + jg + 8 * h;
         *reinterpret_cast<u32x4_v*>(wtile + swz(row, 2 * jj)) = u32x4_v{lo[0], lo[1], lo[2], lo[3]};
@@ -197,19 +198,19 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
         rec_of(e, tr, slab, wl);
         const int row = tr * 16 + (wl >> 2);
         const float s_lo = scale_rt<SDT>(ws.sr_lo[e], sdt), s_hi = scale_rt<SDT>(ws.sr_hi[e], sdt);
-        const float b_lo = -128.f * s_lo, b_hi = -128.f * s_hi;
+        const float b_lo = -1152.f * s_lo, b_hi = -1152.f * s_hi;  // qe_tile::dq_pair's W8 bias
         const u32x4_v tv = xpose4(ws.wr[e]);  // tv[t'] = dword (lane t) of record (g, t')
         if constexpr (FMT == kFmtQ8) {
             // Q8 word 2 s + h: row g + 8 h, bytes at k0 + {0, 8, 1, 9}, k0 = 32 slab + 16 s + 2 t: lane t now holds
             // word t of the quad, i.e. row g + 8 (t % 2) at chunks 4 slab + 2 (t / 2) (bytes 0, 2) and + 1 (bytes 1, 3)
             const int t = wl & 3;
-            const float sc = (t & 1) ? s_hi : s_lo, bs = -128.f * sc;
+            const float sc = (t & 1) ? s_hi : s_lo, bs = -1152.f * sc;
             uint32_t a[4], b[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const uint32_t x = tv[u] ^ 0x80808080u;  // w + 128
-                a[u] = pack_bf16x2(fmaf(cvt_ubyte<0>(x), sc, bs), fmaf(cvt_ubyte<2>(x), sc, bs));
-                b[u] = pack_bf16x2(fmaf(cvt_ubyte<1>(x), sc, bs), fmaf(cvt_ubyte<3>(x), sc, bs));
+                a[u] = dq_pair(magic_f16<kSel02>(x), sc, bs);
+                b[u] = dq_pair(magic_f16<kSel13>(x), sc, bs);
             }
             const int qrow = row + 8 * (t & 1), ch = 4 * slab + 2 * (t >> 1);
             *reinterpret_cast<u32x4_v*>(wtile + swz(qrow, ch)) = u32x4_v{a[0], a[1], a[2], a[3]};
@@ -220,8 +221,8 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
 #pragma unroll
         for (int u = 0; u < 4; u++) {
             const uint32_t x = tv[u] ^ 0x80808080u;  // w + 128
-            lo[u] = pack_bf16x2(fmaf(cvt_ubyte<0>(x), s_lo, b_lo), fmaf(cvt_ubyte<1>(x), s_lo, b_lo));
-            hi[u] = pack_bf16x2(fmaf(cvt_ubyte<2>(x), s_hi, b_hi), fmaf(cvt_ubyte<3>(x), s_hi, b_hi));
+            lo[u] = dq_pair(magic_f16<kSel01>(x), s_lo, b_lo);
+            hi[u] = dq_pair(magic_f16<kSel23>(x), s_hi, b_hi);
         }
         const int ch = 4 * slab + (wl & 3);
         *reinterpret_cast<u32x4_v*>(wtile + swz(row, ch)) = u32x4_v{lo[0], lo[1], lo[2], lo[3]};
@@ -333,10 +334,11 @@ __global__ void __launch_bounds__(NTH) gemm_kernel(const uint4* __restrict__ q, 
                     if (slot % STRIDE != STRIDE - 1 || slot / STRIDE >= 8) return;
                     // unit (h, t): word t, nibbles of row g + 8 h -> bf16 pairs at k0 (lo) and k0 + 8 (hi)
                     const int un = slot / STRIDE, h = un >> 2, t = un & 3;
-                    const float bias = -8.f * scl[h];
-                    const uint32_t u = (h ? wd[t] >> 4 : wd[t]) & nib_mask();  // bytes: k0, k0+8, k0+1, k0+9
-                    lo[h][t] = pack_bf16x2(fmaf(cvt_ubyte<0>(u), scl[h], bias), fmaf(cvt_ubyte<2>(u), scl[h], bias));
-                    hi[h][t] = pack_bf16x2(fmaf(cvt_ubyte<1>(u), scl[h], bias), fmaf(cvt_ubyte<3>(u), scl[h], bias));
+                    // h = 1 keeps its nibbles high (v = 16 u): qe_tile::dq_pair's s / 16, -72 s
+                    const float sv = h ? scl[h] * 0.0625f : scl[h], bv = h ? -72.f * scl[h] : -1032.f * scl[h];
+                    const uint32_t u = wd[t] & (h ? 0xF0F0F0F0u : nib_mask());  // bytes: k0, k0+8, k0+1, k0+9
+                    lo[h][t] = dq_pair(magic_f16<kSel02>(u), sv, bv);
+                    hi[h][t] = dq_pair(magic_f16<kSel13>(u), sv, bv);
                     if (t == 3 && (NJOB >= NTH || jactive)) {
                         const int row = jtr * 16 + jg + 8 * h;
                         *reinterpret_cast<u32x4_v*>(wnext + swz(row, 2 * jj)) = u32x4_v{lo[h][0], lo[h][1], lo[h][2], lo[h][3]};

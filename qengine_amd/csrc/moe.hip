@@ -552,7 +552,7 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
     // 3. per group: the row's scale, 4 k steps of one MFMA on the dequantized weights (pairs of bytes 0 / 2 and 1 / 3
-    //    of the nibble words: k, k + 1 and k + 8, k + 9 of the record's byte order; qe_tile::dq_bf16_pair /
+    //    of the nibble words: k, k + 1 and k + 8, k + 9 of the record's byte order; qe_tile::dq_pair /
     //    dq_f16_pair). bf16: rows g + 8 (lanes i >= 8) keep their high nibbles in place (v = 16 u) and take s / 16;
     //    fp16: those lanes shift their nibbles down. B columns i >= MT read row 0 again (never stored).
     const uint32_t lmask = sh ? 0xF0F0F0F0u : qe_tile::nib_mask();
@@ -573,14 +573,14 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
             u32x4_v a;
             if constexpr (F16) {
                 const uint32_t t0 = (rec[j0] >> sh) & qe_tile::nib_mask(), t1 = (rec[j0 + 1] >> sh) & qe_tile::nib_mask();
-                a = u32x4_v{qe_tile::dq_f16_pair(qe_tile::magic_f16_b02(t0), s2), qe_tile::dq_f16_pair(qe_tile::magic_f16_b13(t0), s2),
-                            qe_tile::dq_f16_pair(qe_tile::magic_f16_b02(t1), s2), qe_tile::dq_f16_pair(qe_tile::magic_f16_b13(t1), s2)};
+                a = u32x4_v{qe_tile::dq_f16_pair(qe_tile::magic_f16<qe_tile::kSel02>(t0), s2), qe_tile::dq_f16_pair(qe_tile::magic_f16<qe_tile::kSel13>(t0), s2),
+                            qe_tile::dq_f16_pair(qe_tile::magic_f16<qe_tile::kSel02>(t1), s2), qe_tile::dq_f16_pair(qe_tile::magic_f16<qe_tile::kSel13>(t1), s2)};
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_v, a), __builtin_bit_cast(f16x8_v, b),
                                                              acc, 0, 0, 0);
             } else {
                 const uint32_t t0 = rec[j0] & lmask, t1 = rec[j0 + 1] & lmask;
-                a = u32x4_v{qe_tile::dq_bf16_pair(qe_tile::magic_f16_b02(t0), sv, bv), qe_tile::dq_bf16_pair(qe_tile::magic_f16_b13(t0), sv, bv),
-                            qe_tile::dq_bf16_pair(qe_tile::magic_f16_b02(t1), sv, bv), qe_tile::dq_bf16_pair(qe_tile::magic_f16_b13(t1), sv, bv)};
+                a = u32x4_v{qe_tile::dq_pair(qe_tile::magic_f16<qe_tile::kSel02>(t0), sv, bv), qe_tile::dq_pair(qe_tile::magic_f16<qe_tile::kSel13>(t0), sv, bv),
+                            qe_tile::dq_pair(qe_tile::magic_f16<qe_tile::kSel02>(t1), sv, bv), qe_tile::dq_pair(qe_tile::magic_f16<qe_tile::kSel13>(t1), sv, bv)};
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, a), __builtin_bit_cast(bf16x8_v, b),
                                                               acc, 0, 0, 0);
             }

@@ -150,8 +150,8 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
         sl[S] = scale_to_f32<kScaleF16>(sc[0]);
         const float s_hi = scale_to_f32<kScaleF16>(sc[8]);
         sh16[S] = s_hi * 0.0625f;
-        bl[S] = -8.f * sl[S];
-        bh[S] = -8.f * s_hi;
+        bl[S] = -1032.f * sl[S];  // qe_tile::dq_pair: v = u (low), v = 16 u (high, s / 16)
+        bh[S] = -72.f * s_hi;
     };
     // unit u of the dequantization of k16 step j from set S: operand u / 4, pair t = u % 4 (record t, bytes
     // (h, h + 2) of word 2 (j % 2) + kh, h = j / 2)
@@ -160,9 +160,8 @@ __device__ __forceinline__ void rw_body(const MoePfArgs& ma, char* lds, int nt, 
         const int bb = u >> 2, t = u & 3;
         const uint32_t v = mw[S][bb][t][j & 1];
         const float s = bb ? sh16[S] : sl[S], bias = bb ? bh[S] : bl[S];
-        auto pk = [](float lo, float hi) { return MODE == 2 ? pack_f16x2(lo, hi) : pack_bf16x2(lo, hi); };
-        an[j & 1][bb][t] = (j >> 1) ? pk(fmaf(cvt_ubyte<1>(v), s, bias), fmaf(cvt_ubyte<3>(v), s, bias))
-                                    : pk(fmaf(cvt_ubyte<0>(v), s, bias), fmaf(cvt_ubyte<2>(v), s, bias));
+        an[j & 1][bb][t] = (j >> 1) ? dq_pair<MODE == 2>(magic_f16<kSel13>(v), s, bias)
+                                    : dq_pair<MODE == 2>(magic_f16<kSel02>(v), s, bias);
     };
     using P0 = std::integral_constant<int, 0>;
     using P1 = std::integral_constant<int, 1>;
