@@ -9,7 +9,10 @@ more than the 256 MB Infinity Cache) so every call streams its weights from HBM.
 Every secondary figure rotates enough weight copies (or MoE routings) that its working set exceeds the Infinity
 Cache and says so (`working_set`, bytes). The K decode launches are captured in one HIP graph and replayed (as a decode loop is served), so the host's
 per-call overhead does not starve the GPU. `roofline.achieved` = bytes per call / the stream time per launch
-(HIP events on the launch stream before and after the K timed launches). The prefill GEMM (config 2) and the other configs are reported beside it in `secondary`.
+(HIP events on the launch stream before and after the K timed launches); `roofline.read_floor_us` is the same run's
+load-only floor of that launch shape (qe_read_probe), `frac_of_read_floor` the GEMV's share of it and `clock_mhz`
+the shader clock measured right after the GEMV (qe_clock_probe_mhz): the GEMV time follows the box's clock. The
+prefill GEMM (config 2) and the other configs are reported beside it in `secondary`.
 The CPU baseline is the oracle's dequantize + fp32 matmul of the same workload on the host cores.
 """
 import argparse
@@ -140,6 +143,13 @@ def bench_gemv(args, m=1, n=17408, k=5120, steps=None, warmup=None, invariant=Fa
     del ws
     torch.cuda.empty_cache()
     return res
+
+
+def clock_probe():
+    """the shader clock in MHz (qe_clock_probe_mhz: clock64 cycles over 50 us of the constant-rate wall clock)"""
+    from qengine_amd import ops
+    from qengine_amd.qe import lib
+    return round(float(lib().qe_clock_probe_mhz(ops._stream())), 1)
 
 
 def set_config(**kw):
@@ -376,9 +386,10 @@ def main():
         return
 
     g = bench_gemv(args)
-    secondary = {"gemv_c0": {"copies": g["copies"], "working_set": g["working_set"]}}
+    clock_mhz = clock_probe()  # right after the GEMV's replays: the shader clock this box ran them at
+    floor = bench_read_floor(args, steps=400, warmup=20)
+    secondary = {"gemv_c0": {"copies": g["copies"], "working_set": g["working_set"]}, "read_floor_c0": floor}
     if not args.no_secondary:
-        secondary["read_floor_c0"] = bench_read_floor(args, steps=400, warmup=20)
         gi = bench_gemv(args, steps=400, warmup=20, invariant=True)
         secondary["gemv_c0_batch_invariant"] = {"us_kernel": round(gi["kernel_ms_mean"] * 1e3, 3),
                                                 "pct_hbm": round(100 * gi["gbs_kernel"] / HBM_PEAK_GBS, 1),
@@ -425,7 +436,11 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": read_traffic("gemv_w4_c0_m1_traffic.txt"),
-                     "kernel_us_mean": round(g["kernel_ms_mean"] * 1e3, 3)},
+                     "kernel_us_mean": round(g["kernel_ms_mean"] * 1e3, 3),
+                     # same run: the load-only floor of this launch shape, the GEMV's share of it, the shader clock
+                     "read_floor_us": floor["us_per_launch"],
+                     "frac_of_read_floor": round(floor["us_per_launch"] / (g["kernel_ms_mean"] * 1e3), 4),
+                     "clock_mhz": clock_mhz},
         "cpu_baseline": cpu,
         "secondary": secondary,
     }

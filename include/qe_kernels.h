@@ -115,6 +115,10 @@ int qe_gemm_w4_choice(const void* q, const void* s, int n, int k, const uint16_t
  * of the m = 1 decode GEMV (n/16 blocks, its K slices) and does nothing else, the HBM read floor that GEMV is held
  * against. sink: n/16 dwords (written only on a 2^-32 chance, so the loads cannot be dropped). */
 void qe_read_probe(const void* q, int n, int k, uint32_t* sink, void* stream);
+/* Measurement helper (no reference counterpart): the shader clock in MHz, counted by one lane over 50 us of the
+ * constant-rate wall clock (clock64 / wall_clock64); synchronizes the stream and allocates 16 bytes. The bench reports
+ * it beside the GEMV time, which follows the clock of the box it runs on. */
+float qe_clock_probe_mhz(void* stream);
 
 /* ---- reference-named hooks (src/capi.cpp): bf16 scales, fp32 outputs, default stream ---- */
 

@@ -118,6 +118,8 @@ void qe_read_probe(const void* q, int n, int k, uint32_t* sink, void* stream) {
     read_probe_w4(q, n, k, sink, reinterpret_cast<hipStream_t>(stream));
 }
 
+float qe_clock_probe_mhz(void* stream) { return clock_probe_mhz(reinterpret_cast<hipStream_t>(stream)); }
+
 // ---------------------------------------------------------------- reference-named hooks
 void qe_gemv_workspace_init(void) {
     gemv_workspace_init();

@@ -436,3 +436,34 @@ void read_probe_w4(const void* q, int n, int k, uint32_t* sink, hipStream_t st) 
     else read_probe_kernel<2><<<grid, block, 0, st>>>(qq, k, sink);
     HIP_CHECK(hipGetLastError());
 }
+
+// ---- the shader clock: one lane counts clock64() (shader clock cycles) over `ticks` of wall_clock64() (a constant
+// rate), then stores both spans; the loop ends once the wall clock has advanced `ticks`, whatever the shader clock
+namespace qe_gemv1 {
+__global__ void __launch_bounds__(64) clock_probe_kernel(unsigned long long* __restrict__ out, long long ticks) {
+    if (threadIdx.x != 0) return;
+    const long long r0 = wall_clock64(), c0 = clock64();
+    long long r = r0;
+    while (r - r0 < ticks) r = wall_clock64();
+    const long long c1 = clock64();
+    out[0] = (unsigned long long)(r - r0);
+    out[1] = (unsigned long long)(c1 - c0);
+}
+}  // namespace qe_gemv1
+
+float clock_probe_mhz(hipStream_t st) {
+    int dev = 0, rate_khz = 0;
+    HIP_CHECK(hipGetDevice(&dev));
+    HIP_CHECK(hipDeviceGetAttribute(&rate_khz, hipDeviceAttributeWallClockRate, dev));
+    CHECK(rate_khz > 0, "clock_probe: wall clock rate %d kHz", rate_khz);
+    unsigned long long* d = nullptr;
+    unsigned long long h[2] = {0, 0};
+    HIP_CHECK(hipMalloc(&d, sizeof(h)));
+    const long long ticks = (long long)rate_khz / 20;  // 50 us of wall clock
+    qe_gemv1::clock_probe_kernel<<<1, 64, 0, st>>>(d, ticks);
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipMemcpyAsync(h, d, sizeof(h), hipMemcpyDeviceToHost, st));
+    HIP_CHECK(hipStreamSynchronize(st));
+    HIP_CHECK(hipFree(d));
+    return h[0] ? (float)((double)h[1] / (double)h[0] * rate_khz / 1000.0) : 0.f;
+}

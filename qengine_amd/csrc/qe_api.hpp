@@ -73,6 +73,7 @@ void gemv_h16(const uint4* q, const uint16_t* s, int n, int k, int sdt, bool q8,
 // the m = 1 GEMV's record stream with no arithmetic (its HBM read floor); falls back to 4-group slices where the
 // GEMV has no even slicing
 void read_probe_w4(const void* q, int n, int k, uint32_t* sink, hipStream_t st);
+float clock_probe_mhz(hipStream_t st);  // the shader clock over 50 us of wall clock (synchronizes st)
 // Kernel policy, set explicitly by the caller (qe_set_config) instead of scattered environment reads:
 //   skinny_min_m    smallest row count gemv_w4 sends to the matrix-core skinny kernel (default 2)
 //   w8_mfma_min_m   the same for INT8 / Q8 (0 = automatic: 1 where the m = 1 slicing has >= 4 groups, else 2)

@@ -26,6 +26,7 @@ def lib():
         _LIB.qe_skinny_w4.restype = ctypes.c_int
         _LIB.qe_gemv_w4hxx.restype = ctypes.c_int
         _LIB.qe_abi_version.restype = ctypes.c_int
+        _LIB.qe_clock_probe_mhz.restype = ctypes.c_float
     return _LIB
 
 

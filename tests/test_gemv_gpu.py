@@ -458,3 +458,19 @@ def test_batch_invariant_w8(dev, batch_invariant):
 def test_config_defaults_and_checks(dev):
     c = ops.get_config()
     assert c == {"skinny_min_m": 2, "w8_mfma_min_m": 0, "batch_invariant": 0, "gemm_tune": 0, "gemm_h16": 0}
+
+
+def test_measurement_probes(dev):
+    """the bench's measurement helpers: the shader clock is within gfx950's range, and the read probe runs on the
+    m = 1 GEMV's launch shape without writing its sink (a 2^-32 chance per block)"""
+    from qengine_amd.qe import lib
+    mhz = float(lib().qe_clock_probe_mhz(ops._stream()))
+    print(f"shader clock {mhz:.0f} MHz")
+    assert 300.0 <= mhz <= 3500.0, mhz
+    n, k = 1024, 5120
+    q, s = synth.w4_dev(n, k, seed=3)
+    w = ops.repack_w4(q, s)
+    sink = torch.zeros(n // 16, dtype=torch.int32, device="cuda")
+    call("qe_read_probe", w.q, n, k, sink, ops._stream())
+    torch.cuda.synchronize()
+    assert int((sink != 0).sum()) <= 1
