@@ -179,6 +179,12 @@ void qe_gemm_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x,
 /* on != 0: later non-GLU GEMM calls write bf16 (round to nearest even) into y viewed as bf16 [t][n].
  * Replaces reference src/capi.cpp:114 (gemm_set_out_bf16, gemm.cu:4363-4375). */
 void qe_gemm_set_out_bf16(int on);
+/* run-time cap of the stream-K split: later prefill GEMM calls (W4, W8 / Q8 bf16-activation GEMMs) split the tiles
+ * of their last partial round into at most n K ranges (n <= 0: no cap, the default; splits here are 1, 2 or 4, so
+ * n = 1 turns the split off and n = 2 or 3 allows 2). Applies to the cost model's, the tuner's and a stored choice
+ * alike (a stored split above the cap runs as the largest allowed one). Replaces reference src/capi.cpp:115
+ * (gemm_set_sk_maxparts, gemm.cu:3485-3496,4359). */
+void qe_gemm_set_sk_maxparts(int n);
 
 /* RTN INT8 group-128 quantization of a row-major bf16 [n][k] into the W8 layout: scale = bf16(amax/127),
  * q = clamp(rint(v/scale), -127, 127). Replaces reference src/capi.cpp:124 (quantize_w8, gemv.cu:1085-1116). */

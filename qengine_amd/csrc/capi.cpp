@@ -22,6 +22,7 @@
 
 namespace {
 std::atomic<int> g_out_bf16{0};
+std::atomic<int> g_sk_maxparts{0};
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline W4 mk_w4(const void* q, const void* s, int n, int k, bool glu, int sdt) {
     W4 w;
@@ -47,6 +48,8 @@ inline W8 mk_w8(const void* q, const void* s, int n, int k, bool per_channel, in
 
 void gemm_set_out_bf16(bool on) { g_out_bf16.store(on ? 1 : 0); }
 bool gemm_out_bf16() { return g_out_bf16.load() != 0; }
+void gemm_set_sk_maxparts(int n) { g_sk_maxparts.store(n > 0 ? n : 0); }
+int gemm_sk_maxparts() { return g_sk_maxparts.load(); }
 
 extern "C" {
 
@@ -172,6 +175,7 @@ void qe_gemm_w4_s(const void* q, const void* s, int n, int k, const uint16_t* x,
 }
 
 void qe_gemm_set_out_bf16(int on) { gemm_set_out_bf16(on != 0); }
+void qe_gemm_set_sk_maxparts(int n) { gemm_set_sk_maxparts(n); }
 
 void qe_xh_pack(const uint16_t* x, int k, int m, void* xh, int ldxh) {
     xh_pack(x, k, k, m, reinterpret_cast<uint16_t*>(xh), ldxh, 0);

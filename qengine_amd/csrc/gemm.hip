@@ -631,6 +631,13 @@ GemmChoice gemm_tune_choice(int n, int k, const uint16_t* x, int ldx, int t, voi
     return cl[best];
 }
 
+// the largest split <= ks that qe_gemm_set_sk_maxparts allows (splits are 1, 2 or 4)
+int capped_split(int ks) {
+    const int cap = gemm_sk_maxparts();
+    while (cap > 0 && ks > cap) ks /= 2;
+    return ks < 1 ? 1 : ks;
+}
+
 template <int FMT, int SDT>
 void launch_gemm(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, int ldx, int t, void* c, int ldc,
                  int out, int sdt, bool tuned, hipStream_t st) {
@@ -646,7 +653,7 @@ void launch_gemm(const uint4* q, const uint16_t* s, int n, int k, const uint16_t
             ch = gemm_model_choice(n, k, t);
         }
     }
-    run_choice<FMT, SDT>(ch.cfg, ch.ks, q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
+    run_choice<FMT, SDT>(ch.cfg, capped_split(ch.ks), q, s, n, k, x, ldx, t, c, ldc, out, sdt, st);
 }
 
 void gemm_check(int n, int k, const void* x, int ldx, int ldc, int t, bool glu) {

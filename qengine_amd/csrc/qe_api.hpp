@@ -127,6 +127,9 @@ void gemm_set_out_bf16(bool on);
 // reserve the split-K workspace of (the current device, st) (grown on demand otherwise, never during graph capture)
 void gemm_reserve(size_t bytes, hipStream_t st);
 bool gemm_out_bf16();
+// run-time cap of the split count of the prefill GEMMs' last partial round (0 or less: no cap, i.e. up to 4)
+void gemm_set_sk_maxparts(int n);
+int gemm_sk_maxparts();
 
 // GEMV for m <= 32 (split into row blocks of 16), GEMM above (reference gemv.cuh:187-190)
 void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);

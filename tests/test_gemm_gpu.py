@@ -207,6 +207,35 @@ def test_gemm_split_tail(dev, cfg, ks):
     assert np.all(np.abs(agv - a1v) <= 1e-5 * np.sqrt(np.mean(a1v ** 2)) + 2.0 ** -7 * np.abs(a1v))
 
 
+def test_gemm_sk_maxparts(dev):
+    """qe_gemm_set_sk_maxparts caps the split of the last partial round: on SPLIT_SHAPE the cost model splits it in 2
+    (bits of the (0, 2) choice); with the cap at 1 the same call is the unsplit (0, 1) GEMM bit for bit, and the
+    reference-named hook is honoured by qe_gemm_w4 too; cap 0 restores the split"""
+    n, k, t = SPLIT_SHAPE
+    w, q, s = setup(n, k, 0, seed=8)  # bf16 scales: the reference-named qe_gemm_w4 takes them
+    x = synth.to_dev(synth.x_host(t, k, seed=9))
+    call("qe_gemm_tune_clear")
+    split, applied = ops.gemm_w4_choice(w, x, 0, 2)
+    whole, _ = ops.gemm_w4_choice(w, x, 0, 1)
+    assert applied
+    try:
+        y0 = ops.gemm_w4(w, x)
+        call("qe_gemm_set_sk_maxparts", 1)
+        y1 = ops.gemm_w4(w, x)
+        yr = torch.empty(t, n, dtype=torch.float32, device=dev)
+        call("qe_gemm_w4", w.q, w.s, n, k, x, yr, t)
+        call("qe_gemm_set_sk_maxparts", 3)  # 2 or 3: a split in 2 stays allowed
+        y3 = ops.gemm_w4(w, x)
+    finally:
+        call("qe_gemm_set_sk_maxparts", 0)
+    y00 = ops.gemm_w4(w, x)
+    torch.cuda.synchronize()
+    iv = torch.int32
+    assert torch.equal(y0.view(iv), split.view(iv)) and torch.equal(y00.view(iv), split.view(iv))
+    assert torch.equal(y1.view(iv), whole.view(iv)) and torch.equal(yr.view(iv), whole.view(iv))
+    assert torch.equal(y3.view(iv), split.view(iv))
+
+
 def test_gemm_tuner_table_and_file(dev, tmp_path):
     """qe_gemm_w4_t times the candidates once per (shape, token bucket) and keeps the choice; with a tuning file the
     choice survives a cleared table (reloaded from the file) and the output is bit-identical"""
