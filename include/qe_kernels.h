@@ -110,6 +110,13 @@ void qe_gemm_i8_reserve_s(int k, int t, void* stream);
  * unsplit and returns 0). The reference's QE_GEMM_FORCE (src/kernels/gemm.cu:4376-4394). */
 int qe_gemm_w4_choice(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                       int flags, int cfg, int ks, void* stream);
+/* test hook: the one-pass decode GEMM of qe_matmul_w4_ex for m = 1..64 rows whatever the dispatch would pick (the
+ * weights read once for all rows, as the reference's wide decode GEMVs, src/kernels/gemv_x.cu:902-980; this build's
+ * decode numerics: the exact products (u - 8) x summed in fp32 and scaled once per 128-k group). Returns 0 without
+ * running when the shape does not fit it (n % 64, x not 16-byte aligned or ldx % 8, K / 64 not an even number of
+ * steps per wave), else 1. */
+int qe_matmul_w4_onepass_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy,
+                            int m, int flags, void* stream);
 
 /* Measurement helper (no reference counterpart): streams the n*k/2 record bytes of a W4 matrix with the launch shape
  * of the m = 1 decode GEMV (n/16 blocks, its K slices) and does nothing else, the HBM read floor that GEMV is held
@@ -139,10 +146,11 @@ void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, f
  * Replaces reference src/capi.cpp:52. */
 void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);
 
-/* skinny GEMM, bit-identical to qe_gemv_w4g for every row count; m = 1..32 (the reference's skinny_w4 range,
- * skinny.cu:572): 17..32 rows run as one launch of the wide kernel, which needs 16-byte aligned rows (k % 8 == 0)
- * and an even K slicing. Returns 0 (nothing written) when the shape is unsupported, 1 when it ran. Replaces
- * reference src/capi.cpp:79-83 (skinny_w4, skinny.cu:572-604). */
+/* skinny GEMM, bit-identical to qe_gemv_w4g for every row count (it is qe_gemv_w4g's decode dispatch); m = 1..32
+ * (the reference's skinny_w4 range, skinny.cu:572): 17..32 rows run as one launch (the one-pass kernel, or with
+ * batch_invariant the wide skinny kernel), which needs 16-byte aligned rows and an even K slicing. Returns 0 (nothing
+ * written) when the shape is unsupported, 1 when it ran. Replaces reference src/capi.cpp:79-83 (skinny_w4,
+ * skinny.cu:572-604). */
 int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);
 
 /* qe_gemv_w4 on an explicit stream. Replaces reference src/capi.cpp:101. */

@@ -109,6 +109,14 @@ void qe_gemm_w4_i8_ex(const void* q, const void* s, int n, int k, const uint16_t
                ldy, t, G, (flags & QE_OUT_BF16) != 0, as_stream(st));
 }
 
+int qe_matmul_w4_onepass_ex(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy,
+                            int m, int flags, void* stream) {
+    const W4 w = mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16);
+    if (!wdec_w4_fits(w, x, ldx, m)) return 0;
+    wdec_w4(w, x, ldx, y, ldy, m, (flags & QE_OUT_BF16) != 0, as_stream(stream));
+    return 1;
+}
+
 int qe_gemm_w4_choice(const void* q, const void* s, int n, int k, const uint16_t* x, int ldx, void* y, int ldy, int t,
                       int flags, int cfg, int ks, void* stream) {
     const W4 w = mk_w4(q, s, n, k, (flags & QE_GLU) != 0, (flags & QE_SCALE_F16) ? kScaleF16 : kScaleBF16);
@@ -144,16 +152,20 @@ void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, 
     matmul_w4(mk_w4(q, s, n, k, glu != 0, kScaleBF16), x, k, y, glu ? n / 2 : n, m, false, 0);
 }
 
-// the reference's skinny_w4 takes 1..32 rows (src/kernels/skinny.cu:572); here 1..16 rows run the decode GEMV and
-// 17..32 rows one launch of the wide skinny kernel, which needs 16-byte aligned rows and an even K slicing (else 0:
-// unsupported, the caller falls back to qe_gemv_w4 as the reference's callers do)
+// the reference's skinny_w4 takes 1..32 rows (src/kernels/skinny.cu:572) and equals its GEMV bit for bit; here it is
+// the decode dispatch of qe_gemv_w4g itself (matmul_w4: 1..16 rows the decode GEMV / skinny kernel, 17..32 the
+// one-pass kernel, or with batch_invariant the 32-row skinny launch), so the bits are equal by construction. 17..32
+// rows that neither of those one-launch kernels takes (x not 16-byte aligned, K slicing) return 0: unsupported, the
+// caller falls back to qe_gemv_w4 as the reference's callers do.
 int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu) {
     if (m < 1 || m > kWideRows || n <= 0 || k <= 0 || n % 16 != 0 || k % 128 != 0 || k % 8 != 0) return 0;
     const W4 w = mk_w4(q, s, n, k, glu != 0, kScaleBF16);
-    if (m > kMaxGemvRows && !skinny_w4_wide_fits(w, x, k)) return 0;
+    if (m > kMaxGemvRows) {
+        const bool onepass = !qe_config().batch_invariant && wdec_w4_fits(w, x, k, m);
+        if (!onepass && !skinny_w4_wide_fits(w, x, k)) return 0;
+    }
     gemv_workspace_init();
-    if (m > kMaxGemvRows) skinny_w4_wide(w, x, k, y, glu ? n / 2 : n, m, false, 0);
-    else gemv_w4(w, x, k, y, glu ? n / 2 : n, m, false, 0);
+    matmul_w4(w, x, k, y, glu ? n / 2 : n, m, false, 0);
     return 1;
 }
 

@@ -706,6 +706,12 @@ void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m,
         gemm_w4(w, x, ldx, y, ldy, m, out_bf16, st);
         return;
     }
+    // 17..64 rows: one pass over the weights (wdec.hip) where the shape fits it, unless every row must keep the bits
+    // it has alone (batch_invariant)
+    if (m > kMaxGemvRows && !qe_config().batch_invariant && wdec_w4_fits(w, x, ldx, m)) {
+        wdec_w4(w, x, ldx, y, ldy, m, out_bf16, st);
+        return;
+    }
     // row blocks: 32 rows per launch (the skinny kernel's wide variant) while more than 16 remain and the rows are
     // 16-byte aligned, else 16; a row's bits do not depend on the block it falls in
     const size_t esz = (w.glu || out_bf16) ? 2 : 4;

@@ -23,6 +23,12 @@ __device__ __forceinline__ uint32_t nib_mask() {
     asm("s_mov_b32 %0, 0x0f0f0f0f" : "=s"(m));
     return m;
 }
+// 0xF0F0F0F0 in an SGPR (as nib_mask)
+__device__ __forceinline__ uint32_t nib_mask_hi() {
+    uint32_t m;
+    asm("s_mov_b32 %0, 0xf0f0f0f0" : "=s"(m));
+    return m;
+}
 
 template <int SDT>
 __device__ __forceinline__ float scale_rt(uint16_t v, int sdt) {

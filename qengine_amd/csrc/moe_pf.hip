@@ -39,13 +39,6 @@ constexpr int kScWave = 256;                 // one wave's scales of one k step:
 constexpr int kRawOff = NBUF * kXStage, kScOff = kRawOff + NBUF * 8 * kRawWave;
 constexpr int kLds = kScOff + NBUF * 8 * kScWave;  // 136 KB: every buffer four deep (steps kt .. kt + 3)
 
-// 0xF0F0F0F0 in an SGPR (see nib_mask)
-__device__ __forceinline__ uint32_t nib_mask_hi() {
-    uint32_t m;
-    asm("s_mov_b32 %0, 0xf0f0f0f0" : "=s"(m));
-    return m;
-}
-
 // MODE 1: gate_up, N = 2 I GLU rows (records of 256 rows x K = H), epilogue act[slot][I] = silu(gate) up w_slot.
 // MODE 2: down, N = H rows, K = I over the expert's records (128 k each), epilogue slot_out[slot][H].
 // NA: 32-row token tiles holding a row of the job (the others are not computed). SHORT: K = 128 (two k steps).

@@ -54,6 +54,11 @@ void skinny_w4_mfma(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, i
 // 17..32 rows in one pass (INT4, x 16-byte aligned, ldx % 8 == 0); the rows' bits equal the 16-row launches'
 void skinny_w4_wide(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 bool skinny_w4_wide_fits(const W4& w, const uint16_t* x, int ldx);
+// one pass over the weights for 1..64 rows (wdec.hip): the decode numerics (exact (u - 8) x products, group scale on
+// the fp32 sums) on the 32 x 32 matrix cores, K split over the waves of a block, fixed-order sums; n % 64 == 0, x
+// 16-byte aligned, ldx % 8 == 0 and the K steps even per wave (wdec_w4_fits)
+bool wdec_w4_fits(const W4& w, const uint16_t* x, int ldx, int m);
+void wdec_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 // the same kernel on W8 / Q8 records (GLU for Q8): m = 1..16, x 16-byte aligned, ldx % 8 == 0
 void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st);
 // m = 1 decode GEMV on the matrix cores (gemv1.hip); false when the shape takes the VALU GEMV (uneven K slices,

@@ -47,9 +47,10 @@ enum QeFlags : int {
 constexpr int kMaxGemvRows = 16;   // VALU decode GEMV / skinny GEMM: m = 1..16 rows per launch
 constexpr int kWideRows = 32;      // the INT4 skinny kernel's wide variant: 17..32 rows per launch
 constexpr int kMaxGemvW4Tokens = 32;  // reference matmul(): m <= 32 -> GEMV, else GEMM (gemv.cuh:187-190)
-// this build's matmul_w4 dispatch: the decode kernels (16-row launches) up to 64 rows, the GEMM above. Measured on
-// MI355X (N = 17408, K = 5120): the 256-token-tile GEMM takes about 82 us for any m in 33..64 (68 tiles on 256 CUs),
-// two to four 16-row launches 48 to 73 us; every row of a 1..64-row call then has the same bits as alone
+// this build's matmul_w4 dispatch: the decode kernels up to 64 rows, the GEMM above. Measured on MI355X (N = 17408,
+// K = 5120): the 256-token-tile GEMM takes about 82 us for any m in 33..64 (68 tiles on 256 CUs). 17..64 rows run the
+// one-pass kernel (wdec.hip: m = 32 / 64 in 26 / 40 us against 29 / 58 us for 32-row skinny launches); with
+// batch_invariant, 16- and 32-row skinny launches, so every row of a 1..64-row call has the same bits as alone
 constexpr int kMatmulGemvRows = 64;
 
 #ifdef __HIPCC__

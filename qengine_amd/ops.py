@@ -201,6 +201,19 @@ def gemm_w4_choice(w: W4, x, cfg, ks, out_bf16=False, y=None):
     return y, bool(r)
 
 
+def matmul_w4_onepass(w: W4, x, out_bf16=False, y=None):
+    """the one-pass decode GEMM (qe_matmul_w4_onepass_ex) for 1..64 rows (the decode numerics: unrounded weights);
+    returns y, or None if the shape does not fit it"""
+    t = x.shape[0]
+    assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1
+    y = _out(t, w.n, out_bf16, w.glu, x.device) if y is None else y
+    from .qe import lib
+    lib().qe_matmul_w4_onepass_ex.restype = ctypes.c_int
+    r = call("qe_matmul_w4_onepass_ex", w.q, w.s, w.n, w.k, x, x.stride(0), y, y.stride(0), t,
+             w.flags | (OUT_BF16 if out_bf16 else 0), _stream())
+    return y if r else None
+
+
 def matmul_w4(w: W4, x, out_bf16=False, y=None):
     t = x.shape[0]
     assert x.dtype == torch.bfloat16 and x.shape[1] == w.k and x.stride(1) == 1

@@ -70,8 +70,8 @@ def test_gemm_w4_strided_output(dev, glu):
 
 
 def test_gemm_matches_gemv_rows(dev):
-    """matmul dispatch: m <= 64 runs the decode GEMV (16-row launches), from 65 rows the GEMM; both meet the gate on
-    the same rows. The GEMV multiplies the exact weights (u - 8) * s, the GEMM their bf16 rounding (the reference's
+    """matmul dispatch: m <= 64 runs the decode kernels (here the one-pass kernel for 64 rows), from 65 rows the GEMM;
+    both meet the gate on the same rows. The decode kernels multiply the exact weights (u - 8) * s, the GEMM their bf16 rounding (the reference's
     operand), so a row's result at m = 64 and m = 65 differs by at most the weight rounding:
     |dy| <= 2^-9 * sum_k |x_k (u_k - 8) s_k| (plus fp32 summation noise), checked element by element"""
     n, k = 1024, 2048
@@ -81,7 +81,7 @@ def test_gemm_matches_gemv_rows(dev):
     ref = oracle_ref(xh, q, s, n, k, 1)
     yg = out_f32(ops.matmul_w4(w, x))                       # GEMM (96 rows)
     y65 = out_f32(ops.matmul_w4(w, x[:65].contiguous()))    # GEMM (65 rows)
-    y64 = out_f32(ops.matmul_w4(w, x[:64].contiguous()))    # GEMV (64 rows in four launches)
+    y64 = out_f32(ops.matmul_w4(w, x[:64].contiguous()))    # decode (64 rows, one pass)
     assert err_ratio(yg, ref) <= 1e-4 and err_ratio(y64, ref[:64]) <= TOL
     assert err_ratio(y64, matmul_f64(xh[:64], exact_w4(q, s, n, k, 1))) <= 1e-4
     wabs = np.abs(exact_w4(q, s, n, k, 1)).astype(np.float64)
