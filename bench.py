@@ -71,13 +71,18 @@ def time_launches(fn, steps, warmup, nvar, graph=False):
     (ctypes + torch stream lookup, comparable to a 10 us kernel) never starves the GPU: the per-step figure is
     then the kernel's duration plus the dispatch gap between consecutive graph nodes."""
     import torch
-    for i in range(warmup):
-        fn(i % nvar)
+    # graph: the warmup runs on the capture stream, as a serving loop warms the stream it captures on (stream-owned
+    # workspaces, e.g. the one-pass decode's tail counters, are set up by the eager calls)
+    cs = torch.cuda.Stream() if graph else torch.cuda.current_stream()
+    cs.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(cs):
+        for i in range(warmup):
+            fn(i % nvar)
     torch.cuda.synchronize()
     run = lambda: [fn(i % nvar) for i in range(steps)]  # noqa: E731
     if graph:
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
+        with torch.cuda.graph(g, stream=cs):
             run()
         # upload, then untimed replays queued back to back (>= 30 ms of work) so the timed pass starts with the
         # GPU at its working clock: a pass started from idle runs ~15 % slower for its first milliseconds

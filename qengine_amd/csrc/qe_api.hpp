@@ -99,9 +99,10 @@ void qe_config_set(const QeConfig& c);
 void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 
 // ---- library-owned workspaces, one per (kind, device, stream) (workspace.cpp) ----
-enum WsKind : int { kWsSplit = 0, kWsI8 = 1, kWsH = 2, kNumWs = 3 };
+enum WsKind : int { kWsSplit = 0, kWsI8 = 1, kWsH = 2, kWsDec = 3, kNumWs = 4 };
 // the buffer of (kind, current device, st), at least `bytes`: grown outside graph capture (the outgrown one kept
-// allocated); nullptr during capture when it is too small
+// allocated); nullptr during capture when it is too small. kWsDec buffers (the one-pass decode's tail counters and
+// sums) are zero-filled when allocated; the kernel leaves its counters zero.
 void* stream_ws(int kind, size_t bytes, hipStream_t st);
 void stream_ws_reserve(int kind, size_t bytes, hipStream_t st);
 int stream_ws_count(int kind);  // buffers of that kind allocated so far (all devices and streams)

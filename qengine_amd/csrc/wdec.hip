@@ -42,18 +42,26 @@ constexpr int kPart = 68;                     // floats per token row of a wave'
 static_assert(NW * 32 * kPart * 4 <= kLds, "the partial sums fit the staging buffers");
 
 // TB token blocks of 32 rows (m <= 32 TB), out: 0 fp32, 1 bf16, 2 GLU (bf16 activation, n / 2 columns)
+// Blocks [0, nmain): one slab each over the whole K. Blocks past nmain: part p = u % P of tail slab nmain + u / P
+// (u = block - nmain), over K steps [p KT / P, (p + 1) KT / P); its sums go to tpart[u] ([TB * 32 tokens][64 rows]
+// fp32, written through to the device-coherent level), then it adds one to tctr[u / P]; the part that brings the
+// count to P adds the P parts in order p = 0..P-1, stores the outputs and sets the count back to zero (the counters
+// are zero when their buffer is allocated). P = 1: no tail blocks.
 template <int SDT, int TB>
 __global__ void __launch_bounds__(NTH, 2) wdec_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s,
                                                       int K, const uint16_t* __restrict__ x, int ldx, int M,
-                                                      void* __restrict__ y, int ldy, int out) {
+                                                      void* __restrict__ y, int ldy, int out, int nmain, int P,
+                                                      float* __restrict__ tpart, uint32_t* __restrict__ tctr) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     constexpr int KP = NW / TB;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const unsigned lds32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)lds);
     const int tb = wave / KP, kp = wave - tb * KP;
-    const int KTw = (K / BK) / KP, kt0 = kp * KTw, G = K >> 7;
-    const int tile0 = blockIdx.x * 4;  // the block's four 16-row tiles
+    const int b = blockIdx.x, tail = b >= nmain ? b - nmain : -1;  // tail part index u, or -1
+    const int slab = tail < 0 ? b : nmain + tail / P, KTb = tail < 0 ? K / BK : K / BK / P;
+    const int KTw = KTb / KP, kt0 = (tail < 0 ? 0 : (tail % P) * KTb) + kp * KTw, G = K >> 7;
+    const int tile0 = slab * 4;  // the block's four 16-row tiles
     const int mr = lane & 31, kh = lane >> 5, g = mr & 7;
     auto buf_at = [&](int b) { return (b * NW + wave) * kBuf; };  // byte offset of this wave's buffer b
 
@@ -230,33 +238,68 @@ __global__ void __launch_bounds__(NTH, 2) wdec_kernel(const uint4* __restrict__ 
         return p[0];
     };
     const int n0 = tile0 * 16;
-    if (out == 2) {  // thread = (token, tile, row quad of the 8 gate rows): gate rows g, up rows g + 8
-        for (int o = tid; o < TB * 32 * 8; o += NTH) {
-            const int otb = o >> 8, tok = (o >> 3) & 31, qq = (o >> 1) & 3, gq = o & 1;
+    // the epilogue of 4 consecutive rows r4 of token otb * 32 + tok, from get4(otb, tok, r4)
+    auto emit = [&](auto&& get4) {
+        if (out == 2) {  // thread = (token, tile, row quad of the 8 gate rows): gate rows g, up rows g + 8
+            for (int o = tid; o < TB * 32 * 8; o += NTH) {
+                const int otb = o >> 8, tok = (o >> 3) & 31, qq = (o >> 1) & 3, gq = o & 1;
+                const int t = 32 * otb + tok;
+                if (t >= M) continue;
+                const f32x4_v ga = get4(otb, tok, 16 * qq + 4 * gq), up = get4(otb, tok, 16 * qq + 8 + 4 * gq);
+                uint16_t* p = reinterpret_cast<uint16_t*>(y) + (size_t)t * ldy + (tile0 + qq) * 8 + 4 * gq;
+#pragma unroll
+                for (int i = 0; i < 4; i++) p[i] = f32_to_bf16(silu_f32(ga[i]) * up[i]);
+            }
+            return;
+        }
+        for (int o = tid; o < TB * 32 * 16; o += NTH) {  // thread = (token, 4 consecutive rows)
+            const int otb = o >> 9, tok = (o >> 4) & 31, r4 = 4 * (o & 15);
             const int t = 32 * otb + tok;
             if (t >= M) continue;
-            const f32x4_v ga = sum4(otb, tok, 16 * qq + 4 * gq), up = sum4(otb, tok, 16 * qq + 8 + 4 * gq);
-            uint16_t* p = reinterpret_cast<uint16_t*>(y) + (size_t)t * ldy + (tile0 + qq) * 8 + 4 * gq;
+            const f32x4_v v = get4(otb, tok, r4);
+            if (out == 1) {
+                uint16_t* p = reinterpret_cast<uint16_t*>(y) + (size_t)t * ldy + n0 + r4;
 #pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = f32_to_bf16(silu_f32(ga[i]) * up[i]);
+                for (int i = 0; i < 4; i++) p[i] = f32_to_bf16(v[i]);
+            } else {
+                float* p = reinterpret_cast<float*>(y) + (size_t)t * ldy + n0 + r4;
+#pragma unroll
+                for (int i = 0; i < 4; i++) p[i] = v[i];
+            }
         }
+    };
+    if (tail < 0) {
+        emit(sum4);
         return;
     }
-    for (int o = tid; o < TB * 32 * 16; o += NTH) {  // thread = (token, 4 consecutive rows)
+    // a tail part: its sums to tpart[tail] (device-coherent stores), completed before the count
+    constexpr int kPartFloats = TB * 32 * 64;
+    float* mine = tpart + (size_t)tail * kPartFloats;
+    for (int o = tid; o < TB * 32 * 16; o += NTH) {
         const int otb = o >> 9, tok = (o >> 4) & 31, r4 = 4 * (o & 15);
-        const int t = 32 * otb + tok;
-        if (t >= M) continue;
         const f32x4_v v = sum4(otb, tok, r4);
-        if (out == 1) {
-            uint16_t* p = reinterpret_cast<uint16_t*>(y) + (size_t)t * ldy + n0 + r4;
 #pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = f32_to_bf16(v[i]);
-        } else {
-            float* p = reinterpret_cast<float*>(y) + (size_t)t * ldy + n0 + r4;
-#pragma unroll
-            for (int i = 0; i < 4; i++) p[i] = v[i];
-        }
+        for (int i = 0; i < 4; i++)
+            __hip_atomic_store(mine + (otb * 32 + tok) * 64 + r4 + i, v[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __shared__ uint32_t last;
+    __syncthreads();
+    const int ts = tail / P;
+    if (tid == 0) last = atomicAdd(&tctr[ts], 1u) == (uint32_t)P - 1u;
+    __syncthreads();
+    if (!last) return;
+    const float* all = tpart + (size_t)ts * P * kPartFloats;  // parts p = 0..P-1 of this tail slab
+    emit([&](int otb, int tok, int r4) {  // the parts in order p = 0..P-1
+        f32x4_v v = {0.f, 0.f, 0.f, 0.f};
+        for (int pp = 0; pp < P; pp++) {
+            float* src = const_cast<float*>(all) + (size_t)pp * kPartFloats + (otb * 32 + tok) * 64 + r4;
+#pragma unroll
+            for (int i = 0; i < 4; i++) v[i] += __hip_atomic_load(src + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return v;
+    });
+    if (tid == 0) __hip_atomic_store(&tctr[ts], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 int token_blocks(int m) { return m > 32 ? 2 : 1; }
@@ -270,13 +313,43 @@ bool wdec_w4_fits(const W4& w, const uint16_t* x, int ldx, int m) {
     return KT % KP == 0 && (KT / KP) % 2 == 0;
 }
 
+// Slabs past the last whole round of CUs (N / 64 = 272 on 256 CUs: 16) would give 16 CUs two slabs; they run as P
+// K parts each instead (tail blocks, sharing CUs with the whole slabs), so no CU gets two slabs' work: P the first
+// of 5, 4, 8, 10, 2 with the tail blocks at most one round and an even number of steps per wave, if the stream's
+// zero-initialised workspace (kWsDec: counters, then the parts' sums) is at hand (not allocated during graph
+// capture: then P = 1). The last part's in-order sum reads the P parts from the device-coherent level, one part at
+// a time, so fewer parts finish sooner: on C0's matrix (16 tail slabs, 80 K steps) P = 5 measured m = 32 / 64
+// 20.7 / 31.7 us against 22.9 / 36.9 us at P = 10, 23.1 / 33.3 us at P = 2, and 26.7 / 40.0 us with no tail split.
 void wdec_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st) {
     using namespace qe_wdec;
     CHECK(wdec_w4_fits(w, x, ldx, m), "wdec_w4: n %d k %d m %d ldx %d", w.n, w.k, m, ldx);
     CHECK(ldy >= (w.glu ? w.n / 2 : w.n), "wdec_w4 ldy %d", ldy);
     const int out = w.glu ? 2 : out_bf16 ? 1 : 0;
-    const dim3 grid((unsigned)(w.n / 64)), block(NTH);
-#define QE_WDEC(SDT_, TB_) wdec_kernel<SDT_, TB_><<<grid, block, kLds, st>>>(w.q, w.s, w.k, x, ldx, m, y, ldy, out)
+    const int TB = token_blocks(m), KP = NW / TB, KT = w.k / BK, nslabs = w.n / 64, ncu = qe_num_cus();
+    int nmain = nslabs, P = 1, rem = 0;
+    float* tpart = nullptr;
+    uint32_t* tctr = nullptr;
+    if (nslabs > ncu && nslabs % ncu != 0) {
+        rem = nslabs % ncu;
+        for (int p : {5, 4, 8, 10, 2})
+            if (rem * p <= ncu && KT % (p * KP) == 0 && (KT / (p * KP)) % 2 == 0) {
+                // one size for every shape (at most ncu tail blocks of two token blocks), so a stream's first call
+                // sizes it for all later ones, graph captures included
+                const size_t cbytes = ((size_t)ncu * 4 + 255) / 256 * 256;
+                char* ws = static_cast<char*>(stream_ws(kWsDec, cbytes + (size_t)ncu * 2 * 32 * 64 * 4, st));
+                if (ws) {
+                    P = p;
+                    tctr = reinterpret_cast<uint32_t*>(ws);
+                    tpart = reinterpret_cast<float*>(ws + cbytes);
+                    nmain = nslabs - rem;
+                }
+                break;
+            }
+    }
+    const dim3 grid((unsigned)(nmain + (P > 1 ? rem * P : 0))), block(NTH);
+#define QE_WDEC(SDT_, TB_)                                                                                    \
+    wdec_kernel<SDT_, TB_><<<grid, block, kLds, st>>>(w.q, w.s, w.k, x, ldx, m, y, ldy, out, nmain, P, tpart, \
+                                                      tctr)
     if (w.sdt == kScaleF16) {
         if (token_blocks(m) == 2) QE_WDEC(kScaleF16, 2);
         else QE_WDEC(kScaleF16, 1);

@@ -1,5 +1,5 @@
 // Library-owned workspaces of the prefill GEMMs (split-K partial sums, the W4A8 / W8A8 and fp16-accumulate
-// pre-pass buffers), one buffer per (kind, device, stream).
+// pre-pass buffers) and of the one-pass decode's tail (counters and part sums), one buffer per (kind, device, stream).
 //
 // The reference keeps these buffers thread_local (src/kernels/gemm.cu:3258-3368), so two host threads never share
 // one. Here the key is the stream a call is enqueued on: calls on one stream run in order, so they can share a
@@ -37,6 +37,10 @@ void* stream_ws(int kind, size_t bytes, hipStream_t st) {
     if (cs != hipStreamCaptureStatusNone) return nullptr;
     void* np = nullptr;
     HIP_CHECK(hipMalloc(&np, bytes));
+    if (kind == kWsDec) {  // counters start at zero (the kernel sets them back to zero at the end of every call)
+        HIP_CHECK(hipMemsetAsync(np, 0, bytes, st));
+        HIP_CHECK(hipStreamSynchronize(st));
+    }
     if (w.p) g_retired.push_back(w.p);
     w.p = np;
     w.bytes = bytes;

@@ -81,3 +81,50 @@ def test_onepass_shape_checks(dev):
     xb = torch.zeros(4 * 2048 + 1, dtype=torch.bfloat16, device=dev)[1:].view(4, 2048)
     w3, _, _ = setup_w4(1024, 2048, 1, seed=94)
     assert ops.matmul_w4_onepass(w3, xb) is None
+
+
+def test_onepass_tail_parts_deterministic_and_graph(dev):
+    """N = 17408 has 272 slabs of 64 rows: the 16 past the last whole round of 256 CUs run as K parts added by the
+    last part to finish (a device-side count per tail slab, zero again after every call). Repeated calls, calls of
+    other shapes in between, and a HIP graph captured on a stream that ran the kernel eagerly all give the same bits;
+    a capture on a stream without its workspace runs the tail slabs whole (another summation order), within the same
+    1e-4 * rms of the exact product"""
+    n, k = 17408, 5120
+    w, q, s = setup_w4(n, k, 1, seed=95)
+    xh = synth.x_host(40, k, seed=96)
+    x = synth.to_dev(xh)
+    exact = matmul_f64(xh, exact_w4(q, s, n, k, 1))
+    iv = torch.int32
+    for m in (40, 8):
+        xm = x[:m].contiguous()
+        y1 = ops.matmul_w4_onepass(w, xm)
+        w2, _, _ = setup_w4(4096, 2048, 1, seed=97)
+        ops.matmul_w4_onepass(w2, synth.to_dev(synth.x_host(3, 2048, seed=98)))  # another shape in between
+        y2 = ops.matmul_w4_onepass(w, xm)
+        torch.cuda.synchronize()
+        assert torch.equal(y1.view(iv), y2.view(iv)), m
+        assert err_ratio(y1.cpu().numpy(), exact[:m]) <= 1e-4
+        for warm in (True, False):
+            cs = torch.cuda.Stream()
+            cs.wait_stream(torch.cuda.current_stream())
+            x_in = xm.clone()
+            out = torch.empty(m, n, dtype=torch.float32, device=dev)
+            if warm:
+                with torch.cuda.stream(cs):
+                    ops.matmul_w4_onepass(w, x_in, y=out)
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cs):
+                ops.matmul_w4_onepass(w, x_in, y=out)
+            for r in range(3):
+                xr = synth.to_dev(synth.x_host(m, k, seed=100 + r))
+                want = ops.matmul_w4_onepass(w, xr)
+                torch.cuda.synchronize()
+                x_in.copy_(xr)
+                g.replay()
+                torch.cuda.synchronize()
+                if warm:
+                    assert torch.equal(out.view(iv), want.view(iv)), (m, r)
+                else:
+                    rr = err_ratio(out.cpu().numpy(), want.cpu().numpy())
+                    assert rr <= 1e-5, (m, r, rr)
