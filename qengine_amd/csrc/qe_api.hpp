@@ -104,6 +104,11 @@ enum WsKind : int { kWsSplit = 0, kWsI8 = 1, kWsH = 2, kWsDec = 3, kNumWs = 4 };
 // allocated); nullptr during capture when it is too small. kWsDec buffers (the one-pass decode's tail counters and
 // sums) are zero-filled when allocated; the kernel leaves its counters zero.
 void* stream_ws(int kind, size_t bytes, hipStream_t st);
+// the stream's tail workspace of the decode kernels (kWsDec, one size for every shape): dec_tail_ctr_bytes() of
+// counters (one per tail tile or slab, at most one per CU), then the tail parts' sums (up to 2 x 32 x 64 floats per
+// CU); nullptr during a graph capture on a stream that has none yet
+char* dec_tail_ws(hipStream_t st);
+size_t dec_tail_ctr_bytes();
 void stream_ws_reserve(int kind, size_t bytes, hipStream_t st);
 int stream_ws_count(int kind);  // buffers of that kind allocated so far (all devices and streams)
 

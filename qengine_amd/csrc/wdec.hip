@@ -335,12 +335,11 @@ void wdec_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
             if (rem * p <= ncu && KT % (p * KP) == 0 && (KT / (p * KP)) % 2 == 0) {
                 // one size for every shape (at most ncu tail blocks of two token blocks), so a stream's first call
                 // sizes it for all later ones, graph captures included
-                const size_t cbytes = ((size_t)ncu * 4 + 255) / 256 * 256;
-                char* ws = static_cast<char*>(stream_ws(kWsDec, cbytes + (size_t)ncu * 2 * 32 * 64 * 4, st));
+                char* ws = dec_tail_ws(st);
                 if (ws) {
                     P = p;
                     tctr = reinterpret_cast<uint32_t*>(ws);
-                    tpart = reinterpret_cast<float*>(ws + cbytes);
+                    tpart = reinterpret_cast<float*>(ws + dec_tail_ctr_bytes());
                     nmain = nslabs - rem;
                 }
                 break;

@@ -47,6 +47,12 @@ void* stream_ws(int kind, size_t bytes, hipStream_t st) {
     return np;
 }
 
+size_t dec_tail_ctr_bytes() { return ((size_t)qe_num_cus() * 4 + 255) / 256 * 256; }
+
+char* dec_tail_ws(hipStream_t st) {
+    return static_cast<char*>(stream_ws(kWsDec, dec_tail_ctr_bytes() + (size_t)qe_num_cus() * 2 * 32 * 64 * 4, st));
+}
+
 void stream_ws_reserve(int kind, size_t bytes, hipStream_t st) {
     if (bytes > 0) CHECK(stream_ws(kind, bytes, st) != nullptr, "workspace reserve: called during graph capture");
 }
