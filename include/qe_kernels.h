@@ -138,8 +138,9 @@ void qe_gemv_workspace_init(void);
  * (dq: n*k/2 bytes, ds: n*k/128 16-bit). Replaces reference src/capi.cpp:13 (repack_w4, gemv.cu:1686-1694). */
 void qe_repack_w4(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds);
 
-/* y[m][n] (fp32, stride n) = x[m][k] (bf16, stride k) . W^T; any m (the decode GEMV in 16-row launches up to 64
- * rows, the prefill GEMM above, as qe_matmul_w4_ex). Replaces reference src/capi.cpp:47 (gemv_w4, gemv.cu:1585). */
+/* y[m][n] (fp32, stride n) = x[m][k] (bf16, stride k) . W^T; any m (1..16 rows: the decode GEMV; 17..64: the
+ * one-pass decode GEMM where the shape fits it, else the GEMV in 16-row launches, which batch_invariant always
+ * takes; the prefill GEMM above, as qe_matmul_w4_ex). Replaces reference src/capi.cpp:47 (gemv_w4, gemv.cu:1585). */
 void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m);
 
 /* as qe_gemv_w4; glu != 0: y is the bf16 activation [m][n/2] = bf16(silu(gate) * up).
