@@ -220,14 +220,140 @@ constexpr int st_xbytes() { return (NG * 256 + 1023) / 1024 * 1024; }
 template <int NG>
 constexpr int st_wbytes() { return st_xbytes<NG>() + 1024 + 256; }  // x, scales (NG x 32 B <= 1 KB), zeros
 
-template <int NG, int D, int SDT>
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 1 && N <= 5, "vm_wait");
+    if constexpr (N == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
+    else if constexpr (N == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
+    else if constexpr (N == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
+    else if constexpr (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(5)" ::: "memory");
+}
+
+// Quarter tiles. A grid of whole tiles leaves the CUs that receive one more tile than the others (C0: 1088 tiles, 64
+// CUs with a fifth) streaming after the rest have finished. The tiles past the last whole round of CUs therefore run
+// as four quarter blocks each, at the end of the grid: rows {2a, 2a + 1} (low nibbles) and {2a + 8, 2a + 9} (high
+// nibbles) of a tile are W4 lanes 8a .. 8a + 7 of every record, 128 contiguous bytes per 64-k step, and no sum
+// crosses blocks. A wave-load covers 8 steps of the wave's K slice: lane L = 8 st + 4 gq + t holds W4 lane
+// 4 (2a + gq) + t of step st, i.e. k = 64 st + 16 j + 2 t + {0, 1, 8, 9} of rows 2a + gq and 2a + gq + 8; the
+// products run on v_dot2 against the staged activations (dwords 32 st + t + 4 i), chained from -136 x their sum, and
+// are scaled per lane. Lanes past the slice (NG not a multiple of 4) load the slice's last step and add nothing.
+// Measured (m = 1, K = 5120): N = 17408 9.25 -> 8.83 us, N = 5120 5.48 -> 4.85 us; N = 14336, K = 4096 (two
+// quarters on half the CUs) 7.09 -> 6.74 us.
+template <int NG, int SDT>
+__device__ __forceinline__ void gemv1s_quarter(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int K,
+                                               const uint16_t* __restrict__ x, void* __restrict__ y, int out,
+                                               int tile, int a, char* lds8) {
+    constexpr int XB = st_xbytes<NG>(), WB = st_wbytes<NG>();
+    constexpr int NS = 2 * NG, NL = (NS + 7) / 8;  // 64-k steps of the slice, wave-loads of 8 steps
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const int G = K >> 7, gb = w * NG;
+    char* wl = lds8 + (size_t)w * WB;
+    const unsigned wl32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)wl);
+    float* red = reinterpret_cast<float*>(lds8 + (size_t)S * WB);  // [S][16]
+    // the slice's activations and scales by DMA, as for a whole tile, then every weight load of the slice
+    const char* xs0 = reinterpret_cast<const char*>(x) + (size_t)gb * 256;
+#pragma unroll
+    for (int r = 0; r < XB / 1024; r++) {
+        const int p = 64 * r + L < NG * 16 ? 64 * r + L : NG * 16 - 1;
+        qe_tile::dma16(xs0 + 16 * p, wl32 + 1024 * r);
+    }
+    {
+        const int p = L < NG * 2 ? L : NG * 2 - 1;
+        qe_tile::dma16(reinterpret_cast<const char*>(s + ((size_t)tile * G + gb) * 16) + 16 * p, wl32 + XB);
+    }
+    const int st = L >> 3, gq = (L >> 2) & 1, t = L & 3, g = 2 * a + gq;
+    const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + 4 * g + t;
+    u32x4_v wv[NL];
+#pragma unroll
+    for (int ld = 0; ld < NL; ld++) {
+        const int si = 8 * ld + st < NS ? 8 * ld + st : NS - 1;
+        wv[ld] = ld_stream(qp + (size_t)si * 32);
+    }
+    vm_wait<NL>();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    const uint32_t* xl = reinterpret_cast<const uint32_t*>(wl);
+    const uint16_t* sl = reinterpret_cast<const uint16_t*>(wl + XB);
+    constexpr uint32_t kBias = 0xC308C308u;  // bf16 (-136, -136)
+    float acc_lo = 0.f, acc_hi = 0.f;
+#pragma unroll
+    for (int ld = 0; ld < NL; ld++) {
+        const bool valid = NS % 8 == 0 || ld < NL - 1 || 8 * ld + st < NS;
+        const int si = valid ? 8 * ld + st : NS - 1;
+        const uint32_t* xb = xl + si * 32 + t;
+        uint32_t xd[8];  // x pairs (k, k + 1) of word j at 2 j, (k + 8, k + 9) at 2 j + 1
+#pragma unroll
+        for (int i = 0; i < 8; i++) xd[i] = xb[4 * i];
+        float cb = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) cb = dot2_bf16(kBias, xd[i], cb);
+        const u32x4_v r = wv[ld];
+        float lo = cb, hi = cb;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const uint32_t t0 = r[j] & kNib, t1 = (r[j] >> 4) & kNib;
+            lo = dot2_bf16(bf16x2_b02(t0), xd[2 * j], lo);
+            lo = dot2_bf16(bf16x2_b13(t0), xd[2 * j + 1], lo);
+            hi = dot2_bf16(bf16x2_b02(t1), xd[2 * j], hi);
+            hi = dot2_bf16(bf16x2_b13(t1), xd[2 * j + 1], hi);
+        }
+        const int grp = si >> 1;
+        const float s_lo = scale_to_f32<SDT>(sl[grp * 16 + g]), s_hi = scale_to_f32<SDT>(sl[grp * 16 + g + 8]);
+        const float nlo = fmaf(s_lo, lo, acc_lo), nhi = fmaf(s_hi, hi, acc_hi);
+        acc_lo = valid ? nlo : acc_lo;
+        acc_hi = valid ? nhi : acc_hi;
+    }
+    // t by DPP, the two steps of a 16-lane row by row_ror 8: lanes 16 r + 4 gq hold (row 2a + gq, row 2a + gq + 8)
+    // of steps 2 r, 2 r + 1; the four 16-lane rows and the S slices are added through LDS in a fixed order
+    constexpr int kDppRowRor8 = 0x128;
+    acc_lo = dpp_add<kDppXor1>(acc_lo);
+    acc_hi = dpp_add<kDppXor1>(acc_hi);
+    acc_lo = dpp_add<kDppXor2>(acc_lo);
+    acc_hi = dpp_add<kDppXor2>(acc_hi);
+    acc_lo = dpp_add<kDppRowRor8>(acc_lo);
+    acc_hi = dpp_add<kDppRowRor8>(acc_hi);
+    if ((L & 11) == 0) {
+        red[w * 16 + 4 * (L >> 4) + 2 * gq] = acc_lo;
+        red[w * 16 + 4 * (L >> 4) + 2 * gq + 1] = acc_hi;
+    }
+    __syncthreads();
+    if (threadIdx.x < 4) {
+        const int e = threadIdx.x;  // row 2a + e / 2 (+ 8 for odd e)
+        float v = 0.f;
+        for (int ws = 0; ws < S; ws++)
+            for (int rr = 0; rr < 4; rr++) v += red[ws * 16 + 4 * rr + e];
+        if (out == kOutGLU) {
+            const float up = __shfl_xor(v, 1, 64);  // lanes e, e ^ 1: gate and up of GLU output 2a + e / 2
+            if ((e & 1) == 0) reinterpret_cast<uint16_t*>(y)[8 * tile + 2 * a + (e >> 1)] = f32_to_bf16(silu_f32(v) * up);
+        } else {
+            const int row = 16 * tile + 2 * a + (e >> 1) + 8 * (e & 1);
+            if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[row] = f32_to_bf16(v);
+            else reinterpret_cast<float*>(y)[row] = v;
+        }
+    }
+}
+
+// QT: blocks tq.. are quarter blocks (b = blockIdx.x - tq: quarter b % 4 of tile tq + b / 4); the kernel without them
+// is a separate instance, whose code is then exactly the whole-tile kernel's (the branch alone, taken by no block,
+// cost up to 5 % on some shapes)
+template <int NG, int D, int SDT, bool QT>
 __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
 gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K,
-              const uint16_t* __restrict__ x, void* __restrict__ y, int out) {
+              const uint16_t* __restrict__ x, void* __restrict__ y, int out, int tq) {
     static_assert(NG * 32 <= 1024 && D >= 1 && D <= 4 && D < NG, "gemv1s slice");
     constexpr int XB = st_xbytes<NG>(), WB = st_wbytes<NG>();
     extern __shared__ __attribute__((aligned(16))) char lds8[];
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    if constexpr (QT) {
+        if (__builtin_expect((int)blockIdx.x >= tq, 0)) {
+            const int b = blockIdx.x - tq;
+            gemv1s_quarter<NG, SDT>(q, s, K, x, y, out, tq + (b >> 2), b & 3, lds8);
+            return;
+        }
+    }
     const int tile = blockIdx.x, G = K >> 7, gb = w * NG;
     char* wl = lds8 + (size_t)w * WB;
     const unsigned wl32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)wl);
@@ -251,10 +377,7 @@ gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N
 #pragma unroll
     for (int i = 0; i < D; i++) wv[i] = ld_stream(qp + (size_t)i * 64);
     reinterpret_cast<uint32_t*>(wl + XB + 1024)[L] = 0u;
-    if constexpr (D == 1) asm volatile("s_waitcnt vmcnt(1)" ::: "memory");
-    else if constexpr (D == 2) asm volatile("s_waitcnt vmcnt(2)" ::: "memory");
-    else if constexpr (D == 3) asm volatile("s_waitcnt vmcnt(3)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    vm_wait<D>();
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -361,10 +484,16 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
     const int sng = stream_groups(w.n, w.k);
     if (sng > 0) {
         const int S = w.k / 128 / sng;
-        const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
+        // the tiles past the last whole round of CUs as quarter blocks at the end of the grid
+        const int tiles = w.n / 16, ncu = qe_num_cus(), rem = tiles > ncu ? tiles % ncu : 0;
+        const int tq = tiles - rem;
+        const dim3 grid((unsigned)(tq + 4 * rem)), block(64 * S);
 #define QE_GEMV1S(NG_, SDT_)                                                                                  \
-    gemv1s_kernel<NG_, 3, SDT_><<<grid, block, (size_t)S * st_wbytes<NG_>() + (size_t)S * 64, st>>>(        \
-        w.q, w.s, w.n, w.k, x, y, out)
+    do {                                                                                                      \
+        const size_t lb = (size_t)S * st_wbytes<NG_>() + (size_t)S * 64;                                      \
+        if (rem) gemv1s_kernel<NG_, 3, SDT_, true><<<grid, block, lb, st>>>(w.q, w.s, w.n, w.k, x, y, out, tq); \
+        else gemv1s_kernel<NG_, 3, SDT_, false><<<grid, block, lb, st>>>(w.q, w.s, w.n, w.k, x, y, out, tq);   \
+    } while (0)
 #define QE_GEMV1S_NG(SDT_)                          \
     do {                                            \
         if (sng == 20) QE_GEMV1S(20, SDT_);         \

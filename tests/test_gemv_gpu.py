@@ -316,6 +316,35 @@ def test_gemv_long_slices(dev, n, k):
         assert_bf16_close(out_f32(ops.gemv_w8(w8, x[:m], out_bf16=True)), ref8[:m])
 
 
+# m = 1 grids whose tiles past the last whole round of the 256 CUs run as quarter blocks (4 rows each): slices of
+# 20 groups (5 wave-loads of 8 steps), 5 (the last wave-load 2 steps short), 8 with two quarters on half the CUs, 10
+# (the last wave-load half full) and 16
+@pytest.mark.parametrize("n,k,sdt", [(17408, 5120, 1), (5120, 5120, 0), (14336, 4096, 1), (16640, 2560, 0),
+                                     (17408, 4096, 0)])
+def test_gemv_m1_quarter_tiles(dev, n, k, sdt):
+    """every row (quarter rows included) within 1e-4 * rms of the exact product, the bf16 output its RN, GLU outputs
+    silu(gate) up of the same sums, repeated calls bit-identical"""
+    w, q, s = setup_w4(n, k, sdt, seed=n + 3 * k + sdt)
+    xh = synth.x_host(1, k, seed=k + 5)
+    x = synth.to_dev(xh)
+    y = ops.gemv_w4(w, x)
+    y2 = ops.gemv_w4(w, x)
+    yb = ops.gemv_w4(w, x, out_bf16=True)
+    torch.cuda.synchronize()
+    ex = matmul_f64(xh, exact_w4(q, s, n, k, sdt))
+    r = err_ratio(y.cpu().numpy(), ex)
+    tail = err_ratio(y.cpu().numpy()[:, n - 1024:], ex[:, n - 1024:])
+    print(f"m1 quarter n={n} k={k}: max|y - exact| / rms = {r:.2e} (last 1024 rows {tail:.2e})", flush=True)
+    assert r <= 1e-4 and tail <= 1e-4
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    assert_rn_of(yb, y.cpu().numpy(), f"quarter n={n}")
+    del w, ex
+    wg, qg, sg = setup_w4(n, k, sdt, seed=n + 3 * k + sdt + 1, glu=True)
+    a = ops.gemv_w4(wg, x)
+    torch.cuda.synchronize()
+    assert_glu_close(out_f32(a), glu_act(matmul_f64(xh, exact_w4(qg, sg, n, k, sdt))), 1e-4)
+
+
 @pytest.mark.parametrize("per_channel", [True, False])
 @pytest.mark.parametrize("n,k", [(64, 256), (8192, 2048), (4096, 5120)])
 def test_gemv_w8_parity(dev, per_channel, n, k):
