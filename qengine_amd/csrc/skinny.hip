@@ -443,8 +443,9 @@ void launch(const uint4* q, const uint16_t* s, int n, int k, const uint16_t* x, 
     // two tiles per wave (where n / 16 is even) at m >= 5, and for m <= 4 on grids of fewer than 16 waves per CU at
     // one tile per wave. Measured (K = 5120): RT = 2 is 3 % slower at m = 2, 4 on N = 17408 (8704 waves), 3 % faster
     // at m = 8, 13 % faster at m = 16 (two blocks per CU since the partial sums reuse the staging LDS), and 6 to 16 %
-    // faster on N = 5120 (2560 waves)
-    const bool rt2 = n % 32 == 0 && (mt >= 8 || (long)(n / 16) * sc.S < 16L * qe_num_cus());
+    // faster on N = 5120 (2560 waves). Not where the tiles fit one round of CUs: N = 4096 (256 tiles), m = 2 / 16:
+    // 4.27 / 6.29 us at RT = 1 (one block per CU) against 5.24 / 7.58 us at RT = 2 (half the CUs idle)
+    const bool rt2 = n % 32 == 0 && n / 16 > qe_num_cus() && (mt >= 8 || (long)(n / 16) * sc.S < 16L * qe_num_cus());
 #define QE_SK_K(MT_, NG_)                                                                                           \
     do {                                                                                                            \
         constexpr int RT_ = skinny_rt<MT_, NG_, FMT>();                                                             \
