@@ -533,6 +533,157 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
     return true;
 }
 
+// ---- W8 per-channel records, m = 1, on the matrix cores. A W8 record (lane (g, t) of a 32-k slab) holds in dword d
+// the bytes (g, k) (g, k + 1) (g + 8, k) (g + 8, k + 1), k = 8 d + 2 t: one row's 8 values of the record are exactly one
+// v_mfma_f32_16x16x32_bf16 A operand (u = w + 128 as floats, whose high halves are the exact bf16 pair), and the
+// activations they meet are dwords 16 s + t + {0, 4, 8, 12} of the slab pair, the class-major B operand of
+// gemv1s_kernel with 32-k slabs in place of 64-k chunks. A wave-load is 64 lanes x 16 B = two slabs (lane L = 16 q + c:
+// W8 lane L % 32 of slab L / 32), B is block diagonal as there, and with one scale per row no per-group scaling is
+// needed: three MFMA chains (rows g, rows g + 8, and -128 x the class sums) run over the whole slice, and the row
+// scale multiplies the slice sums once. Per 1 KB wave-load 28 VALU for the conversion (xor, 4 byte conversions and
+// 2 permutes per dword) and 3 MFMAs.
+namespace qe_gemv1 {
+template <int NWL>
+constexpr int w8_xbytes() { return (NWL * 128 + 1023) / 1024 * 1024; }  // the slice's activations (64 k per wave-load)
+
+template <int NWL, int D, int SDT>
+__global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
+gemv1s_w8c_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int K, const uint16_t* __restrict__ x,
+                  void* __restrict__ y, int out) {
+    static_assert(NWL > D && D >= 1 && D <= 4 && w8_xbytes<NWL>() <= 8192, "gemv1s_w8c slice");
+    constexpr int XB = w8_xbytes<NWL>(), WB = XB + 256;
+    extern __shared__ __attribute__((aligned(16))) char lds8[];
+    const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const int tile = blockIdx.x, kb = w * NWL;  // kb: the slice's first 64-k unit
+    char* wl = lds8 + (size_t)w * WB;
+    const unsigned wl32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)wl);
+    float* red = reinterpret_cast<float*>(lds8 + (size_t)S * WB);  // [S][16]
+
+    // 1. the slice's activations by DMA (lanes past the slice re-read its last 16 bytes into the padding), the first
+    //    D wave-loads of records, the zero block for the lanes off the diagonal
+    const char* xs0 = reinterpret_cast<const char*>(x) + (size_t)kb * 128;
+#pragma unroll
+    for (int r = 0; r < XB / 1024; r++) {
+        const int p = 64 * r + L < NWL * 8 ? 64 * r + L : NWL * 8 - 1;
+        qe_tile::dma16(xs0 + 16 * p, wl32 + 1024 * r);
+    }
+    const uint4* qp = q + ((size_t)tile * (K >> 5) + 2 * kb) * 32 + L;
+    u32x4_v wv[D];
+#pragma unroll
+    for (int i = 0; i < D; i++) wv[i] = ld_stream(qp + (size_t)i * 64);
+    reinterpret_cast<uint32_t*>(wl + XB)[L] = 0u;
+    vm_wait<D>();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // 2. per wave-load: B (diagonal lanes: class (slab qb / 2, t = c % 4); others: zeros), the rows' A operands, the
+    //    three MFMA chains
+    const int qb = L >> 4, c = L & 15;
+    const bool diag = (c >> 2) == qb;
+    const uint32_t* bb = diag ? reinterpret_cast<const uint32_t*>(wl) + 16 * (qb >> 1) + (c & 3)
+                              : reinterpret_cast<const uint32_t*>(wl + XB);
+    const int bstep = diag ? 32 : 0;
+    constexpr uint32_t kBias = 0xC300C300u;  // bf16 (-128, -128)
+    const bf16x8_v a_bias = __builtin_bit_cast(bf16x8_v, u32x4_v{kBias, kBias, kBias, kBias});
+    auto pair = [](uint32_t u, int b0) {  // bf16 pair of bytes b0, b0 + 1 of u (exact: u <= 255)
+        const float f0 = static_cast<float>((u >> (8 * b0)) & 0xFFu), f1 = static_cast<float>((u >> (8 * b0 + 8)) & 0xFFu);
+        return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, f1), __builtin_bit_cast(uint32_t, f0), 0x07060302u);
+    };
+    f32x4_v dl = {0.f, 0.f, 0.f, 0.f}, dh = {0.f, 0.f, 0.f, 0.f}, cb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < NWL; i++) {
+        const uint32_t* b = bb + i * bstep;
+        const u32x4_v bv = {b[0], b[4], b[8], b[12]};
+        const bf16x8_v B = __builtin_bit_cast(bf16x8_v, bv);
+        const u32x4_v r = wv[i % D];
+        u32x4_v alo, ahi;
+#pragma unroll
+        for (int d = 0; d < 4; d++) {
+            const uint32_t u = r[d] ^ 0x80808080u;
+            alo[d] = pair(u, 0);
+            ahi[d] = pair(u, 2);
+        }
+        if (i + D < NWL) wv[i % D] = ld_stream(qp + (size_t)(i + D) * 64);
+        cb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, B, cb, 0, 0, 0);
+        dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, alo), B, dl, 0, 0, 0);
+        dh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_v, ahi), B, dh, 0, 0, 0);
+    }
+
+    // 3. the lane's register (c % 4) with the bias, the quad and slab halves by DPP, the slices through LDS in order,
+    //    then the row scale
+    constexpr int kDppRowRor8 = 0x128;
+    const bool b1 = (c & 1) != 0, b2 = (c & 2) != 0;
+    float vlo = pick4(dl, b1, b2) + pick4(cb, b1, b2), vhi = pick4(dh, b1, b2) + pick4(cb, b1, b2);
+    vlo = dpp_add<kDppXor1>(vlo);
+    vhi = dpp_add<kDppXor1>(vhi);
+    vlo = dpp_add<kDppXor2>(vlo);
+    vhi = dpp_add<kDppXor2>(vhi);
+    vlo = dpp_add<kDppRowRor8>(vlo);
+    vhi = dpp_add<kDppRowRor8>(vhi);
+    const int grow = 4 * ((c >> 2) & 1) + qb;
+    if ((c & 11) == 0) {
+        red[w * 16 + grow] = vlo;
+        red[w * 16 + grow + 8] = vhi;
+    }
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const int rw = threadIdx.x, row = 16 * tile + rw;
+        float v = 0.f;
+        for (int ws = 0; ws < S; ws++) v += red[ws * 16 + rw];
+        v *= scale_to_f32<SDT>(s[row]);
+        if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[row] = f32_to_bf16(v);
+        else reinterpret_cast<float*>(y)[row] = v;
+    }
+}
+
+// K slices: the most waves per tile (S in {8, 4, 2}) with 4..40 wave-loads each and >= 16 waves per CU; 0: none.
+// Measured (one process, window 3): S = 8 / 4 / 2 at N = 8192, K = 2048 (C3) 4.85 / 5.16 / 6.38 us; N = 17408,
+// K = 5120 16.00 / 16.38 / 16.34 us; N = 16384, K = 4096 12.50 / 13.06 / 12.62 us (the VALU GEMV before: 5.2-5.3 us
+// at C3, window 2 or 4 no better). One tile per CU (N = 4096, K = 5120, 8 waves per CU): 5.67 us against 5.53 for
+// the skinny kernel, so those grids keep it
+int w8c_slices(int n, int k) {
+    const int tiles = n / 16, KU = k / 64;
+    for (int S : {8, 4, 2}) {
+        if (KU % S) continue;
+        const int nwl = KU / S;
+        if (nwl != 4 && nwl != 8 && nwl != 10 && nwl != 16 && nwl != 20 && nwl != 32 && nwl != 40) continue;
+        if ((long)tiles * S >= 16L * qe_num_cus()) return S;
+    }
+    return 0;
+}
+}  // namespace qe_gemv1
+
+// m = 1 on W8 per-channel records (x 16-byte aligned, out fp32 or bf16); false when no slicing fits (the caller takes
+// its other kernels)
+bool gemv1_w8c(const W8& w, const uint16_t* x, void* y, int out, hipStream_t st) {
+    using namespace qe_gemv1;
+    if (!w.per_channel || w.q8 || out == kOutGLU || ((uintptr_t)x & 15) != 0) return false;
+    const int S = w8c_slices(w.n, w.k);
+    if (S == 0) return false;
+    const int nwl = w.k / 64 / S;
+    const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
+#define QE_W8C(NWL_, SDT_)                                                                                       \
+    gemv1s_w8c_kernel<NWL_, 3, SDT_><<<grid, block, (size_t)S * (w8_xbytes<NWL_>() + 256) + (size_t)S * 64, st>>>( \
+        w.q, w.s, w.k, x, y, out)
+#define QE_W8C_N(SDT_)                          \
+    do {                                        \
+        if (nwl == 4) QE_W8C(4, SDT_);          \
+        else if (nwl == 8) QE_W8C(8, SDT_);     \
+        else if (nwl == 10) QE_W8C(10, SDT_);   \
+        else if (nwl == 16) QE_W8C(16, SDT_);   \
+        else if (nwl == 20) QE_W8C(20, SDT_);   \
+        else if (nwl == 32) QE_W8C(32, SDT_);   \
+        else QE_W8C(40, SDT_);                  \
+    } while (0)
+    if (w.sdt == kScaleF16) QE_W8C_N(kScaleF16);
+    else QE_W8C_N(kScaleBF16);
+#undef QE_W8C_N
+#undef QE_W8C
+    HIP_CHECK(hipGetLastError());
+    return true;
+}
+
 // ---- the m = 1 GEMV's HBM read floor: the same blocks, waves and record loads, no arithmetic
 namespace qe_gemv1 {
 template <int NG>

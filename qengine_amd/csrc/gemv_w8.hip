@@ -20,6 +20,9 @@ void gemv_w8(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     CHECK(ldy >= (w.glu ? w.n / 2 : w.n), "gemv_w8 ldy %d", ldy);
     CHECK(!w.glu || w.q8, "gemv_w8: GLU is for Q8 matrices");
     const int out = w.glu ? kOutGLU : out_bf16 ? kOutBF16 : kOutF32;
+    // m = 1 on per-channel records: the streaming matrix-core kernel (gemv1.hip) where it takes the shape (not under
+    // batch_invariant, where m = 1 runs the batched rows' kernel)
+    if (m == 1 && !qe_config().batch_invariant && gemv1_w8c(w, x, y, out, st)) return;
     // the matrix-core kernel from w8_mfma_min_m rows (rows that are not 16-byte aligned take its 4-dword loads)
     if (m >= w8_mfma_min_m(w.n, w.k)) {
         skinny_w8_mfma(w, x, ldx, y, ldy, m, out, st);

@@ -353,17 +353,20 @@ __device__ void seg_one_wave(const int32_t* ssel, const float* sw, int T, int E,
     }
 }
 
-// T <= kDecRouteFused: route and segment in one block of T waves (routing into LDS, one barrier, wave 0 segments;
-// the routing is also stored to sel / w, which the fused decode down + combine kernel reads)
-constexpr int kDecRouteFused = 4;
+// T <= kDecRouteSeg: route and segment in one block of T waves (routing into LDS, one barrier, wave 0 segments;
+// the routing is also stored to sel / w, which the fused decode down + combine kernel reads). Measured against
+// routing over CUs then a one-wave segmentation (C4 layer, graph replay, same box): T = 5 / 8 32.1 / 41.4 -> 31.6 /
+// 40.7 us, T = 12 the same, T = 16 62.3 -> 63.1 us (16 routing waves on one CU), so up to 8 tokens
+constexpr int kDecRouteFused = 4;  // routing inside the gate_up blocks (below)
+constexpr int kDecRouteSeg = 8;
 template <int PER>
-__global__ void __launch_bounds__(64 * kDecRouteFused) moe_route_segment_kernel(
+__global__ void __launch_bounds__(64 * kDecRouteSeg) moe_route_segment_kernel(
     const float* __restrict__ logits, int T, int E, int topk, int chunk, int32_t* __restrict__ sel,
     float* __restrict__ w, int32_t* __restrict__ off,
     int32_t* __restrict__ slot_pair, int32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
     int32_t* __restrict__ inv, int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
-    __shared__ int32_t ssel[kDecRouteFused * 16];
-    __shared__ float sw[kDecRouteFused * 16];
+    __shared__ int32_t ssel[kDecRouteSeg * 16];
+    __shared__ float sw[kDecRouteSeg * 16];
     __shared__ int cnt[64 * PER], pre[64 * PER];
     __shared__ unsigned mark[64 * PER];
     const int tid = threadIdx.x, wv = tid >> 6;
@@ -381,7 +384,7 @@ __global__ void __launch_bounds__(64 * kDecRouteFused) moe_route_segment_kernel(
     seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs);
 }
 
-// kDecRouteFused < T <= kDecTokens: routed by moe_route_kernel (tokens over CUs: one CU routing 16+ tokens is
+// kDecRouteSeg < T <= kDecTokens: routed by moe_route_kernel (tokens over CUs: one CU routing 16+ tokens is
 // issue-bound), then this one-wave kernel segments sel / w
 template <int PER>
 __global__ void __launch_bounds__(64) moe_dec_segment_kernel(const int32_t* __restrict__ sel,
@@ -414,10 +417,10 @@ void launch_route_segment(const float* logits, int T, int E, int topk, int chunk
                           int32_t* slot_pair, int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs,
                           int32_t* njobs, hipStream_t st) {
     const int per = (E + 63) / 64;
-    if (T > kDecRouteFused) launch_route(logits, T, E, topk, sel, w, st);
+    if (T > kDecRouteSeg) launch_route(logits, T, E, topk, sel, w, st);
 #define QE_RS(PER_)                                                                                                 \
     do {                                                                                                            \
-        if (T <= kDecRouteFused)                                                                                    \
+        if (T <= kDecRouteSeg)                                                                                      \
             moe_route_segment_kernel<PER_><<<1, 64 * T, 0, st>>>(logits, T, E, topk, chunk, sel, w, off, slot_pair,   \
                                                                  slot_tok, slot_w, inv, jobs, njobs);               \
         else                                                                                                        \

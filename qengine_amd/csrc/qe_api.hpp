@@ -64,6 +64,9 @@ void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, i
 // m = 1 decode GEMV on the matrix cores (gemv1.hip); false when the shape takes the VALU GEMV (uneven K slices,
 // x not 16-byte aligned). out as for skinny_w4_mfma
 bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st);
+// m = 1 on W8 per-channel records on the matrix cores (gemv1.hip); false when it does not take the shape (Q8 or group
+// scales, GLU, x not 16-byte aligned, no K slicing)
+bool gemv1_w8c(const W8& w, const uint16_t* x, void* y, int out, hipStream_t st);
 // H16 decode numerics (the reference's gemv_w4h, gemv_h16.cuh): XH activations (xh_pack), m = 1..16 per launch,
 // W4 or Q8 (q8) records; out as for skinny_w4_mfma; yh: optional XH copy of the outputs [m][ldyh]
 void xh_pack(const uint16_t* x, int ldx, int k, int m, uint16_t* xh, int ldxh, hipStream_t st);

@@ -371,10 +371,43 @@ def test_gemv_w8_parity(dev, per_channel, n, k):
         # so a bf16 output's own rounding, up to 2^-9 |y|, alone can exceed 2e-2 rms); the bf16 output is its RN
         assert_gate(y32.cpu().numpy(), ref_ex[:m], f"W8 m={m} n={n} k={k} pc={per_channel} fp32 out")
         assert_rn_of(y, y32.cpu().numpy(), "W8 GEMV")
-        if m == 1:  # the VALU GEMV at short slices (m >= 2: the matrix-core kernel, the same rows for every m)
+        if m == 1:  # m = 1 kernels (per-channel: the streaming W8 kernel; m >= 2: the skinny kernel, same rows for every m)
             assert err_ratio(y32.cpu().numpy(), full.cpu().numpy()[:1]) <= 1e-5
         else:
             assert np.array_equal(y32.cpu().numpy().view(np.uint32), full.cpu().numpy().view(np.uint32)[:m]), m
+
+
+# the streaming m = 1 kernel on per-channel W8 records (8 K slices of 4, 10 and 8 wave-loads of 64 k: C3, N = 12288 and
+# 16384), and grids it does not take (fewer than 16 waves per CU: the VALU GEMV at K = 2048, the skinny kernel at 5120)
+@pytest.mark.parametrize("n,k,sdt", [(8192, 2048, 1), (12288, 5120, 0), (16384, 4096, 0), (2048, 2048, 1),
+                                     (4096, 5120, 1)])
+def test_gemv_w8c_m1(dev, n, k, sdt):
+    """fp32 output within 1e-4 * rms of the exact product and inside the BASELINE gate, the bf16 output its RN,
+    repeated calls bit-identical, within 1e-5 * rms of the batched rows' kernel (batch_invariant: m = 1 on it)"""
+    q, s16 = synth.w8_host(n, k, seed=n + k + sdt, per_channel=True)
+    s = s16 if sdt else synth.np_bf16(oracle.f16_to_f32(s16))  # fp16 or bf16 scales
+    sf = oracle.f16_to_f32(s) if sdt else oracle.bf16_to_f32(s)
+    w = ops.tile_w8(synth.to_dev(q), synth.to_dev(s, torch.float16 if sdt else torch.bfloat16), True)
+    xh = synth.x_host(1, k, seed=k + 3)
+    x = synth.to_dev(xh)
+    ex = matmul_f64(xh, q.astype(np.float32) * sf.reshape(n, 1))
+    y = ops.gemv_w8(w, x)
+    y2 = ops.gemv_w8(w, x)
+    yb = ops.gemv_w8(w, x, out_bf16=True)
+    torch.cuda.synchronize()
+    r = err_ratio(y.cpu().numpy(), ex)
+    print(f"w8c m1 n={n} k={k}: max|y - exact| / rms = {r:.2e}", flush=True)
+    assert r <= 1e-4
+    assert_gate(y.cpu().numpy(), ex, f"W8C m=1 n={n} k={k}")
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    assert_rn_of(yb, y.cpu().numpy(), "W8C m=1")
+    ops.set_config(batch_invariant=1)
+    try:
+        yi = ops.gemv_w8(w, x)
+        torch.cuda.synchronize()
+    finally:
+        ops.set_config(batch_invariant=0)
+    assert err_ratio(y.cpu().numpy(), yi.cpu().numpy()) <= 1e-5
 
 
 def test_gemv_w8_reference_hook(dev):
