@@ -550,7 +550,7 @@ template <int NWL, int D, int SDT>
 __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
 gemv1s_w8c_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int K, const uint16_t* __restrict__ x,
                   void* __restrict__ y, int out) {
-    static_assert(NWL > D && D >= 1 && D <= 4 && w8_xbytes<NWL>() <= 8192, "gemv1s_w8c slice");
+    static_assert(NWL >= D && D >= 1 && D <= 4 && w8_xbytes<NWL>() <= 8192, "gemv1s_w8c slice");
     constexpr int XB = w8_xbytes<NWL>(), WB = XB + 256;
     extern __shared__ __attribute__((aligned(16))) char lds8[];
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
@@ -559,8 +559,10 @@ gemv1s_w8c_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, i
     const unsigned wl32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)wl);
     float* red = reinterpret_cast<float*>(lds8 + (size_t)S * WB);  // [S][16]
 
-    // 1. the slice's activations by DMA (lanes past the slice re-read its last 16 bytes into the padding), the first
-    //    D wave-loads of records, the zero block for the lanes off the diagonal
+    // 1. the row scale of lane L % 16 (used after the reduction: loaded first, so the block's end does not wait a
+    //    memory latency for it), the slice's activations by DMA (lanes past the slice re-read its last 16 bytes into
+    //    the padding), the first D wave-loads of records, the zero block for the lanes off the diagonal
+    const uint16_t sraw = s[16 * tile + (L & 15)];
     const char* xs0 = reinterpret_cast<const char*>(x) + (size_t)kb * 128;
 #pragma unroll
     for (int r = 0; r < XB / 1024; r++) {
@@ -631,7 +633,7 @@ gemv1s_w8c_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, i
         const int rw = threadIdx.x, row = 16 * tile + rw;
         float v = 0.f;
         for (int ws = 0; ws < S; ws++) v += red[ws * 16 + rw];
-        v *= scale_to_f32<SDT>(s[row]);
+        v *= scale_to_f32<SDT>(sraw);
         if (out == kOutBF16) reinterpret_cast<uint16_t*>(y)[row] = f32_to_bf16(v);
         else reinterpret_cast<float*>(y)[row] = v;
     }
@@ -663,8 +665,9 @@ bool gemv1_w8c(const W8& w, const uint16_t* x, void* y, int out, hipStream_t st)
     if (S == 0) return false;
     const int nwl = w.k / 64 / S;
     const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
+    // all records in flight at 4 wave-loads per wave (C3: 4.80 -> 4.65 us), else a window of 3 (K = 5120: equal)
 #define QE_W8C(NWL_, SDT_)                                                                                       \
-    gemv1s_w8c_kernel<NWL_, 3, SDT_><<<grid, block, (size_t)S * (w8_xbytes<NWL_>() + 256) + (size_t)S * 64, st>>>( \
+    gemv1s_w8c_kernel<NWL_, (NWL_ == 4 ? 4 : 3), SDT_><<<grid, block, (size_t)S * (w8_xbytes<NWL_>() + 256) + (size_t)S * 64, st>>>( \
         w.q, w.s, w.k, x, y, out)
 #define QE_W8C_N(SDT_)                          \
     do {                                        \
