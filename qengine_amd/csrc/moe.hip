@@ -290,11 +290,15 @@ __global__ void __launch_bounds__(kSegThreads) moe_segment_kernel(const int32_t*
 // pair's slot = the expert's offset + the number of earlier tokens on that expert. Same off / slots / jobs as
 // moe_segment_kernel. cnt / pre / mark: LDS [64 PER], cnt and mark zeroed by the caller.
 constexpr int kDecTokens = 32;
+// decode job records (jdec [job][kJobInts]): expert, first slot, rows m, 0, the token of each row (4 slots), its
+// routing weight (float bits; 4 slots), 4 unused: one 64-byte line that the decode kernels load first, in place of the
+// dependent loads of jobs, off, slot_tok and slot_w (slots past m are not written: the kernels use row 0 there)
+constexpr int kJobInts = 16, kJobRows = 4;
 template <int PER>
 __device__ void seg_one_wave(const int32_t* ssel, const float* sw, int T, int E, int topk, int chunk, int* cnt,
                              int* pre, unsigned* mark, int32_t* __restrict__ off, int32_t* __restrict__ slot_pair,
                              int32_t* __restrict__ slot_tok, float* __restrict__ slot_w, int32_t* __restrict__ inv,
-                             int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
+                             int32_t* __restrict__ jobs, int32_t* __restrict__ njobs, int32_t* __restrict__ jdec) {
     const int lane = threadIdx.x & 63;
     const int P = T * topk;
     for (int p = lane; p < P; p += 64) {
@@ -331,7 +335,13 @@ __device__ void seg_one_wave(const int32_t* ssel, const float* sw, int T, int E,
             for (int q = 0; q < nj; q++) {
                 jobs[2 * (jrun + q)] = e;
                 jobs[2 * (jrun + q) + 1] = q * chunk;
+                int32_t* jd = jdec + (size_t)kJobInts * (jrun + q);  // tokens and weights: the pair loop below
+                jd[0] = e;
+                jd[1] = run + q * chunk;
+                jd[2] = min(chunk, c[j] - q * chunk);
+                jd[3] = 0;
             }
+            cnt[e] = jrun;  // the expert's first job (its count is no longer read)
             run += c[j];
             jrun += nj;
         }
@@ -345,11 +355,14 @@ __device__ void seg_one_wave(const int32_t* ssel, const float* sw, int T, int E,
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     for (int p = lane; p < P; p += 64) {
         const int e = ssel[p], t = p / topk;
-        const int slot = pre[e] + __popc(mark[e] & ((1u << t) - 1u));
+        const int i = __popc(mark[e] & ((1u << t) - 1u)), slot = pre[e] + i;
         slot_pair[slot] = p;
         slot_tok[slot] = t;
         slot_w[slot] = sw[p];
         inv[p] = slot;
+        int32_t* jd = jdec + (size_t)kJobInts * (cnt[e] + i / chunk);
+        jd[4 + i % chunk] = t;
+        jd[8 + i % chunk] = __builtin_bit_cast(int32_t, sw[p]);
     }
 }
 
@@ -364,7 +377,7 @@ __global__ void __launch_bounds__(64 * kDecRouteSeg) moe_route_segment_kernel(
     const float* __restrict__ logits, int T, int E, int topk, int chunk, int32_t* __restrict__ sel,
     float* __restrict__ w, int32_t* __restrict__ off,
     int32_t* __restrict__ slot_pair, int32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
-    int32_t* __restrict__ inv, int32_t* __restrict__ jobs, int32_t* __restrict__ njobs) {
+    int32_t* __restrict__ inv, int32_t* __restrict__ jobs, int32_t* __restrict__ njobs, int32_t* __restrict__ jdec) {
     __shared__ int32_t ssel[kDecRouteSeg * 16];
     __shared__ float sw[kDecRouteSeg * 16];
     __shared__ int cnt[64 * PER], pre[64 * PER];
@@ -381,7 +394,8 @@ __global__ void __launch_bounds__(64 * kDecRouteSeg) moe_route_segment_kernel(
         w[p] = sw[p];
     }
     if (wv != 0) return;
-    seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs);
+    seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs,
+                      jdec);
 }
 
 // kDecRouteSeg < T <= kDecTokens: routed by moe_route_kernel (tokens over CUs: one CU routing 16+ tokens is
@@ -393,7 +407,8 @@ __global__ void __launch_bounds__(64) moe_dec_segment_kernel(const int32_t* __re
                                                              int32_t* __restrict__ slot_pair,
                                                              int32_t* __restrict__ slot_tok, float* __restrict__ slot_w,
                                                              int32_t* __restrict__ inv, int32_t* __restrict__ jobs,
-                                                             int32_t* __restrict__ njobs) {
+                                                             int32_t* __restrict__ njobs,
+                                                             int32_t* __restrict__ jdec) {
     __shared__ int32_t ssel[kDecTokens * 16];
     __shared__ float sw[kDecTokens * 16];
     __shared__ int cnt[64 * PER], pre[64 * PER];
@@ -410,22 +425,23 @@ __global__ void __launch_bounds__(64) moe_dec_segment_kernel(const int32_t* __re
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs);
+    seg_one_wave<PER>(ssel, sw, T, E, topk, chunk, cnt, pre, mark, off, slot_pair, slot_tok, slot_w, inv, jobs, njobs,
+                      jdec);
 }
 
 void launch_route_segment(const float* logits, int T, int E, int topk, int chunk, int32_t* sel, float* w, int32_t* off,
                           int32_t* slot_pair, int32_t* slot_tok, float* slot_w, int32_t* inv, int32_t* jobs,
-                          int32_t* njobs, hipStream_t st) {
+                          int32_t* njobs, int32_t* jdec, hipStream_t st) {
     const int per = (E + 63) / 64;
     if (T > kDecRouteSeg) launch_route(logits, T, E, topk, sel, w, st);
 #define QE_RS(PER_)                                                                                                 \
     do {                                                                                                            \
         if (T <= kDecRouteSeg)                                                                                      \
             moe_route_segment_kernel<PER_><<<1, 64 * T, 0, st>>>(logits, T, E, topk, chunk, sel, w, off, slot_pair,   \
-                                                                 slot_tok, slot_w, inv, jobs, njobs);               \
+                                                                 slot_tok, slot_w, inv, jobs, njobs, jdec);         \
         else                                                                                                        \
             moe_dec_segment_kernel<PER_><<<1, 64, 0, st>>>(sel, w, T, E, topk, chunk, off, slot_pair, slot_tok,      \
-                                                           slot_w, inv, jobs, njobs);                               \
+                                                           slot_w, inv, jobs, njobs, jdec);                         \
     } while (0)
     if (per <= 1) QE_RS(1);
     else if (per <= 2) QE_RS(2);
@@ -604,14 +620,17 @@ __device__ __forceinline__ float* mfma_dec_tile(uint32_t* lds, const uint4* __re
 // gate_up: block (job, record g * 16 + 16-row tile); S = G / NG waves over K = H
 template <int MT, int NG>
 __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
-    const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ x, const int32_t* __restrict__ off,
-    const int32_t* __restrict__ slot_tok, const float* __restrict__ slot_w, const int32_t* __restrict__ jobs,
+    const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ x, const int32_t* __restrict__ jdec,
     const int32_t* __restrict__ njobs, uint16_t* __restrict__ act) {
+    static_assert(MT <= kJobRows, "moe decode job rows");
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const int job = blockIdx.x;
     if (job >= *njobs) return;
-    const int e = jobs[2 * job], r0 = jobs[2 * job + 1];
-    const int slot0 = off[e] + r0, m = min(MT, off[e + 1] - slot0);
+    const int4* jr = reinterpret_cast<const int4*>(jdec + (size_t)kJobInts * job);
+    const int4 j0 = jr[0], jt = jr[1], jw = jr[2];  // (e, slot0, m, -), tokens, weights
+    const int e = j0.x, slot0 = j0.y, m = j0.z;
+    const int tok[4] = {jt.x, jt.y, jt.z, jt.w};
+    const int wbits[4] = {jw.x, jw.y, jw.z, jw.w};
     const int g = blockIdx.y >> 4, tile = blockIdx.y & 15;
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6;
     const int G = sh.H >> 7, gb = w * NG;
@@ -621,11 +640,12 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
     const uint32_t* xw[MT];
 #pragma unroll
     for (int r = 0; r < MT; r++)
-        xw[r] = reinterpret_cast<const uint32_t*>(x + (size_t)slot_tok[slot0 + (r < m ? r : 0)] * sh.H) + gb * 64;
+        xw[r] = reinterpret_cast<const uint32_t*>(x + (size_t)tok[r < m ? r : 0] * sh.H) + gb * 64;
     const float* red = mfma_dec_tile<MT, NG>(lds, qp, sp, xw, m, 64, 8);
     for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
         const int r = idx >> 3, gg = idx & 7;
-        const float v = silu_f32(rsum<MT>(red, S, r, gg)) * rsum<MT>(red, S, r, gg + 8) * slot_w[slot0 + r];
+        const float v = silu_f32(rsum<MT>(red, S, r, gg)) * rsum<MT>(red, S, r, gg + 8) *
+                        __builtin_bit_cast(float, wbits[r & 3]);
         act[(size_t)(slot0 + r) * sh.I + g * 128 + tile * 8 + gg] = f32_to_f16(v * kMoeF16Scale);
     }
 }
@@ -673,13 +693,13 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_route_gate_up_kernel(
 // wave streams NGRP KB and no K slice is reduced across waves
 template <int MT, int NGRP>
 __global__ void __launch_bounds__(64) moe_dec_down_kernel(
-    const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ act, const int32_t* __restrict__ off,
-    const int32_t* __restrict__ jobs, const int32_t* __restrict__ njobs, uint16_t* __restrict__ slot_out) {
+    const char* __restrict__ recs, MoeShape sh, const uint16_t* __restrict__ act, const int32_t* __restrict__ jdec,
+    const int32_t* __restrict__ njobs, uint16_t* __restrict__ slot_out) {
     extern __shared__ __attribute__((aligned(16))) uint32_t lds[];
     const int job = blockIdx.x;
     if (job >= *njobs) return;
-    const int e = jobs[2 * job], r0 = jobs[2 * job + 1];
-    const int slot0 = off[e] + r0, m = min(MT, off[e + 1] - slot0);
+    const int4 j0 = *reinterpret_cast<const int4*>(jdec + (size_t)kJobInts * job);  // (e, slot0, m, -)
+    const int e = j0.x, slot0 = j0.y, m = j0.z;
     const int tile = blockIdx.y;
     const char* rp = rec_ptr(recs, sh, e, 0);
     const uint4* qp = reinterpret_cast<const uint4*>(rp + sh.gg_q + sh.gg_s) + (size_t)tile * 2 * 32;
@@ -867,7 +887,7 @@ __global__ void __launch_bounds__(256) moe_pack_kernel(const int32_t* __restrict
 
 // ------------------------------------------------------------------ workspace layout
 struct MoeWs {
-    int32_t *sel, *off, *slot_pair, *slot_tok, *inv, *jobs, *njobs, *cntb;
+    int32_t *sel, *off, *slot_pair, *slot_tok, *inv, *jobs, *njobs, *cntb, *jdec;
     float *w, *slot_w;
     uint16_t *act, *slot_out;
     size_t bytes;
@@ -897,6 +917,7 @@ MoeWs moe_ws(void* base, int T, int E, int topk, int H, int I) {
     ws.inv = reinterpret_cast<int32_t*>(take(P * 4));
     ws.jobs = reinterpret_cast<int32_t*>(take((size_t)mj * 8));
     ws.njobs = reinterpret_cast<int32_t*>(take(4));
+    ws.jdec = reinterpret_cast<int32_t*>(take(T <= kDecTokens ? (size_t)mj * kJobInts * 4 : 0));
     ws.cntb = reinterpret_cast<int32_t*>(take((size_t)((T + kSegChunk - 1) / kSegChunk) * E * 4));
     ws.act = reinterpret_cast<uint16_t*>(take(P * I * 2));
     ws.slot_out = reinterpret_cast<uint16_t*>(take(P * H * 2));
@@ -1005,7 +1026,7 @@ void moe_run(const float* logits, const uint16_t* x, const void* records, int T,
     if (T > kDecTokens) launch_route(logits, T, E, topk, ws.sel, ws.w, st);
     if (T <= kDecTokens) {
         launch_route_segment(logits, T, E, topk, chunk, ws.sel, ws.w, ws.off, ws.slot_pair, ws.slot_tok, ws.slot_w,
-                             ws.inv, ws.jobs, ws.njobs, st);
+                             ws.inv, ws.jobs, ws.njobs, ws.jdec, st);
     } else if (T > kSegOneBlockTokens) {
         const int nchunk = (T + kSegChunk - 1) / kSegChunk;
         moe_seg_count_kernel<<<nchunk, kSegThreads, 0, st>>>(ws.sel, T, E, topk, ws.cntb);
@@ -1031,13 +1052,13 @@ void moe_run(const float* logits, const uint16_t* x, const void* records, int T,
                                         : gemv_lds_bytes<kDecRows, 8, true>(G / 8);
         if (ng == 2)
             moe_dec_gate_up_kernel<kDecRows, 2><<<dim3(mj, sh.ngrp * 16), 64 * (G / 2), lds_gu, st>>>(
-                recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
+                recs, sh, x, ws.jdec, ws.njobs, ws.act);
         else if (ng == 4)
             moe_dec_gate_up_kernel<kDecRows, 4><<<dim3(mj, sh.ngrp * 16), 64 * (G / 4), lds_gu, st>>>(
-                recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
+                recs, sh, x, ws.jdec, ws.njobs, ws.act);
         else
             moe_dec_gate_up_kernel<kDecRows, 8><<<dim3(mj, sh.ngrp * 16), 64 * (G / 8), lds_gu, st>>>(
-                recs, sh, x, ws.off, ws.slot_tok, ws.slot_w, ws.jobs, ws.njobs, ws.act);
+                recs, sh, x, ws.jdec, ws.njobs, ws.act);
         HIP_CHECK(hipGetLastError());
         if (few && sh.ngrp <= 8) {
             launch_down_combine(recs, sh, ws.act, ws.sel, ws.inv, T, topk, H, out, flags, st);
@@ -1045,7 +1066,7 @@ void moe_run(const float* logits, const uint16_t* x, const void* records, int T,
         }
 #define QE_DOWN(NGRP_)                                                                                         \
     moe_dec_down_kernel<kDecRows, NGRP_><<<dim3(mj, H / 16), 64, gemv_lds_bytes<kDecRows, NGRP_, true>(1), st>>>( \
-        recs, sh, ws.act, ws.off, ws.jobs, ws.njobs, ws.slot_out)
+        recs, sh, ws.act, ws.jdec, ws.njobs, ws.slot_out)
         switch (sh.ngrp) {
             case 1: QE_DOWN(1); break;
             case 2: QE_DOWN(2); break;
