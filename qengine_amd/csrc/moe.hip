@@ -362,7 +362,8 @@ __device__ void seg_one_wave(const int32_t* ssel, const float* sw, int T, int E,
         inv[p] = slot;
         int32_t* jd = jdec + (size_t)kJobInts * (cnt[e] + i / chunk);
         jd[4 + i % chunk] = t;
-        jd[8 + i % chunk] = __builtin_bit_cast(int32_t, sw[p]);
+        const float wp = sw[p];
+        jd[8 + i % chunk] = __builtin_bit_cast(int32_t, wp);
     }
 }
 
@@ -644,8 +645,8 @@ __global__ void __launch_bounds__(64 * kMaxWaves) moe_dec_gate_up_kernel(
     const float* red = mfma_dec_tile<MT, NG>(lds, qp, sp, xw, m, 64, 8);
     for (int idx = threadIdx.x; idx < m * 8; idx += blockDim.x) {
         const int r = idx >> 3, gg = idx & 7;
-        const float v = silu_f32(rsum<MT>(red, S, r, gg)) * rsum<MT>(red, S, r, gg + 8) *
-                        __builtin_bit_cast(float, wbits[r & 3]);
+        const int wb = wbits[r & 3];
+        const float v = silu_f32(rsum<MT>(red, S, r, gg)) * rsum<MT>(red, S, r, gg + 8) * __builtin_bit_cast(float, wb);
         act[(size_t)(slot0 + r) * sh.I + g * 128 + tile * 8 + gg] = f32_to_f16(v * kMoeF16Scale);
     }
 }
