@@ -243,11 +243,11 @@ __device__ __forceinline__ void vm_wait() {
 template <int NG, int SDT>
 __device__ __forceinline__ void gemv1s_quarter(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int K,
                                                const uint16_t* __restrict__ x, void* __restrict__ y, int out,
-                                               int tile, int a, char* lds8) {
+                                               int tile, int a, char* lds8, int gb, int ng) {
     constexpr int XB = st_xbytes<NG>(), WB = st_wbytes<NG>();
-    constexpr int NS = 2 * NG, NL = (NS + 7) / 8;  // 64-k steps of the slice, wave-loads of 8 steps
+    constexpr int NL = (2 * NG + 7) / 8;  // wave-loads of 8 steps for the longest slice (ng <= NG groups)
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
-    const int G = K >> 7, gb = w * NG;
+    const int G = K >> 7, NS = 2 * ng;  // the wave's 64-k steps
     char* wl = lds8 + (size_t)w * WB;
     const unsigned wl32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)wl);
     float* red = reinterpret_cast<float*>(lds8 + (size_t)S * WB);  // [S][16]
@@ -255,11 +255,11 @@ __device__ __forceinline__ void gemv1s_quarter(const uint4* __restrict__ q, cons
     const char* xs0 = reinterpret_cast<const char*>(x) + (size_t)gb * 256;
 #pragma unroll
     for (int r = 0; r < XB / 1024; r++) {
-        const int p = 64 * r + L < NG * 16 ? 64 * r + L : NG * 16 - 1;
+        const int p = 64 * r + L < ng * 16 ? 64 * r + L : ng * 16 - 1;
         qe_tile::dma16(xs0 + 16 * p, wl32 + 1024 * r);
     }
     {
-        const int p = L < NG * 2 ? L : NG * 2 - 1;
+        const int p = L < ng * 2 ? L : ng * 2 - 1;
         qe_tile::dma16(reinterpret_cast<const char*>(s + ((size_t)tile * G + gb) * 16) + 16 * p, wl32 + XB);
     }
     const int st = L >> 3, gq = (L >> 2) & 1, t = L & 3, g = 2 * a + gq;
@@ -281,7 +281,7 @@ __device__ __forceinline__ void gemv1s_quarter(const uint4* __restrict__ q, cons
     float acc_lo = 0.f, acc_hi = 0.f;
 #pragma unroll
     for (int ld = 0; ld < NL; ld++) {
-        const bool valid = NS % 8 == 0 || ld < NL - 1 || 8 * ld + st < NS;
+        const bool valid = 8 * ld + st < NS;
         const int si = valid ? 8 * ld + st : NS - 1;
         const uint32_t* xb = xl + si * 32 + t;
         uint32_t xd[8];  // x pairs (k, k + 1) of word j at 2 j, (k + 8, k + 9) at 2 j + 1
@@ -339,7 +339,7 @@ __device__ __forceinline__ void gemv1s_quarter(const uint4* __restrict__ q, cons
 // QT: blocks tq.. are quarter blocks (b = blockIdx.x - tq: quarter b % 4 of tile tq + b / 4); the kernel without them
 // is a separate instance, whose code is then exactly the whole-tile kernel's (the branch alone, taken by no block,
 // cost up to 5 % on some shapes)
-template <int NG, int D, int SDT, bool QT>
+template <int NG, int D, int SDT, bool QT, bool EXACT = true>
 __global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
 gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K,
               const uint16_t* __restrict__ x, void* __restrict__ y, int out, int tq) {
@@ -347,14 +347,17 @@ gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N
     constexpr int XB = st_xbytes<NG>(), WB = st_wbytes<NG>();
     extern __shared__ __attribute__((aligned(16))) char lds8[];
     const int S = blockDim.x >> 6, w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    // EXACT: every wave a slice of NG groups; else wave w takes groups w G / S .. (w + 1) G / S - 1 (ng <= NG, > D)
+    const int G = K >> 7, gb = EXACT ? w * NG : w * G / S;
+    const int ng = EXACT ? NG : (w + 1) * G / S - gb;
     if constexpr (QT) {
         if (__builtin_expect((int)blockIdx.x >= tq, 0)) {
             const int b = blockIdx.x - tq;
-            gemv1s_quarter<NG, SDT>(q, s, K, x, y, out, tq + (b >> 2), b & 3, lds8);
+            gemv1s_quarter<NG, SDT>(q, s, K, x, y, out, tq + (b >> 2), b & 3, lds8, gb, ng);
             return;
         }
     }
-    const int tile = blockIdx.x, G = K >> 7, gb = w * NG;
+    const int tile = blockIdx.x;
     char* wl = lds8 + (size_t)w * WB;
     const unsigned wl32 = __builtin_amdgcn_readfirstlane((unsigned)(size_t)wl);
     float* red = reinterpret_cast<float*>(lds8 + (size_t)S * WB);  // [S][16]
@@ -365,11 +368,11 @@ gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N
     const char* xs0 = reinterpret_cast<const char*>(x) + (size_t)gb * 256;
 #pragma unroll
     for (int r = 0; r < XB / 1024; r++) {
-        const int p = 64 * r + L < NG * 16 ? 64 * r + L : NG * 16 - 1;
+        const int p = 64 * r + L < ng * 16 ? 64 * r + L : ng * 16 - 1;
         qe_tile::dma16(xs0 + 16 * p, wl32 + 1024 * r);
     }
     {
-        const int p = L < NG * 2 ? L : NG * 2 - 1;
+        const int p = L < ng * 2 ? L : ng * 2 - 1;
         qe_tile::dma16(reinterpret_cast<const char*>(s + ((size_t)tile * G + gb) * 16) + 16 * p, wl32 + XB);
     }
     const uint4* qp = q + ((size_t)tile * (K >> 6) + 2 * gb) * 32 + L;
@@ -396,6 +399,7 @@ gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N
     f32x4_v acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NG; i++) {
+        if (!EXACT && i >= ng) break;
         const uint32_t* b = bb + i * bstep;
         const u32x4_v b01 = {b[0], b[4], b[8], b[12]}, b23 = {b[16], b[20], b[24], b[28]};
         const bf16x8_v B01 = __builtin_bit_cast(bf16x8_v, b01), B23 = __builtin_bit_cast(bf16x8_v, b23);
@@ -413,7 +417,7 @@ gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N
             return __builtin_bit_cast(bf16x8_v, a);
         };
         const bf16x8_v A0 = opnd(t0, 0), A1 = opnd(t1, 0), A2 = opnd(t0, 2), A3 = opnd(t1, 2);
-        if (i + D < NG) wv[i % D] = ld_stream(qp + (size_t)(i + D) * 64);
+        if (i + D < ng) wv[i % D] = ld_stream(qp + (size_t)(i + D) * 64);
         f32x4_v cb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, B01, f32x4_v{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
         cb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a_bias, B23, cb, 0, 0, 0);
         f32x4_v dl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A0, B01, cb, 0, 0, 0);
@@ -510,7 +514,32 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
         return true;
     }
     const int ng = decode_groups(w.n, w.k);
-    if (ng == 0) return false;
+    if (ng == 0) {
+        // no even slicing (K = 17408: 136 groups): the streaming kernel with 8 slices of floor / ceil (G / 8) groups,
+        // each longer than the load window. Measured N = 5120, K = 17408: the VALU GEMV's uneven slices 41.5 us
+        const int G = w.k / 128, S = kMaxWaves, ngmax = (G + S - 1) / S;
+        if (G / S <= 3 || ngmax > 32) return false;
+        // quarter blocks for the tiles past the last whole round of CUs (slices of up to 20 groups: the quarter path
+        // keeps all of a slice's wave-loads in flight)
+        const int tiles = w.n / 16, ncu = qe_num_cus();
+        const int rem = tiles > ncu && ngmax <= 20 ? tiles % ncu : 0, tq = tiles - rem;
+        const dim3 grid((unsigned)(tq + 4 * rem)), block(64 * S);
+#define QE_GEMV1U(NG_, QT_, SDT_)                                                                             \
+    gemv1s_kernel<NG_, 3, SDT_, QT_, false><<<grid, block, (size_t)S * st_wbytes<NG_>() + (size_t)S * 64, st>>>( \
+        w.q, w.s, w.n, w.k, x, y, out, tq)
+        if (w.sdt == kScaleF16) {
+            if (ngmax > 20) QE_GEMV1U(32, false, kScaleF16);
+            else if (rem) QE_GEMV1U(20, true, kScaleF16);
+            else QE_GEMV1U(20, false, kScaleF16);
+        } else {
+            if (ngmax > 20) QE_GEMV1U(32, false, kScaleBF16);
+            else if (rem) QE_GEMV1U(20, true, kScaleBF16);
+            else QE_GEMV1U(20, false, kScaleBF16);
+        }
+#undef QE_GEMV1U
+        HIP_CHECK(hipGetLastError());
+        return true;
+    }
     const int S = w.k / 128 / ng;
     const dim3 grid((unsigned)(w.n / 16)), block(64 * S);
     // all of a slice's records in flight for slices of up to 5 groups, else a window of 3

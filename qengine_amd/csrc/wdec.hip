@@ -62,7 +62,7 @@ __global__ void __launch_bounds__(NTH, 2) wdec_kernel(const uint4* __restrict__ 
     const int slab = tail < 0 ? b : nmain + tail / P, KTb = tail < 0 ? K / BK : K / BK / P;
     const int KTw = KTb / KP, kt0 = (tail < 0 ? 0 : (tail % P) * KTb) + kp * KTw, G = K >> 7;
     const int tile0 = slab * 4;  // the block's four 16-row tiles
-    const int mr = lane & 31, kh = lane >> 5, g = mr & 7;
+    const int mr = lane & 31, kh = lane >> 5;
     auto buf_at = [&](int b) { return (b * NW + wave) * kBuf; };  // byte offset of this wave's buffer b
 
     // DMA sources. Activations: piece r (rows 8 r .. 8 r + 7), lane i lands at slot i of the piece, so it loads the
@@ -329,9 +329,12 @@ void wdec_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     int nmain = nslabs, P = 1, rem = 0;
     float* tpart = nullptr;
     uint32_t* tctr = nullptr;
-    if (nslabs > ncu && nslabs % ncu != 0) {
-        rem = nslabs % ncu;
-        for (int p : {5, 4, 8, 10, 2})
+    // K parts for the slabs past the last whole round of CUs, and for every slab where the slabs fill at most half of
+    // the CUs (N = 5120: 80 slabs; the most parts that fit the CUs)
+    const bool few = 2 * nslabs <= ncu;
+    if ((nslabs > ncu && nslabs % ncu != 0) || few) {
+        rem = few ? nslabs : nslabs % ncu;
+        for (int p : few ? std::initializer_list<int>{10, 8, 5, 4, 3, 2} : std::initializer_list<int>{5, 4, 8, 10, 2})
             if (rem * p <= ncu && KT % (p * KP) == 0 && (KT / (p * KP)) % 2 == 0) {
                 // one size for every shape (at most ncu tail blocks of two token blocks), so a stream's first call
                 // sizes it for all later ones, graph captures included

@@ -345,6 +345,33 @@ def test_gemv_m1_quarter_tiles(dev, n, k, sdt):
     assert_glu_close(out_f32(a), glu_act(matmul_f64(xh, exact_w4(qg, sg, n, k, sdt))), 1e-4)
 
 
+# m = 1 where K / 128 has no even slicing of the streaming kernel: 8 slices of floor / ceil (K / 1024) groups.
+# K = 17408 (136 groups, 17 per slice) on 320 tiles (quarter blocks for the 64 past one round) and on 128 tiles;
+# K = 13824 (108 groups: slices of 13 and 14); K = 28672 (224 groups: 28 per slice, the 32-group instance)
+@pytest.mark.parametrize("n,k,sdt", [(5120, 17408, 1), (2048, 17408, 0), (4096, 13824, 1), (1024, 28672, 0)])
+def test_gemv_m1_uneven_slices(dev, n, k, sdt):
+    """every row within 1e-4 * rms of the exact product, the bf16 output its RN, GLU outputs silu(gate) up of the same
+    sums, repeated calls bit-identical"""
+    w, q, s = setup_w4(n, k, sdt, seed=n + k + sdt + 7)
+    xh = synth.x_host(1, k, seed=k + 9)
+    x = synth.to_dev(xh)
+    y = ops.gemv_w4(w, x)
+    y2 = ops.gemv_w4(w, x)
+    yb = ops.gemv_w4(w, x, out_bf16=True)
+    torch.cuda.synchronize()
+    ex = matmul_f64(xh, exact_w4(q, s, n, k, sdt))
+    r = err_ratio(y.cpu().numpy(), ex)
+    print(f"m1 uneven n={n} k={k}: max|y - exact| / rms = {r:.2e}", flush=True)
+    assert r <= 1e-4
+    assert torch.equal(y.view(torch.int32), y2.view(torch.int32))
+    assert_rn_of(yb, y.cpu().numpy(), f"uneven n={n}")
+    del w, ex
+    wg, qg, sg = setup_w4(n, k, sdt, seed=n + k + sdt + 8, glu=True)
+    a = ops.gemv_w4(wg, x)
+    torch.cuda.synchronize()
+    assert_glu_close(out_f32(a), glu_act(matmul_f64(xh, exact_w4(qg, sg, n, k, sdt))), 1e-4)
+
+
 @pytest.mark.parametrize("per_channel", [True, False])
 @pytest.mark.parametrize("n,k", [(64, 256), (8192, 2048), (4096, 5120)])
 def test_gemv_w8_parity(dev, per_channel, n, k):
