@@ -340,7 +340,7 @@ __device__ __forceinline__ void gemv1s_quarter(const uint4* __restrict__ q, cons
 // is a separate instance, whose code is then exactly the whole-tile kernel's (the branch alone, taken by no block,
 // cost up to 5 % on some shapes)
 template <int NG, int D, int SDT, bool QT, bool EXACT = true>
-__global__ void __launch_bounds__(64 * kMaxWaves) __attribute__((amdgpu_waves_per_eu(7)))
+__global__ void __launch_bounds__(64 * (EXACT ? kMaxWaves : 2 * kMaxWaves)) __attribute__((amdgpu_waves_per_eu(7)))
 gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N, int K,
               const uint16_t* __restrict__ x, void* __restrict__ y, int out, int tq) {
     static_assert(NG * 32 <= 1024 && D >= 1 && D <= 4 && D < NG, "gemv1s slice");
@@ -399,7 +399,9 @@ gemv1s_kernel(const uint4* __restrict__ q, const uint16_t* __restrict__ s, int N
     f32x4_v acc_lo = {0.f, 0.f, 0.f, 0.f}, acc_hi = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < NG; i++) {
-        if (!EXACT && i >= ng) break;
+        // the first D groups unconditionally (ng > D): with a branch before group 0 the compiler sank the D record
+        // loads below vm_wait<D> into it, and the wait then no longer covered the activation and scale DMAs
+        if (!EXACT && i >= D && i >= ng) break;
         const uint32_t* b = bb + i * bstep;
         const u32x4_v b01 = {b[0], b[4], b[8], b[12]}, b23 = {b[16], b[20], b[24], b[28]};
         const bf16x8_v B01 = __builtin_bit_cast(bf16x8_v, b01), B23 = __builtin_bit_cast(bf16x8_v, b23);
@@ -516,26 +518,31 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
     const int ng = decode_groups(w.n, w.k);
     if (ng == 0) {
         // no even slicing (K = 17408: 136 groups): the streaming kernel with 8 slices of floor / ceil (G / 8) groups,
-        // each longer than the load window. Measured N = 5120, K = 17408: the VALU GEMV's uneven slices 41.5 us
-        const int G = w.k / 128, S = kMaxWaves, ngmax = (G + S - 1) / S;
+        // each longer than the load window, or 16 where 8 leave fewer than 16 waves per CU (few tiles, long K: one
+        // 8-wave block per CU keeps too few bytes in flight). Measured N = 5120, K = 17408: the VALU GEMV's uneven
+        // slices 41.5 us
+        const int G = w.k / 128, tiles = w.n / 16, ncu = qe_num_cus();
+        const int S = (long)tiles * kMaxWaves < 16L * ncu && G / (2 * kMaxWaves) > 3 ? 2 * kMaxWaves : kMaxWaves;
+        const int ngmax = (G + S - 1) / S;
         if (G / S <= 3 || ngmax > 32) return false;
         // quarter blocks for the tiles past the last whole round of CUs (slices of up to 20 groups: the quarter path
         // keeps all of a slice's wave-loads in flight)
-        const int tiles = w.n / 16, ncu = qe_num_cus();
         const int rem = tiles > ncu && ngmax <= 20 ? tiles % ncu : 0, tq = tiles - rem;
         const dim3 grid((unsigned)(tq + 4 * rem)), block(64 * S);
 #define QE_GEMV1U(NG_, QT_, SDT_)                                                                             \
     gemv1s_kernel<NG_, 3, SDT_, QT_, false><<<grid, block, (size_t)S * st_wbytes<NG_>() + (size_t)S * 64, st>>>( \
         w.q, w.s, w.n, w.k, x, y, out, tq)
-        if (w.sdt == kScaleF16) {
-            if (ngmax > 20) QE_GEMV1U(32, false, kScaleF16);
-            else if (rem) QE_GEMV1U(20, true, kScaleF16);
-            else QE_GEMV1U(20, false, kScaleF16);
-        } else {
-            if (ngmax > 20) QE_GEMV1U(32, false, kScaleBF16);
-            else if (rem) QE_GEMV1U(20, true, kScaleBF16);
-            else QE_GEMV1U(20, false, kScaleBF16);
-        }
+#define QE_GEMV1U_S(SDT_)                                  \
+    do {                                                   \
+        if (ngmax > 20) QE_GEMV1U(32, false, SDT_);        \
+        else if (ngmax > 8 && rem) QE_GEMV1U(20, true, SDT_); \
+        else if (ngmax > 8) QE_GEMV1U(20, false, SDT_);    \
+        else if (rem) QE_GEMV1U(8, true, SDT_);            \
+        else QE_GEMV1U(8, false, SDT_);                    \
+    } while (0)
+        if (w.sdt == kScaleF16) QE_GEMV1U_S(kScaleF16);
+        else QE_GEMV1U_S(kScaleBF16);
+#undef QE_GEMV1U_S
 #undef QE_GEMV1U
         HIP_CHECK(hipGetLastError());
         return true;
