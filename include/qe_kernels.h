@@ -139,8 +139,10 @@ void qe_gemv_workspace_init(void);
 void qe_repack_w4(const int32_t* q, const uint16_t* s, int n, int k, void* dq, void* ds);
 
 /* y[m][n] (fp32, stride n) = x[m][k] (bf16, stride k) . W^T; any m (1..16 rows: the decode GEMV; 17..64: the
- * one-pass decode GEMM where the shape fits it, else the GEMV in 16-row launches, which batch_invariant always
- * takes; the prefill GEMM above, as qe_matmul_w4_ex). Replaces reference src/capi.cpp:47 (gemv_w4, gemv.cu:1585). */
+ * one-pass decode GEMM where the shape fits it and it is the faster choice (N >= 64 x the CU count, K without an even
+ * slicing of the skinny kernel, more than 48 rows on matrices of >= ~26 M weights), else the skinny kernel's 32- and
+ * 16-row launches, which batch_invariant always takes; the prefill GEMM above, as qe_matmul_w4_ex).
+ * Replaces reference src/capi.cpp:47 (gemv_w4, gemv.cu:1585). */
 void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m);
 
 /* as qe_gemv_w4; glu != 0: y is the bf16 activation [m][n/2] = bf16(silu(gate) * up).
@@ -148,8 +150,8 @@ void qe_gemv_w4(const void* q, const void* s, int n, int k, const uint16_t* x, f
 void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);
 
 /* skinny GEMM, bit-identical to qe_gemv_w4g for every row count (it is qe_gemv_w4g's decode dispatch); m = 1..32
- * (the reference's skinny_w4 range, skinny.cu:572): 17..32 rows run as one launch (the one-pass kernel, or with
- * batch_invariant the wide skinny kernel), which needs 16-byte aligned rows and an even K slicing. Returns 0 (nothing
+ * (the reference's skinny_w4 range, skinny.cu:572): 17..32 rows run as one launch (the one-pass kernel where the
+ * dispatch picks it, else the wide skinny kernel), which needs 16-byte aligned rows and an even K slicing. Returns 0 (nothing
  * written) when the shape is unsupported, 1 when it ran. Replaces reference src/capi.cpp:79-83 (skinny_w4,
  * skinny.cu:572-604). */
 int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu);

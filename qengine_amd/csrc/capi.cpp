@@ -154,14 +154,14 @@ void qe_gemv_w4g(const void* q, const void* s, int n, int k, const uint16_t* x, 
 
 // the reference's skinny_w4 takes 1..32 rows (src/kernels/skinny.cu:572) and equals its GEMV bit for bit; here it is
 // the decode dispatch of qe_gemv_w4g itself (matmul_w4: 1..16 rows the decode GEMV / skinny kernel, 17..32 the
-// one-pass kernel, or with batch_invariant the 32-row skinny launch), so the bits are equal by construction. 17..32
+// one-pass kernel where the dispatch picks it, else the 32-row skinny launch), so the bits are equal by construction. 17..32
 // rows that neither of those one-launch kernels takes (x not 16-byte aligned, K slicing) return 0: unsupported, the
 // caller falls back to qe_gemv_w4 as the reference's callers do.
 int qe_skinny_w4(const void* q, const void* s, int n, int k, const uint16_t* x, float* y, int m, int glu) {
     if (m < 1 || m > kWideRows || n <= 0 || k <= 0 || n % 16 != 0 || k % 128 != 0 || k % 8 != 0) return 0;
     const W4 w = mk_w4(q, s, n, k, glu != 0, kScaleBF16);
     if (m > kMaxGemvRows) {
-        const bool onepass = !qe_config().batch_invariant && wdec_w4_fits(w, x, k, m);
+        const bool onepass = !qe_config().batch_invariant && wdec_w4_pick(w, x, k, m);
         if (!onepass && !skinny_w4_wide_fits(w, x, k)) return 0;
     }
     gemv_workspace_init();

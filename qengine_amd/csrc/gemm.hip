@@ -706,9 +706,9 @@ void matmul_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m,
         gemm_w4(w, x, ldx, y, ldy, m, out_bf16, st);
         return;
     }
-    // 17..64 rows: one pass over the weights (wdec.hip) where the shape fits it, unless every row must keep the bits
-    // it has alone (batch_invariant)
-    if (m > kMaxGemvRows && !qe_config().batch_invariant && wdec_w4_fits(w, x, ldx, m)) {
+    // 17..64 rows: one pass over the weights (wdec.hip) where the shape fits it and it is the faster choice, unless
+    // every row must keep the bits it has alone (batch_invariant)
+    if (m > kMaxGemvRows && !qe_config().batch_invariant && wdec_w4_pick(w, x, ldx, m)) {
         wdec_w4(w, x, ldx, y, ldy, m, out_bf16, st);
         return;
     }

@@ -58,6 +58,8 @@ bool skinny_w4_wide_fits(const W4& w, const uint16_t* x, int ldx);
 // the fp32 sums) on the 32 x 32 matrix cores, K split over the waves of a block, fixed-order sums; n % 64 == 0, x
 // 16-byte aligned, ldx % 8 == 0 and the K steps even per wave (wdec_w4_fits)
 bool wdec_w4_fits(const W4& w, const uint16_t* x, int ldx, int m);
+// the dispatch's choice for 17..64 rows outside batch_invariant: fits, and faster than the skinny kernel's launches
+bool wdec_w4_pick(const W4& w, const uint16_t* x, int ldx, int m);
 void wdec_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, bool out_bf16, hipStream_t st);
 // the same kernel on W8 / Q8 records (GLU for Q8): m = 1..16, x 16-byte aligned, ldx % 8 == 0
 void skinny_w8_mfma(const W8& w, const uint16_t* x, int ldx, void* y, int ldy, int m, int out, hipStream_t st);

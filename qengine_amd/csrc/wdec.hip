@@ -306,11 +306,45 @@ int token_blocks(int m) { return m > 32 ? 2 : 1; }
 
 }  // namespace qe_wdec
 
+namespace qe_wdec {
+// K parts per tail slab (1: none): for the slabs past the last whole round of CUs, and for every slab where the slabs
+// fill at most half of the CUs (N = 5120: 80 slabs; then the most parts that fit the CUs), the first P of the list with
+// the tail blocks within one round and an even number of K steps per wave
+int tail_parts(int nslabs, int KT, int KP, int ncu) {
+    const bool few = 2 * nslabs <= ncu;
+    if (!few && (nslabs <= ncu || nslabs % ncu == 0)) return 1;
+    const int rem = few ? nslabs : nslabs % ncu;
+    for (int p : few ? std::initializer_list<int>{10, 8, 5, 4, 3, 2} : std::initializer_list<int>{5, 4, 8, 10, 2})
+        if (rem * p <= ncu && KT % (p * KP) == 0 && (KT / (p * KP)) % 2 == 0) return p;
+    return 1;
+}
+}  // namespace qe_wdec
+
 bool wdec_w4_fits(const W4& w, const uint16_t* x, int ldx, int m) {
     using namespace qe_wdec;
     if (m < 1 || m > 64 || w.n % 64 != 0 || w.k % BK != 0 || ((uintptr_t)x & 15) != 0 || ldx % 8 != 0) return false;
     const int KP = NW / token_blocks(m), KT = w.k / BK;
     return KT % KP == 0 && (KT / KP) % 2 == 0;
+}
+
+namespace qe_gemv {
+int decode_groups(int n, int k);
+}
+
+// Where the one-pass kernel beats the skinny kernel's 32-row launches (measured in one process, bf16 out, us one-pass
+// / skinny): one round of slabs or more (N = 17408, K = 5120, m = 32: 20.7 / 28.9), K without an even skinny slicing
+// (the skinny kernel's uneven slices; N = 3072, K = 9216, m = 32: 14.5 / 20.4), and more than 48 rows from ~26 M
+// weights (N = K = 8192, m = 64: 27.6 / 30.2; N = K = 5120: 20.3 / 21.5). Small matrices keep the skinny launches:
+// N = K = 4096, m = 32: 11.8 / 7.8; N = K = 2048: 9.4 / 5.0; N = 6144, K = 4096, m = 64: 18.9 / 18.2.
+bool wdec_w4_pick(const W4& w, const uint16_t* x, int ldx, int m) {
+    using namespace qe_wdec;
+    if (!wdec_w4_fits(w, x, ldx, m)) return false;
+    const int nslabs = w.n / 64, ncu = qe_num_cus();
+    // slabs filling at most half the CUs only with K parts (N = 4096, K = 11008, m = 48: 64 slabs, no part count fits
+    // 172 steps: 48.4 us against 35.2)
+    if (2 * nslabs <= ncu && tail_parts(nslabs, w.k / BK, NW / token_blocks(m), ncu) == 1) return false;
+    if (nslabs >= ncu || qe_gemv::decode_groups(w.n, w.k) == 0) return true;
+    return m > 48 && (long)w.n * w.k >= (26L << 20);
 }
 
 // Slabs past the last whole round of CUs (N / 64 = 272 on 256 CUs: 16) would give 16 CUs two slabs; they run as P
@@ -329,24 +363,18 @@ void wdec_w4(const W4& w, const uint16_t* x, int ldx, void* y, int ldy, int m, b
     int nmain = nslabs, P = 1, rem = 0;
     float* tpart = nullptr;
     uint32_t* tctr = nullptr;
-    // K parts for the slabs past the last whole round of CUs, and for every slab where the slabs fill at most half of
-    // the CUs (N = 5120: 80 slabs; the most parts that fit the CUs)
-    const bool few = 2 * nslabs <= ncu;
-    if ((nslabs > ncu && nslabs % ncu != 0) || few) {
-        rem = few ? nslabs : nslabs % ncu;
-        for (int p : few ? std::initializer_list<int>{10, 8, 5, 4, 3, 2} : std::initializer_list<int>{5, 4, 8, 10, 2})
-            if (rem * p <= ncu && KT % (p * KP) == 0 && (KT / (p * KP)) % 2 == 0) {
-                // one size for every shape (at most ncu tail blocks of two token blocks), so a stream's first call
-                // sizes it for all later ones, graph captures included
-                char* ws = dec_tail_ws(st);
-                if (ws) {
-                    P = p;
-                    tctr = reinterpret_cast<uint32_t*>(ws);
-                    tpart = reinterpret_cast<float*>(ws + dec_tail_ctr_bytes());
-                    nmain = nslabs - rem;
-                }
-                break;
-            }
+    const int p = qe_wdec::tail_parts(nslabs, KT, KP, ncu);
+    if (p > 1) {
+        // one size for every shape (at most ncu tail blocks of two token blocks), so a stream's first call sizes it
+        // for all later ones, graph captures included
+        char* ws = dec_tail_ws(st);
+        if (ws) {
+            rem = 2 * nslabs <= ncu ? nslabs : nslabs % ncu;
+            P = p;
+            tctr = reinterpret_cast<uint32_t*>(ws);
+            tpart = reinterpret_cast<float*>(ws + dec_tail_ctr_bytes());
+            nmain = nslabs - rem;
+        }
     }
     const dim3 grid((unsigned)(nmain + (P > 1 ? rem * P : 0))), block(NTH);
 #define QE_WDEC(SDT_, TB_)                                                                                    \
