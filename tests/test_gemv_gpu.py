@@ -206,7 +206,9 @@ def test_reference_named_hooks(dev):
 MS_SKINNY = [1, 2, 5, 8, 9, 12, 15, 16, 17, 20, 24, 25, 31, 32]
 
 
-@pytest.mark.parametrize("n,k", [(5120, 5120), (2048, 1280)])
+# 17..32 rows: (5120, 5120) and (2048, 1280) take the skinny kernel's 32-row launch, (16384, 2048) (one round of
+# 64-row slabs) the one-pass kernel
+@pytest.mark.parametrize("n,k", [(5120, 5120), (2048, 1280), (16384, 2048)])
 def test_skinny_hook_bit_identical_to_gemv_w4g(dev, n, k):
     """the reference's skinny test (tests/test_skinny.py:16-41) bound to this library: qe_skinny_w4 returns 1 for
     every m in its MS list (1..32, the reference's skinny_w4 range, skinny.cu:572) and its outputs equal qe_gemv_w4g's
