@@ -417,6 +417,12 @@ def main():
             key = f"decode_m{m}_n17408" if mode == "matmul" else f"h16_m{m}_n17408"
             secondary[key] = {"gbs_kernel": round(r["gbs_kernel"], 1), "pct_hbm": round(100 * r["gbs_kernel"] / HBM_PEAK_GBS, 1),
                               "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2), "working_set": r["working_set"]}
+        # decode of C2's second matrix (K = 17408: 136 groups, no even K slicing)
+        for (m, mode) in [(1, "w4"), (32, "matmul")]:
+            r = bench_gemv(args, m=m, n=5120, k=17408, steps=200, warmup=20, mode=mode)
+            secondary[f"decode_m{m}_n5120_k17408"] = {
+                "gbs_kernel": round(r["gbs_kernel"], 1), "pct_hbm": round(100 * r["gbs_kernel"] / HBM_PEAK_GBS, 1),
+                "us_kernel": round(r["kernel_ms_mean"] * 1e3, 2), "working_set": r["working_set"]}
         secondary["prefill_k5120_n17408"] = bench_gemm(8192, 17408, 5120)
         secondary["prefill_k17408_n5120"] = bench_gemm(8192, 5120, 17408)
         secondary["prefill_h16_k5120_n17408"] = bench_gemm(8192, 17408, 5120, h16=True)
