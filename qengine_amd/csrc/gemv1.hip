@@ -518,11 +518,15 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
     const int ng = decode_groups(w.n, w.k);
     if (ng == 0) {
         // no even slicing (K = 17408: 136 groups): the streaming kernel with 8 slices of floor / ceil (G / 8) groups,
-        // each longer than the load window, or 16 where 8 leave fewer than 16 waves per CU (few tiles, long K: one
-        // 8-wave block per CU keeps too few bytes in flight). Measured N = 5120, K = 17408: the VALU GEMV's uneven
-        // slices 41.5 us
+        // each longer than the load window, or 16 where the grid holds at most one tile per CU (long K: one 8-wave
+        // block per CU keeps too few bytes in flight) or where 8 slices would be too long for quarter blocks. Past one
+        // tile per CU, 16 slices (100 KB of LDS per block) leave one block per CU, and the quarter blocks wait for the
+        // whole tiles; with 8 (51 KB) they run beside them. Measured N = 5120, K = 17408: the VALU GEMV's uneven
+        // slices 41.5 us; 16 slices 13.25 us, 8 slices 10.66 us (K = 13824: 9.94 -> 8.84 us); at N = 2048 .. 4096 16
+        // slices stay ahead (7.5 vs 8.4 us)
         const int G = w.k / 128, tiles = w.n / 16, ncu = qe_num_cus();
-        const int S = (long)tiles * kMaxWaves < 16L * ncu && G / (2 * kMaxWaves) > 3 ? 2 * kMaxWaves : kMaxWaves;
+        const bool s16 = tiles <= ncu || (G + kMaxWaves - 1) / kMaxWaves > 20;
+        const int S = s16 && G / (2 * kMaxWaves) > 3 ? 2 * kMaxWaves : kMaxWaves;
         const int ngmax = (G + S - 1) / S;
         if (G / S <= 3 || ngmax > 32) return false;
         // quarter blocks for the tiles past the last whole round of CUs (slices of up to 20 groups: the quarter path
