@@ -19,16 +19,27 @@ from test_gemv_gpu import assert_bf16_close, assert_gate, assert_rn_of, out_f32
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("T,E,topk", [(1, 512, 10), (16, 512, 10), (300, 64, 6), (4096, 512, 10)])
+@pytest.mark.parametrize("T,E,topk", [(1, 512, 10), (16, 512, 10), (300, 64, 6), (4096, 512, 10), (3, 1000, 8), (2, 200, 4)])
 def test_route_and_segment_bit_exact(dev, T, E, topk):
     lg = synth.logits_host(T, E, seed=T + E)
-    lg[0, 3] = lg[0, 7] = lg[0].max() + 1.0  # a tie at the top: lower index first
+    m0 = lg[0].max()
+    lg[0, 3] = lg[0, 7] = m0 + 1.0  # a tie at the top between lanes: lower index first
+    if E > 69:
+        lg[0, 69] = lg[0, 5] = m0 + 0.5  # a tie inside one lane (experts 5 and 69 share lane 5)
+    if T > 1:
+        lg[1] = -np.abs(lg[1]) - 1.0
+        lg[1, E - 1] = 0.0
+        lg[1, 10] = -0.0  # -0 and +0 compare equal: the lower expert first
     sel_ref, w_ref = oracle.moe_route(lg, topk)
     sel, w = ops.moe_route(torch.from_numpy(lg).to(dev), topk)
     torch.cuda.synchronize()
     assert np.array_equal(sel.cpu().numpy(), sel_ref)
     assert np.allclose(w.cpu().numpy(), w_ref, rtol=2e-6, atol=1e-7)
     assert sel_ref[0, 0] == 3 and sel_ref[0, 1] == 7
+    if E > 69:
+        assert sel_ref[0, 2] == 5 and sel_ref[0, 3] == 69
+    if T > 1:
+        assert sel_ref[1, 0] == 10 and sel_ref[1, 1] == E - 1
     cnt, off, lst, inv = oracle.moe_segment(sel_ref, E)
     for chunk in (2, 64):
         seg = ops.moe_segment(sel, w, E, chunk)
