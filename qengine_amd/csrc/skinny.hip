@@ -32,14 +32,18 @@ using namespace qe_gemv;
 
 // Tiles per wave RT: the weight tiles of RT consecutive 16-row tiles share one wave's staged activations and B
 // operand reads (the activation traffic per tile halves at RT = 2). Even slices can take RT = 2 (the host picks it
-// in launch()); uneven slices (NG = 0) take RT = 1. Weight groups in flight per wave D and the occupancy hint
-// WPE, measured on the BASELINE shapes (K = 5120, 5-group slices; N = 5120 and 17408):
+// in launch()), uneven slices (NG = 0) at MT = 2..8 (16 rows at RT = 2 spill: N = 5120, K = 17408 29.8 -> 55.9 us).
+// Measured on uneven slices, RT = 1 -> 2: N = 5120, K = 17408, m = 2 / 4 / 8 15.7 / 16.3 / 21.6 -> 14.8 / 14.8 / 16.0
+// us; K = 13824 13.0 / 13.7 / 17.6 -> 12.2 / 12.2 / 13.1 us; N = 8192, K = 17408, m = 8 24.5 -> 17.5 us. Weight
+// groups in flight per wave D and the occupancy hint WPE, measured on the BASELINE shapes (K = 5120, 5-group slices;
+// N = 5120 and 17408):
 //   RT = 2: D = 2 on slices of <= 5 groups (WPE 4: <= 128 VGPRs), else D = 3 (MT = 8: 2)
 //   RT = 1: D = 2 for MT <= 8 (MT = 2 / 4: 5 / 2.5 % faster than 3, 4 and 5 slower still), else 3; WPE 6 at
 //   MT <= 4 on even slices of <= 5 groups
 template <int MT, int NG, int FMT>
 constexpr int skinny_rt() {
-    return NG == 0 || FMT != kFmtW4 ? 1 : 2;
+    if (FMT != kFmtW4) return 1;
+    return NG > 0 || (MT >= 2 && MT <= 8) ? 2 : 1;
 }
 template <int MT, int NG, int RT, int FMT>
 constexpr int skinny_d() {

@@ -102,7 +102,7 @@ def test_xh_pack_bit_exact(dev):
     assert not len(bad), [(int(r), int(c), hex(got[r, c]), hex(want[r, c])) for r, c in bad[:8]]
 
 
-@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048)])
+@pytest.mark.parametrize("n,k", [(64, 256), (1024, 2048), (5120, 13824)])
 def test_gemv_w4h_exact_on_integer_inputs(dev, n, k):
     rng = np.random.default_rng(n)
     q, _ = synth.w4_host(n, k, seed=n + 1, sdt=0)
@@ -110,7 +110,7 @@ def test_gemv_w4h_exact_on_integer_inputs(dev, n, k):
     w = ops.repack_w4(synth.to_dev(q), synth.to_dev(s, torch.bfloat16))
     x = synth.np_bf16((rng.integers(-3, 4, (20, k)) * 16).astype(np.float32))
     want = exact(x, oracle.unpack_w4(q, n, k), oracle.bf16_to_f32(s)).astype(np.float32)
-    for m in (1, 5, 16, 20):
+    for m in (1, 2, 5, 16, 20):
         y, _, _ = ops.gemv_w4h(w, synth.to_dev(x[:m]))
         torch.cuda.synchronize()
         assert np.array_equal(y.cpu().numpy(), want[:m]), m
