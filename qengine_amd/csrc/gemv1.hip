@@ -523,15 +523,18 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
         // tile per CU, 16 slices (100 KB of LDS per block) leave one block per CU, and the quarter blocks wait for the
         // whole tiles; with 8 (51 KB) they run beside them. Measured N = 5120, K = 17408: the VALU GEMV's uneven
         // slices 41.5 us; 16 slices 13.25 us, 8 slices 10.66 us (K = 13824: 9.94 -> 8.84 us); at N = 2048 .. 4096 16
-        // slices stay ahead (7.5 vs 8.4 us)
+        // slices stay ahead (7.5 vs 8.4 us). Where the tiles fill at most half the CUs, every tile runs as four quarter
+        // blocks of 8 slices (16 where 8 would exceed 20 groups), so that every CU streams: N = 2048, K = 17408 7.50 ->
+        // 6.59 us, N = 1024 7.23 -> 4.61 us (at one tile per CU, N = 4096, quarters lose: 7.5 -> 9.8 us)
         const int G = w.k / 128, tiles = w.n / 16, ncu = qe_num_cus();
-        const bool s16 = tiles <= ncu || (G + kMaxWaves - 1) / kMaxWaves > 20;
+        const bool aq = 2 * tiles <= ncu && (G + 2 * kMaxWaves - 1) / (2 * kMaxWaves) <= 20;
+        const bool s16 = (G + kMaxWaves - 1) / kMaxWaves > 20 || (!aq && tiles <= ncu);
         const int S = s16 && G / (2 * kMaxWaves) > 3 ? 2 * kMaxWaves : kMaxWaves;
         const int ngmax = (G + S - 1) / S;
         if (G / S <= 3 || ngmax > 32) return false;
-        // quarter blocks for the tiles past the last whole round of CUs (slices of up to 20 groups: the quarter path
-        // keeps all of a slice's wave-loads in flight)
-        const int rem = tiles > ncu && ngmax <= 20 ? tiles % ncu : 0, tq = tiles - rem;
+        // quarter blocks for the tiles past the last whole round of CUs, or for all of them (slices of up to 20
+        // groups: the quarter path keeps all of a slice's wave-loads in flight)
+        const int rem = aq ? tiles : tiles > ncu && ngmax <= 20 ? tiles % ncu : 0, tq = tiles - rem;
         const dim3 grid((unsigned)(tq + 4 * rem)), block(64 * S);
 #define QE_GEMV1U(NG_, QT_, SDT_)                                                                             \
     gemv1s_kernel<NG_, 3, SDT_, QT_, false><<<grid, block, (size_t)S * st_wbytes<NG_>() + (size_t)S * 64, st>>>( \
