@@ -481,9 +481,11 @@ int stream_groups(int n, int k) {
 }
 }  // namespace qe_gemv1
 
-// m = 1 on the matrix cores (x 16-byte aligned): the streaming kernel where stream_groups finds a slicing, else
-// gemv1_kernel when K / 128 splits evenly into slices of 10, 8, 5, 4 or 2 groups; returns false otherwise (the caller
-// takes the VALU GEMV)
+// m = 1 on the matrix cores (x 16-byte aligned): the streaming kernel where stream_groups finds a slicing; its
+// run-time slices (8 or 16 per tile, quarter blocks past the last whole round of CUs or for every tile of a grid
+// filling at most half the CUs) where K / 128 has no even slicing or few tiles meet a long K; else gemv1_kernel when
+// K / 128 splits evenly into slices of 10, 8, 5, 4 or 2 groups; returns false otherwise (the caller takes the VALU
+// GEMV)
 bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) {
     using namespace qe_gemv1;
     if (((uintptr_t)x & 15) != 0) return false;
@@ -516,7 +518,10 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
         return true;
     }
     const int ng = decode_groups(w.n, w.k);
-    if (ng == 0) {
+    // even K too where the tiles fill at most half the CUs and K >= 6144: the quarter blocks below (N = 1024, K = 8192
+    // 4.24 -> 3.51 us, N = 1536, K = 6144 4.33 -> 3.98 us; at K = 4096 / 5120 the whole-tile kernel stays ahead)
+    const int G0 = w.k / 128;
+    if (ng == 0 || (2 * (w.n / 16) <= qe_num_cus() && G0 >= 48 && (G0 + 2 * kMaxWaves - 1) / (2 * kMaxWaves) <= 20)) {
         // no even slicing (K = 17408: 136 groups): the streaming kernel with 8 slices of floor / ceil (G / 8) groups,
         // each longer than the load window, or 16 where the grid holds at most one tile per CU (long K: one 8-wave
         // block per CU keeps too few bytes in flight) or where 8 slices would be too long for quarter blocks. Past one

@@ -350,7 +350,7 @@ def test_gemv_m1_quarter_tiles(dev, n, k, sdt):
 # m = 1 where K / 128 has no even slicing of the streaming kernel: 8 slices of floor / ceil (K / 1024) groups.
 # K = 17408 (136 groups, 17 per slice) on 320 tiles (quarter blocks for the 64 past one round) and on 128 tiles;
 # K = 13824 (108 groups: slices of 13 and 14); K = 28672 (224 groups: 28 per slice, the 32-group instance)
-@pytest.mark.parametrize("n,k,sdt", [(5120, 17408, 1), (2048, 17408, 0), (4096, 13824, 1), (1024, 28672, 0), (5120, 13824, 0)])
+@pytest.mark.parametrize("n,k,sdt", [(5120, 17408, 1), (2048, 17408, 0), (4096, 13824, 1), (1024, 28672, 0), (5120, 13824, 0), (1024, 8192, 1), (1536, 6144, 0)])
 def test_gemv_m1_uneven_slices(dev, n, k, sdt):
     """every row within 1e-4 * rms of the exact product, the bf16 output its RN, GLU outputs silu(gate) up of the same
     sums, repeated calls bit-identical"""
