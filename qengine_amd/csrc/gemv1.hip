@@ -519,7 +519,7 @@ bool gemv1_w4(const W4& w, const uint16_t* x, void* y, int out, hipStream_t st) 
     }
     const int ng = decode_groups(w.n, w.k);
     // even K too where the tiles fill at most half the CUs and K >= 6144: the quarter blocks below (N = 1024, K = 8192
-    // 4.24 -> 3.51 us, N = 1536, K = 6144 4.33 -> 3.98 us; at K = 4096 / 5120 the whole-tile kernel stays ahead)
+    // 4.24 -> 3.54 us, N = 1536, K = 6144 4.33 -> 3.96 us; at K = 4096 / 5120 the whole-tile kernel stays ahead)
     const int G0 = w.k / 128;
     if (ng == 0 || (2 * (w.n / 16) <= qe_num_cus() && G0 >= 48 && (G0 + 2 * kMaxWaves - 1) / (2 * kMaxWaves) <= 20)) {
         // no even slicing (K = 17408: 136 groups): the streaming kernel with 8 slices of floor / ceil (G / 8) groups,
