@@ -56,8 +56,11 @@ Slicing gemv_slicing(int n, int k) {
     }
     if (best > 0) return {best, G / best};
     // uneven: up to 12 waves toward the target (skinny kernel, K = 17408, 136 groups: N = 5120 m = 2 / 8 16.2 / 24.5 ->
-    // 15.6 / 21.7 us at 12 slices instead of 9; N = 2048 12.8 -> 10.8 us at m = 2; 16 slices: mixed)
-    int S = std::max((G + kGenericNG - 1) / kGenericNG, std::min(s_target, std::min(G, 12)));
+    // 15.6 / 21.7 us at 12 slices instead of 9; N = 2048 12.8 -> 10.8 us at m = 2), 16 where the tiles fit one round
+    // of CUs (N = 2048, K = 17408, m = 1 (batch_invariant) / 2 / 4 / 8 / 16: 10.7 / 10.9 / 10.9 / 11.7 / 15.9 -> 9.7 /
+    // 9.8 / 9.8 / 11.6 / 16.0 us; N = 3072 and 4096 alike, m = 8 up to 5 % slower; the VALU GEMV 2-8 % faster)
+    const int cap = tiles <= qe_num_cus() ? 16 : 12;
+    int S = std::max((G + kGenericNG - 1) / kGenericNG, std::min(s_target, std::min(G, cap)));
     CHECK(S <= kMaxWavesGeneric, "gemv: k = %d above the supported 32768", k);
     return {0, S};
 }

@@ -131,7 +131,7 @@ def test_gemv_w4_parity(dev, n, k, sdt):
                 assert ex <= 1e-4, (m, ex)
 
 
-@pytest.mark.parametrize("n,k", [(256, 1280), (5120, 5120), (16384, 2048), (5120, 13824)])
+@pytest.mark.parametrize("n,k", [(256, 1280), (5120, 5120), (16384, 2048), (5120, 13824), (2048, 13824)])
 def test_gemv_w4_batch_equals_alone(dev, n, k):
     w, _, _ = setup_w4(n, k, 1, seed=7)
     x = synth.to_dev(synth.x_host(16, k, seed=8))
