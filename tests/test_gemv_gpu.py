@@ -473,7 +473,7 @@ def _unaligned_rows(xh, mode):
 
 
 @pytest.mark.parametrize("mode", ["offset", "stride"])
-@pytest.mark.parametrize("n,k", [(1024, 5120), (256, 1280)])
+@pytest.mark.parametrize("n,k", [(1024, 5120), (256, 1280), (5120, 13824)])
 def test_gemv_unaligned_activations(dev, mode, n, k):
     """activation rows that are only 4-byte aligned: m = 1 takes the VALU GEMV, m >= 2 the matrix-core kernel with
     4-dword activation loads, whose rows equal those of the aligned copy bit for bit; W4 and W8 against the oracle"""
