@@ -38,7 +38,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-secondary", action="store_true", help="only the headline GEMV")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--only", choices=["prefill", "w8", "moe", "skinny", "decode"], default=None,
+    ap.add_argument("--only", choices=["prefill", "w8", "moe", "skinny", "decode", "c2decode"], default=None,
                     help="run one secondary workload alone (profiling); prints its result")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MB",
                     help="time a plain device copy of MB megabytes x 20 (scale for FETCH_SIZE / WRITE_SIZE) and exit")
@@ -393,7 +393,12 @@ def main():
                "decode": lambda: {f"{mode}_m{m}": (lambda r: {"us": round(r["kernel_ms_mean"] * 1e3, 2),
                                                               "gbs": round(r["gbs_kernel"], 1)})(
                    bench_gemv(args, m=m, steps=200, warmup=20, mode=mode))
-                   for (m, mode) in [(1, "h16"), (16, "h16"), (32, "matmul"), (48, "matmul"), (64, "matmul")]}}
+                   for (m, mode) in [(1, "h16"), (16, "h16"), (32, "matmul"), (48, "matmul"), (64, "matmul")]},
+               # decode of C2's second matrix (N = 5120, K = 17408: no even K slicing)
+               "c2decode": lambda: {f"m{m}": (lambda r: {"us": round(r["kernel_ms_mean"] * 1e3, 2),
+                                                         "gbs": round(r["gbs_kernel"], 1)})(
+                   bench_gemv(args, m=m, n=5120, k=17408, steps=200, warmup=20, mode="w4" if m <= 16 else "matmul"))
+                   for m in (1, 2, 4, 8, 16, 32)}}
         print(json.dumps({args.only: fns[args.only]()}))
         return
 
