@@ -40,6 +40,8 @@ using namespace qe_gemv;
 //   RT = 2: D = 2 on slices of <= 5 groups (WPE 4: <= 128 VGPRs), else D = 3 (MT = 8: 2)
 //   RT = 1: D = 2 for MT <= 8 (MT = 2 / 4: 5 / 2.5 % faster than 3, 4 and 5 slower still), else 3; WPE 6 at
 //   MT <= 4 on even slices of <= 5 groups
+//   uneven slices: D = 2 at MT = 16 too (N = 5120, K = 13824 / 17408, m = 12: 22.7 / 27.0 -> 21.5 / 26.0 us; N = 8192,
+//   K = 17408, m = 16: 32.0 -> 30.5 us)
 template <int MT, int NG, int FMT>
 constexpr int skinny_rt() {
     if (FMT != kFmtW4) return 1;
@@ -47,7 +49,7 @@ constexpr int skinny_rt() {
 }
 template <int MT, int NG, int RT, int FMT>
 constexpr int skinny_d() {
-    constexpr int d = MT <= 8 || FMT != kFmtW4 || (RT == 2 && NG > 0 && NG <= 5) ? 2 : 3;
+    constexpr int d = MT <= 8 || FMT != kFmtW4 || NG == 0 || (RT == 2 && NG <= 5) ? 2 : 3;
     return NG > 0 && NG < d ? NG : d;
 }
 template <int MT, int NG, int RT, int FMT>
